@@ -1,0 +1,66 @@
+/*
+ * edsl_hip_device.h -- device-resident, asynchronous entry points.
+ *
+ * No counterpart in the reference: its GPU path copies every operand in and
+ * out and synchronises after each of its three launches
+ * (reference cpp/src/MLIRCompiler.cpp:367-454, cpp/src/MLIRExecutor.cpp:211-214).
+ * These entry points are for callers that keep tensors resident in HBM and own
+ * their streams: benchmark harnesses timing the kernel with stream events, and
+ * chains of dense layers whose intermediates never leave the device
+ * (reference tests/linalg/test_binary_op_execution.py:223-268 builds such chains).
+ *
+ * All pointers are device pointers; ld* are row strides in elements (inner
+ * stride 1). Work is enqueued on `stream` (a hipStream_t; NULL = null stream)
+ * and the call returns without waiting. Returns 0 on success, otherwise an
+ * error code with the message in edsl_hip_last_error(). Library-owned
+ * workspaces (small-M split-K partials, int8 operand copies) are shared by all
+ * calls on a device: launches that overlap in time on different streams of
+ * one device must not be issued.
+ */
+#ifndef EDSL_HIP_DEVICE_H
+#define EDSL_HIP_DEVICE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Epilogue codes: bit 0 = add bias[N]; bits 1-2 = activation. */
+#define EDSL_EPI_NONE 0
+#define EDSL_EPI_BIAS 1
+#define EDSL_EPI_RELU 2
+#define EDSL_EPI_BIAS_RELU 3
+#define EDSL_EPI_LEAKY 4
+#define EDSL_EPI_BIAS_LEAKY 5
+
+/* Y[M,N] = epilogue(X[M,K] @ W[K,N] (+ bias)), f32. */
+int edsl_hip_dense_f32_launch(const float *X, int64_t ldx, const float *W, int64_t ldw,
+                              const float *bias, float *Y, int64_t ldy, int64_t M,
+                              int64_t N, int64_t K, int epilogue, float alpha, void *stream);
+
+/* Y[M,N] = epilogue(X[M,K] @ W[K,N] (+ bias)), i32 wrapping arithmetic.
+ * Leaky epilogues are rejected (float-only in the reference). */
+int edsl_hip_dense_i32_launch(const int32_t *X, int64_t ldx, const int32_t *W, int64_t ldw,
+                              const int32_t *bias, int32_t *Y, int64_t ldy, int64_t M,
+                              int64_t N, int64_t K, int epilogue, void *stream);
+
+/* Description of the kernels the calling thread's last call launched
+ * (e.g. "gemv_f32 mb=1 ksplit=4 grid=512"); returns its length. */
+int edsl_hip_last_plan(char *buf, size_t len);
+
+/* Tuning overrides: force an f32 tile configuration (index into the table
+ * reported by edsl_hip_f32_config_name; -1 = automatic) and the small-M
+ * split-K factor (0 = automatic). Calls that cannot use the forced choice
+ * fall back to the automatic one. */
+void edsl_hip_set_f32_config(int cfg);
+void edsl_hip_set_gemv_ksplit(int ksplit);
+int edsl_hip_f32_config_count(void);
+int edsl_hip_f32_config_name(int cfg, char *buf, size_t len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EDSL_HIP_DEVICE_H */

@@ -1,0 +1,89 @@
+// Shared device-side definitions for the gfx950 dense-path kernels.
+//
+// Epilogue semantics follow the reference's linalg lowering of the dense layer:
+//   bias:  linalg.generic body `arith.addf` / `arith.addi`
+//          (reference cpp/src/builders/LinalgBuilder.cpp:301-339)
+//   relu:  `arith.maximumf(x, 0)` for f32 (LinalgBuilder.cpp:213-215) -- NaN
+//          propagates and max(-0, +0) = +0; for i32 the reference spells ReLU as
+//          tensor_map(v -> If(v > 0, v, 0)) (LinalgBuilder.cpp:141-178).
+//   leaky: max(x,0) + alpha*min(x,0) with arith.maximumf / arith.minimumf,
+//          mulf, addf (LinalgBuilder.cpp:216-225).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace edsl {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+// Epilogue code: bit 0 = bias present; bits 1-2 = activation.
+enum : int {
+  EPI_BIAS_BIT = 1,
+  ACT_NONE = 0,
+  ACT_RELU = 1,
+  ACT_LEAKY = 2,
+};
+constexpr int epi_code(bool bias, int act) { return (bias ? 1 : 0) | (act << 1); }
+constexpr bool epi_has_bias(int epi) { return (epi & 1) != 0; }
+constexpr int epi_act(int epi) { return (epi >> 1) & 3; }
+
+// arith.maximumf(x, +0.0): NaN in -> NaN out; -0 -> +0.
+__device__ __forceinline__ float maximumf_zero(float x) {
+  return (x > 0.0f || x != x) ? x : 0.0f;
+}
+// arith.minimumf(x, +0.0): NaN in -> NaN out; -0 -> -0; positive -> +0.
+__device__ __forceinline__ float minimumf_zero(float x) {
+  return (x < 0.0f || x != x || x == 0.0f) ? x : 0.0f;
+}
+
+template <int EPI>
+__device__ __forceinline__ float apply_epilogue_f32(float acc, float b, float alpha) {
+  float y = acc;
+  if constexpr (epi_has_bias(EPI)) y = __fadd_rn(y, b);
+  if constexpr (epi_act(EPI) == ACT_RELU) {
+    y = maximumf_zero(y);
+  } else if constexpr (epi_act(EPI) == ACT_LEAKY) {
+    // mulf then addf, each rounded (no contraction), as the reference emits them.
+    y = __fadd_rn(maximumf_zero(y), __fmul_rn(minimumf_zero(y), alpha));
+  }
+  return y;
+}
+
+template <int EPI>
+__device__ __forceinline__ int32_t apply_epilogue_i32(int32_t acc, int32_t b) {
+  // arith.addi wraps modulo 2^32.
+  int32_t y = acc;
+  if constexpr (epi_has_bias(EPI)) y = (int32_t)((uint32_t)y + (uint32_t)b);
+  if constexpr (epi_act(EPI) == ACT_RELU) y = y > 0 ? y : 0;
+  return y;
+}
+
+// Workgroup -> output tile mapping.
+//
+// The hardware hands workgroup w to XCD (w % 8). Each XCD has its own L2, so
+// consecutive *logical* tiles are given to the same XCD: logical id
+// L = (w % 8) * (T / 8) + w / 8 when the tile count T divides by 8. Logical ids
+// are then walked in groups of GROUP_M tile-rows, column-major inside a group,
+// so one XCD's tiles share a few A row-panels and B column-panels.
+__device__ __forceinline__ void tile_coords(int wg, int tiles_m, int tiles_n, int& tm,
+                                            int& tn) {
+  constexpr int kXcds = 8;
+  constexpr int kGroupM = 4;
+  const int total = tiles_m * tiles_n;
+  int L = wg;
+  if (total % kXcds == 0) L = (wg % kXcds) * (total / kXcds) + wg / kXcds;
+  const int span = kGroupM * tiles_n;
+  const int group = L / span;
+  const int first_m = group * kGroupM;
+  const int rows = min(tiles_m - first_m, kGroupM);
+  const int in_group = L - group * span;
+  tm = first_m + in_group % rows;
+  tn = in_group / rows;
+}
+
+}  // namespace edsl

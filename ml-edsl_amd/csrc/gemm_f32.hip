@@ -1,0 +1,295 @@
+// fp32 dense layer / matmul on gfx950 matrix cores.
+//
+// C[M,N] = epilogue(A[M,K] x B[K,N] (+ bias[N])), fp32 accumulate.
+//
+// This realises, as one kernel, the reference's fill + linalg.matmul + bias
+// generic + ReLU generic chain (reference cpp/src/builders/LinalgBuilder.cpp:106-139,
+// 180-239, 301-339), which the reference GPU lowering runs as three kernels
+// (reference cpp/src/MLIRLowering.cpp:495-518): the zero fill becomes the
+// register-zeroed accumulator, and bias + activation run on the accumulator
+// registers before the one store of C.
+//
+// Design (per workgroup, one BM x BN output tile):
+//  * K is walked in BK-deep steps; A and B tiles are staged in LDS, double
+//    buffered, with the next step's global loads (16-byte, coalesced) issued
+//    before the current step's MFMAs and written to the other LDS buffer after.
+//  * v_mfma_f32_32x32x2_f32: lane l supplies A[row l%32][k-slot l/32] and
+//    B[k-slot l/32][col l%32]. A lane reads 4 consecutive k of an A row with one
+//    ds_read_b128, and for each of those k one ds_read_b{32,64,128} of CP
+//    consecutive B columns. The two lane halves take k = 8j+s and 8j+4+s for
+//    MFMA step s, so the same k pairs A and B. Column phase c of a wave tile
+//    therefore holds output columns wn0 + CP*(l%32) + c, which gives each lane
+//    CP consecutive columns in the epilogue: one vector store per row.
+//  * A tiles are stored row-major in LDS with the 16-byte chunk index XOR-ed by
+//    a row hash, so the 16 lanes of a ds_read_b128 phase hit distinct banks.
+//  * Workgroups map to tiles XCD-aware (common.hpp: tile_coords).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace edsl {
+namespace {
+
+template <int KCH>
+__device__ __forceinline__ int a_swizzle(int row) {
+  // A row holds KCH 16-byte chunks; 8/KCH rows fill the 32 four-byte banks.
+  return (row / (8 / KCH)) % KCH;
+}
+
+template <int CP>
+__device__ __forceinline__ void load_b_frag(const float* p, float (&v)[CP]) {
+  if constexpr (CP == 4) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(p);
+    v[0] = t[0]; v[1] = t[1]; v[2] = t[2]; v[3] = t[3];
+  } else if constexpr (CP == 2) {
+    const f32x2 t = *reinterpret_cast<const f32x2*>(p);
+    v[0] = t[0]; v[1] = t[1];
+  } else {
+    v[0] = *p;
+  }
+}
+
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int EPI, bool GUARD>
+__global__ void __launch_bounds__(WAVES_M * WAVES_N * 64)
+gemm_f32_kernel(GemmF32Args args) {
+  constexpr int NT = WAVES_M * WAVES_N * 64;
+  constexpr int WM = BM / WAVES_M;
+  constexpr int WN = BN / WAVES_N;
+  constexpr int CP = WN / 32;
+  constexpr int RB = WM / 32;
+  constexpr int KCH = BK / 4;
+  static_assert(WM % 32 == 0, "wave tile rows must be a multiple of 32");
+  static_assert(WN == 32 * CP && (CP == 1 || CP == 2 || CP == 4), "wave tile cols");
+  static_assert(BK % 8 == 0 && KCH <= 8, "BK");
+  constexpr int A_F4 = BM * KCH;
+  constexpr int B_F4 = BK * BN / 4;
+  static_assert(A_F4 % NT == 0 && B_F4 % NT == 0, "tile loads must divide evenly");
+  constexpr int A_LD = A_F4 / NT;
+  constexpr int B_LD = B_F4 / NT;
+
+  __shared__ f32x4 sA[2][A_F4];
+  __shared__ float sB[2][BK * BN];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wave_m = wave / WAVES_N;
+  const int wave_n = wave % WAVES_N;
+  int tm, tn;
+  tile_coords(blockIdx.x, args.tiles_m, args.tiles_n, tm, tn);
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+  const int M = args.M, N = args.N, K = args.K;
+
+  f32x4 ra[A_LD];
+  f32x4 rb[B_LD];
+
+  auto load_global = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int idx = tid + i * NT;
+      const int r = idx / KCH;
+      const int q = idx % KCH;
+      const int gm = m0 + r;
+      const int gk = k0 + 4 * q;
+      if constexpr (!GUARD) {
+        ra[i] = *reinterpret_cast<const f32x4*>(args.A + (int64_t)gm * args.lda + gk);
+      } else {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = (gm < M && gk + e < K) ? args.A[(int64_t)gm * args.lda + gk + e] : 0.0f;
+        ra[i] = v;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int idx = tid + i * NT;
+      const int r = idx / (BN / 4);
+      const int c = 4 * (idx % (BN / 4));
+      const int gk = k0 + r;
+      const int gn = n0 + c;
+      if constexpr (!GUARD) {
+        rb[i] = *reinterpret_cast<const f32x4*>(args.B + (int64_t)gk * args.ldb + gn);
+      } else {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = (gk < K && gn + e < N) ? args.B[(int64_t)gk * args.ldb + gn + e] : 0.0f;
+        rb[i] = v;
+      }
+    }
+  };
+
+  auto store_lds = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int idx = tid + i * NT;
+      const int r = idx / KCH;
+      const int q = idx % KCH;
+      sA[buf][r * KCH + (q ^ a_swizzle<KCH>(r))] = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int idx = tid + i * NT;
+      const int r = idx / (BN / 4);
+      const int c = 4 * (idx % (BN / 4));
+      *reinterpret_cast<f32x4*>(&sB[buf][r * BN + c]) = rb[i];
+    }
+  };
+
+  f32x16 acc[RB][CP];
+#pragma unroll
+  for (int i = 0; i < RB; ++i)
+#pragma unroll
+    for (int c = 0; c < CP; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.0f;
+
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < BK / 8; ++j) {
+      f32x4 a[RB];
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int row = wave_m * WM + i * 32 + l32;
+        const int q = 2 * j + half;
+        a[i] = sA[buf][row * KCH + (q ^ a_swizzle<KCH>(row))];
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int k = 8 * j + 4 * half + s;
+        float bv[CP];
+        load_b_frag<CP>(&sB[buf][k * BN + wave_n * WN + CP * l32], bv);
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int c = 0; c < CP; ++c)
+            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], bv[c], acc[i][c], 0, 0, 0);
+      }
+    }
+  };
+
+  const int nk = (K + BK - 1) / BK;
+  if (nk > 0) {
+    load_global(0);
+    store_lds(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int buf = kt & 1;
+      const bool more = kt + 1 < nk;
+      if (more) load_global((kt + 1) * BK);
+      compute(buf);
+      if (more) store_lds(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // Epilogue: lane holds rows rbase + 8*(r/4) + 4*half + r%4 of each 32-row
+  // block and columns col0 + c, c < CP.
+  const int col0 = n0 + wave_n * WN + CP * l32;
+  float bvals[CP];
+#pragma unroll
+  for (int c = 0; c < CP; ++c) bvals[c] = 0.0f;
+  if constexpr (epi_has_bias(EPI)) {
+    if constexpr (!GUARD) {
+      load_b_frag<CP>(args.bias + col0, bvals);
+    } else {
+#pragma unroll
+      for (int c = 0; c < CP; ++c) bvals[c] = (col0 + c < N) ? args.bias[col0 + c] : 0.0f;
+    }
+  }
+  const float alpha = args.alpha;
+#pragma unroll
+  for (int i = 0; i < RB; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + wave_m * WM + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+      float v[CP];
+#pragma unroll
+      for (int c = 0; c < CP; ++c) v[c] = apply_epilogue_f32<EPI>(acc[i][c][r], bvals[c], alpha);
+      float* dst = args.C + (int64_t)row * args.ldc + col0;
+      if constexpr (!GUARD) {
+        if constexpr (CP == 4) {
+          f32x4 t = {v[0], v[1], v[2], v[3]};
+          *reinterpret_cast<f32x4*>(dst) = t;
+        } else if constexpr (CP == 2) {
+          f32x2 t = {v[0], v[1]};
+          *reinterpret_cast<f32x2*>(dst) = t;
+        } else {
+          *dst = v[0];
+        }
+      } else {
+        if (row < M) {
+#pragma unroll
+          for (int c = 0; c < CP; ++c)
+            if (col0 + c < N) dst[c] = v[c];
+        }
+      }
+    }
+  }
+}
+
+// Tile configurations. Keep in sync with kConfigs below.
+//  0: 256x256x16, 2x2 waves (wave tile 128x128, 256 accumulators / lane)
+//  1: 256x256x16, 4x2 waves (wave tile  64x128)
+//  2: 128x128x16, 2x2 waves (wave tile  64x64)
+//  3:  64x64x16,  2x2 waves (wave tile  32x32)
+//  4:  64x64x16,  2x2 waves, guarded (any shape / alignment)
+//  5: 256x256x32, 4x2 waves
+//  6: 128x256x16, 2x2 waves (wave tile 64x128)
+const GemmF32Config kConfigs[] = {
+    {256, 256, 16, 2, 2, false, "f32_256x256x16_w2x2"},
+    {256, 256, 16, 4, 2, false, "f32_256x256x16_w4x2"},
+    {128, 128, 16, 2, 2, false, "f32_128x128x16_w2x2"},
+    {64, 64, 16, 2, 2, false, "f32_64x64x16_w2x2"},
+    {64, 64, 16, 2, 2, true, "f32_64x64x16_w2x2_guard"},
+    {256, 256, 32, 4, 2, false, "f32_256x256x32_w4x2"},
+    {128, 256, 16, 2, 2, false, "f32_128x256x16_w2x2"},
+};
+constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
+
+template <int BM, int BN, int BK, int WMW, int WNW, bool GUARD>
+hipError_t launch_cfg(int epi, const GemmF32Args& a, hipStream_t stream) {
+  const dim3 grid(a.tiles_m * a.tiles_n);
+  const dim3 block(WMW * WNW * 64);
+#define EDSL_F32_CASE(E)                                                                      \
+  case E:                                                                                     \
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WMW, WNW, E, GUARD>), grid, block, 0, \
+                       stream, a);                                                            \
+    break;
+  switch (epi) {
+    EDSL_F32_CASE(epi_code(false, ACT_NONE))
+    EDSL_F32_CASE(epi_code(true, ACT_NONE))
+    EDSL_F32_CASE(epi_code(false, ACT_RELU))
+    EDSL_F32_CASE(epi_code(true, ACT_RELU))
+    EDSL_F32_CASE(epi_code(false, ACT_LEAKY))
+    EDSL_F32_CASE(epi_code(true, ACT_LEAKY))
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef EDSL_F32_CASE
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int gemm_f32_num_configs() { return kNumConfigs; }
+const GemmF32Config& gemm_f32_config(int cfg) { return kConfigs[cfg]; }
+
+hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) {
+  switch (cfg) {
+    case 0: return launch_cfg<256, 256, 16, 2, 2, false>(epi, a, stream);
+    case 1: return launch_cfg<256, 256, 16, 4, 2, false>(epi, a, stream);
+    case 2: return launch_cfg<128, 128, 16, 2, 2, false>(epi, a, stream);
+    case 3: return launch_cfg<64, 64, 16, 2, 2, false>(epi, a, stream);
+    case 4: return launch_cfg<64, 64, 16, 2, 2, true>(epi, a, stream);
+    case 5: return launch_cfg<256, 256, 32, 4, 2, false>(epi, a, stream);
+    case 6: return launch_cfg<128, 256, 16, 2, 2, false>(epi, a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace edsl

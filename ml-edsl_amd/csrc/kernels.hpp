@@ -1,0 +1,84 @@
+// Host-visible launch interface of the gfx950 dense-path kernels.
+// All pointers are device pointers; leading dimensions are in elements.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace edsl {
+
+// ---------------------------------------------------------------- fp32 tiled
+struct GemmF32Args {
+  const float* A;     // [M][K], row stride lda
+  const float* B;     // [K][N], row stride ldb
+  const float* bias;  // [N] or nullptr
+  float* C;           // [M][N], row stride ldc
+  int64_t lda, ldb, ldc;
+  int M, N, K;
+  int tiles_m, tiles_n;
+  float alpha;        // leaky-ReLU slope
+};
+
+struct GemmF32Config {
+  int bm, bn, bk;
+  int waves_m, waves_n;
+  bool guarded;       // bounds-checked scalar loads / stores (any shape, any alignment)
+  const char* name;
+};
+
+int gemm_f32_num_configs();
+const GemmF32Config& gemm_f32_config(int cfg);
+hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args args, hipStream_t stream);
+
+// ------------------------------------------------------------ fp32 small-M
+struct GemvF32Args {
+  const float* X;     // [M][K], row stride ldx
+  const float* W;     // [K][N], row stride ldw
+  const float* bias;  // [N] or nullptr
+  float* Y;           // [M][N], row stride ldy
+  int64_t ldx, ldw, ldy;
+  int M, N, K;
+  int ksplit;         // K slices reduced across workgroups (1 = none)
+  float alpha;
+  float* partials;    // [ksplit][16*mblocks][N] when ksplit > 1
+  unsigned* counters; // [N/64], all zero between calls
+};
+
+// Requirements (checked by the caller): 1 <= M <= 64, N % 64 == 0,
+// K % (64*ksplit) == 0, 16-byte aligned X/W/Y/bias and row strides % 4 == 0.
+hipError_t launch_gemv_f32(int epi, GemvF32Args args, hipStream_t stream);
+constexpr int kGemvMaxM = 64;
+
+// ------------------------------------------------------------- integer path
+struct NarrowI8Args {
+  const int32_t* X;   // [M][K], ldx
+  const int32_t* W;   // [K][N], ldw
+  int8_t* X8;         // [M][K] dense
+  int8_t* W8t;        // [N][K] dense (transposed)
+  int64_t ldx, ldw;
+  int M, N, K;
+  unsigned* flag;     // set to `epoch` when a value lies outside [-128, 127]
+  unsigned epoch;
+};
+
+struct GemmI32Args {
+  const int8_t* A8;   // [M][K] dense  (int8 fast path)
+  const int8_t* B8t;  // [N][K] dense  (int8 fast path)
+  const int32_t* X;   // [M][K], ldx   (exact i32 fallback)
+  const int32_t* W;   // [K][N], ldw   (exact i32 fallback)
+  const int32_t* bias;
+  int32_t* C;         // [M][N], ldc
+  int64_t ldx, ldw, ldc;
+  int M, N, K;
+  int tiles_m, tiles_n;
+  const unsigned* flag;  // fast path only when *flag != epoch
+  unsigned epoch;
+};
+
+constexpr int kI8Tile = 128;   // M, N, K multiples of this for the int8 MFMA path
+hipError_t launch_narrow_i8(NarrowI8Args args, hipStream_t stream);
+hipError_t launch_gemm_i8(int epi, GemmI32Args args, hipStream_t stream);
+// Exact wrapping i32 GEMM on the vector ALUs: any shape, any alignment.
+hipError_t launch_gemm_i32_valu(int epi, GemmI32Args args, hipStream_t stream);
+
+}  // namespace edsl

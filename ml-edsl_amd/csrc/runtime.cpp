@@ -1,0 +1,656 @@
+// HIP runtime module for ml-edsl's dense hot path: the C ABI of
+// include/edsl_hip.h and include/edsl_hip_device.h.
+//
+// It replaces the reference's NVVM/CUDA execution path -- MLIRGPUExecutor
+// (reference cpp/src/MLIRExecutor.cpp:158-247) and
+// MLIRCompiler::executeGPUFunction (cpp/src/MLIRCompiler.cpp:352-461), which
+// allocate, copy in, launch fill / matmul / bias+ReLU as three synchronous
+// kernels, copy out and free on every call -- with:
+//  * descriptor validation of MLIR's expanded memref arguments,
+//  * host or device operands (host operands staged through grow-only device
+//    buffers that persist across calls instead of per-call alloc/free),
+//  * one fused kernel per dense layer (two for the int8 path: narrow + GEMM),
+//  * kernel selection by shape: small-M weight streaming, tiled MFMA, or the
+//    bounds-checked tile for odd shapes / alignments.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <exception>
+#include <mutex>
+#include <string>
+
+#include "../../include/edsl_hip.h"
+#include "../../include/edsl_hip_device.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace {
+
+using namespace edsl;
+
+// ------------------------------------------------------------------ errors
+enum ErrorCode : int {
+  kErrShape = -1,     // sizes inconsistent with the op
+  kErrStride = -2,    // unsupported stride / layout
+  kErrDtype = -3,     // element type / size
+  kErrArgument = -4,  // null pointer, bad pattern, bad epilogue
+  kErrLimit = -5,     // size beyond what the kernels index
+  kErrInternal = -6,
+};
+
+struct Failure {
+  int code;
+  std::string msg;
+};
+
+thread_local int t_err_code = 0;
+thread_local std::string t_err_msg;
+thread_local std::string t_plan;
+
+[[noreturn]] void fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  throw Failure{code, buf};
+}
+
+void check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) fail((int)e, "%s failed: %s", what, hipGetErrorString(e));
+}
+
+template <typename F>
+int guarded(F&& f) {
+  t_err_code = 0;
+  t_err_msg.clear();
+  try {
+    f();
+    return 0;
+  } catch (const Failure& e) {
+    t_err_code = e.code;
+    t_err_msg = e.msg;
+  } catch (const std::exception& e) {
+    t_err_code = kErrInternal;
+    t_err_msg = e.what();
+  } catch (...) {
+    t_err_code = kErrInternal;
+    t_err_msg = "unknown error";
+  }
+  return t_err_code;
+}
+
+void set_plan(const char* fmt, ...) {
+  char buf[256];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  t_plan = buf;
+}
+
+int copy_out(const std::string& s, char* buf, size_t len) {
+  if (buf && len > 0) {
+    const size_t n = std::min(len - 1, s.size());
+    memcpy(buf, s.data(), n);
+    buf[n] = '\0';
+  }
+  return (int)s.size();
+}
+
+// ------------------------------------------------------------ device state
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+  // Grow-only. The old buffer may still be in use by queued work, so the
+  // device is drained before it is released.
+  void* ensure(size_t bytes, bool zero_fill) {
+    if (bytes <= cap && p) return p;
+    if (p) {
+      check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
+      check_hip(hipFree(p), "hipFree");
+      p = nullptr;
+      cap = 0;
+    }
+    const size_t want = std::max<size_t>((bytes + 255) & ~size_t(255), 256);
+    check_hip(hipMalloc(&p, want), "hipMalloc");
+    if (zero_fill) check_hip(hipMemset(p, 0, want), "hipMemset");
+    cap = want;
+    return p;
+  }
+};
+
+struct DeviceState {
+  bool ready = false;
+  int cus = 256;
+  DevBuf stage[4];  // host-operand staging: X/A, W/B, bias, Y/C
+  DevBuf gemv_partials;
+  DevBuf gemv_counters;
+  DevBuf i8_x, i8_w, i8_flag;
+  unsigned epoch = 0;
+};
+
+constexpr int kMaxDevices = 64;
+std::mutex g_mu;
+DeviceState g_dev[kMaxDevices];
+int g_force_cfg = -1;
+int g_force_ksplit = 0;
+
+void read_env_overrides() {
+  static bool done = false;
+  if (done) return;
+  done = true;
+  if (const char* s = getenv("EDSL_HIP_F32_CONFIG")) g_force_cfg = atoi(s);
+  if (const char* s = getenv("EDSL_HIP_GEMV_KSPLIT")) g_force_ksplit = atoi(s);
+}
+
+DeviceState& device_state(int* dev_out) {
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) fail(kErrLimit, "device index %d out of range", dev);
+  DeviceState& s = g_dev[dev];
+  if (!s.ready) {
+    hipDeviceProp_t prop;
+    check_hip(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
+    s.cus = std::max(1, prop.multiProcessorCount);
+    s.ready = true;
+  }
+  if (dev_out) *dev_out = dev;
+  return s;
+}
+
+// ---------------------------------------------------------- operand views
+struct Mat {
+  char* base = nullptr;  // aligned + offset
+  int64_t rows = 0, cols = 0, ld = 0;
+};
+
+struct Vec {
+  char* base = nullptr;
+  int64_t n = 0;
+};
+
+Mat mat_from_desc(void* aligned, int64_t offset, int64_t d0, int64_t d1, int64_t s0, int64_t s1,
+                  size_t esize, const char* name) {
+  if (d0 < 0 || d1 < 0) fail(kErrShape, "%s: negative size (%lld, %lld)", name, (long long)d0, (long long)d1);
+  Mat m;
+  m.rows = d0;
+  m.cols = d1;
+  m.ld = d1;
+  if (d0 == 0 || d1 == 0) return m;
+  if (!aligned) fail(kErrArgument, "%s: null data pointer", name);
+  if (offset < 0) fail(kErrArgument, "%s: negative offset %lld", name, (long long)offset);
+  if (d1 > 1 && s1 != 1)
+    fail(kErrStride, "%s: innermost stride %lld unsupported (must be 1)", name, (long long)s1);
+  if (d0 > 1) {
+    if (s0 < d1) fail(kErrStride, "%s: row stride %lld < row length %lld", name, (long long)s0, (long long)d1);
+    m.ld = s0;
+  }
+  m.base = static_cast<char*>(aligned) + offset * (int64_t)esize;
+  return m;
+}
+
+Vec vec_from_desc(void* aligned, int64_t offset, int64_t d0, int64_t s0, size_t esize, const char* name) {
+  if (d0 < 0) fail(kErrShape, "%s: negative size %lld", name, (long long)d0);
+  Vec v;
+  v.n = d0;
+  if (d0 == 0) return v;
+  if (!aligned) fail(kErrArgument, "%s: null data pointer", name);
+  if (offset < 0) fail(kErrArgument, "%s: negative offset %lld", name, (long long)offset);
+  if (d0 > 1 && s0 != 1) fail(kErrStride, "%s: stride %lld unsupported (must be 1)", name, (long long)s0);
+  v.base = static_cast<char*>(aligned) + offset * (int64_t)esize;
+  return v;
+}
+
+bool is_device_pointer(const void* p, int dev) {
+  hipPointerAttribute_t a;
+  const hipError_t e = hipPointerGetAttributes(&a, p);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  if (a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged) {
+    if (a.type == hipMemoryTypeDevice && a.device != dev)
+      fail(kErrArgument, "operand lives on device %d but the current device is %d", a.device, dev);
+    return true;
+  }
+  return false;
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// ------------------------------------------------------- kernel selection
+struct DenseLaunch {
+  int dtype;  // EDSL_DTYPE_*
+  int epi;
+  float alpha;
+  const void* x;
+  int64_t ldx;
+  const void* w;
+  int64_t ldw;
+  const void* bias;
+  void* y;
+  int64_t ldy;
+  int64_t M, N, K;
+};
+
+void check_dims(int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N < 0 || K < 0) fail(kErrShape, "negative dimension");
+  if (M > INT_MAX / 2 || N > INT_MAX / 2 || K > INT_MAX / 2)
+    fail(kErrLimit, "dimension beyond 2^30 (M=%lld N=%lld K=%lld)", (long long)M, (long long)N,
+         (long long)K);
+}
+
+int choose_gemv_ksplit(const DeviceState& ds, int64_t N, int64_t K) {
+  const int64_t groups = N / 64;
+  if (g_force_ksplit > 0 && K % (64LL * g_force_ksplit) == 0) return g_force_ksplit;
+  int ks = 1;
+  while (groups * ks < 2LL * ds.cus && K % (64LL * ks * 2) == 0 && K / (ks * 2) >= 256) ks *= 2;
+  return ks;
+}
+
+void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
+  const bool has_bias = epi_has_bias(L.epi);
+  const bool aligned = al16(L.x) && al16(L.w) && al16(L.y) && (!has_bias || al16(L.bias)) &&
+                       L.ldx % 4 == 0 && L.ldw % 4 == 0 && L.ldy % 4 == 0;
+  const int M = (int)L.M, N = (int)L.N, K = (int)L.K;
+
+  if (aligned && M >= 1 && M <= kGemvMaxM && N % 64 == 0 && K % 64 == 0 && K > 0) {
+    GemvF32Args a{};
+    a.X = static_cast<const float*>(L.x);
+    a.W = static_cast<const float*>(L.w);
+    a.bias = static_cast<const float*>(L.bias);
+    a.Y = static_cast<float*>(L.y);
+    a.ldx = L.ldx;
+    a.ldw = L.ldw;
+    a.ldy = L.ldy;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.alpha = L.alpha;
+    a.ksplit = choose_gemv_ksplit(ds, N, K);
+    const int mb = (M + 15) / 16;
+    if (a.ksplit > 1) {
+      a.partials = static_cast<float*>(
+          ds.gemv_partials.ensure((size_t)a.ksplit * 16 * mb * N * sizeof(float), false));
+      a.counters = static_cast<unsigned*>(ds.gemv_counters.ensure((size_t)(N / 64) * sizeof(unsigned), true));
+    }
+    check_hip(launch_gemv_f32(L.epi, a, stream), "gemv_f32 launch");
+    set_plan("gemv_f32 mb=%d ksplit=%d grid=%d", mb, a.ksplit, (N / 64) * a.ksplit);
+    return;
+  }
+
+  int cfg = -1;
+  auto fits = [&](int c) {
+    const GemmF32Config& g = gemm_f32_config(c);
+    return !g.guarded && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
+  };
+  if (aligned && K > 0) {
+    if (g_force_cfg >= 0 && g_force_cfg < gemm_f32_num_configs() && fits(g_force_cfg)) {
+      cfg = g_force_cfg;
+    } else {
+      static const int kOrder[] = {0, 6, 2, 3};
+      int best = -1;
+      int64_t best_tiles = 0;
+      for (int c : kOrder) {
+        if (!fits(c)) continue;
+        const GemmF32Config& g = gemm_f32_config(c);
+        const int64_t tiles = (int64_t)(M / g.bm) * (N / g.bn);
+        if (tiles >= ds.cus) {
+          cfg = c;
+          break;
+        }
+        if (tiles > best_tiles) {
+          best_tiles = tiles;
+          best = c;
+        }
+      }
+      if (cfg < 0) cfg = best;
+    }
+  }
+  if (cfg < 0) cfg = 4;  // guarded: any shape and alignment
+  const GemmF32Config& g = gemm_f32_config(cfg);
+  GemmF32Args a{};
+  a.A = static_cast<const float*>(L.x);
+  a.B = static_cast<const float*>(L.w);
+  a.bias = static_cast<const float*>(L.bias);
+  a.C = static_cast<float*>(L.y);
+  a.lda = L.ldx;
+  a.ldb = L.ldw;
+  a.ldc = L.ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.alpha = L.alpha;
+  a.tiles_m = (M + g.bm - 1) / g.bm;
+  a.tiles_n = (N + g.bn - 1) / g.bn;
+  check_hip(launch_gemm_f32(cfg, L.epi, a, stream), "gemm_f32 launch");
+  set_plan("gemm_f32 cfg=%s grid=%d", g.name, a.tiles_m * a.tiles_n);
+}
+
+void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
+  if (epi_act(L.epi) == ACT_LEAKY) fail(kErrDtype, "leaky_relu is float-only");
+  GemmI32Args a{};
+  a.X = static_cast<const int32_t*>(L.x);
+  a.W = static_cast<const int32_t*>(L.w);
+  a.bias = static_cast<const int32_t*>(L.bias);
+  a.C = static_cast<int32_t*>(L.y);
+  a.ldx = L.ldx;
+  a.ldw = L.ldw;
+  a.ldc = L.ldy;
+  a.M = (int)L.M;
+  a.N = (int)L.N;
+  a.K = (int)L.K;
+  const bool tiled = a.M % kI8Tile == 0 && a.N % kI8Tile == 0 && a.K % kI8Tile == 0 && a.K > 0 &&
+                     a.K < (1 << 17);
+  if (tiled) {
+    const size_t xs = (size_t)a.M * a.K, ws = (size_t)a.N * a.K;
+    int8_t* x8 = static_cast<int8_t*>(ds.i8_x.ensure(xs, false));
+    int8_t* w8 = static_cast<int8_t*>(ds.i8_w.ensure(ws, false));
+    unsigned* flag = static_cast<unsigned*>(ds.i8_flag.ensure(sizeof(unsigned), true));
+    if (++ds.epoch == 0) ++ds.epoch;
+    NarrowI8Args n{};
+    n.X = a.X;
+    n.W = a.W;
+    n.X8 = x8;
+    n.W8t = w8;
+    n.ldx = a.ldx;
+    n.ldw = a.ldw;
+    n.M = a.M;
+    n.N = a.N;
+    n.K = a.K;
+    n.flag = flag;
+    n.epoch = ds.epoch;
+    check_hip(launch_narrow_i8(n, stream), "narrow_i8 launch");
+    a.A8 = x8;
+    a.B8t = w8;
+    a.flag = flag;
+    a.epoch = ds.epoch;
+    check_hip(launch_gemm_i8(L.epi, a, stream), "gemm_i8 launch");
+    set_plan("narrow_i8+gemm_i8 grid=%d", (a.M / kI8Tile) * (a.N / kI8Tile));
+  } else {
+    check_hip(launch_gemm_i32_valu(L.epi, a, stream), "gemm_i32_valu launch");
+    set_plan("gemm_i32_valu grid=%d", ((a.M + 127) / 128) * ((a.N + 127) / 128));
+  }
+}
+
+void launch_dense(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
+  check_dims(L.M, L.N, L.K);
+  if (L.M == 0 || L.N == 0) {
+    set_plan("empty");
+    return;
+  }
+  if (L.epi < 0 || L.epi > 5) fail(kErrArgument, "bad epilogue code %d", L.epi);
+  if (L.dtype == EDSL_DTYPE_F32)
+    launch_f32(ds, L, stream);
+  else if (L.dtype == EDSL_DTYPE_I32)
+    launch_i32(ds, L, stream);
+  else
+    fail(kErrDtype, "bad dtype %d", L.dtype);
+}
+
+// ------------------------------------------------- synchronous host entry
+// Shapes: X [M,K], W [K,N], bias [N] (when the epilogue adds one), Y [M,N].
+void sync_dense(int dtype, int epi, float alpha, const Mat& X, const Mat& W, const Vec* b, const Mat& Y) {
+  const int64_t M = X.rows, K = X.cols, N = W.cols;
+  if (W.rows != K)
+    fail(kErrShape, "matmul inner dimensions must match: lhs K=%lld, rhs K=%lld", (long long)K,
+         (long long)W.rows);
+  if (Y.rows != M || Y.cols != N)
+    fail(kErrShape, "output shape [%lld,%lld] does not match [%lld,%lld]", (long long)Y.rows,
+         (long long)Y.cols, (long long)M, (long long)N);
+  if (epi_has_bias(epi) && (!b || b->n != N))
+    fail(kErrShape, "bias length %lld does not match N=%lld", (long long)(b ? b->n : -1), (long long)N);
+  check_dims(M, N, K);
+  if (M == 0 || N == 0) {
+    set_plan("empty");
+    return;
+  }
+
+  std::lock_guard<std::mutex> lock(g_mu);
+  read_env_overrides();
+  int dev = 0;
+  DeviceState& ds = device_state(&dev);
+  hipStream_t stream = nullptr;
+  const size_t es = 4;
+
+  // Host operands are staged through persistent device buffers with 16-byte
+  // aligned rows so the fast kernels stay eligible.
+  auto stage_in = [&](const Mat& m, DevBuf& buf, int64_t* ld) -> const void* {
+    if (m.rows == 0 || m.cols == 0) {
+      *ld = m.ld;
+      return m.base;
+    }
+    if (is_device_pointer(m.base, dev)) {
+      *ld = m.ld;
+      return m.base;
+    }
+    const int64_t dld = (m.cols + 3) & ~int64_t(3);
+    void* d = buf.ensure((size_t)m.rows * dld * es, false);
+    check_hip(hipMemcpy2DAsync(d, dld * es, m.base, m.ld * es, m.cols * es, m.rows,
+                               hipMemcpyHostToDevice, stream),
+              "hipMemcpy2DAsync H2D");
+    *ld = dld;
+    return d;
+  };
+
+  DenseLaunch L{};
+  L.dtype = dtype;
+  L.epi = epi;
+  L.alpha = alpha;
+  L.M = M;
+  L.N = N;
+  L.K = K;
+  L.x = stage_in(X, ds.stage[0], &L.ldx);
+  L.w = stage_in(W, ds.stage[1], &L.ldw);
+  if (epi_has_bias(epi)) {
+    if (is_device_pointer(b->base, dev)) {
+      L.bias = b->base;
+    } else {
+      void* d = ds.stage[2].ensure((size_t)N * es, false);
+      check_hip(hipMemcpyAsync(d, b->base, (size_t)N * es, hipMemcpyHostToDevice, stream), "hipMemcpyAsync H2D");
+      L.bias = d;
+    }
+  }
+  const bool y_dev = is_device_pointer(Y.base, dev);
+  if (y_dev) {
+    L.y = Y.base;
+    L.ldy = Y.ld;
+  } else {
+    L.ldy = (N + 3) & ~int64_t(3);
+    L.y = ds.stage[3].ensure((size_t)M * L.ldy * es, false);
+  }
+
+  launch_dense(ds, L, stream);
+  if (!y_dev)
+    check_hip(hipMemcpy2DAsync(Y.base, Y.ld * es, L.y, L.ldy * es, N * es, M, hipMemcpyDeviceToHost, stream),
+              "hipMemcpy2DAsync D2H");
+  check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  check_hip(hipGetLastError(), "kernel execution");
+}
+
+}  // namespace
+
+// ====================================================================== ABI
+#define MEMREF2(T, p) \
+  T *p##_allocated, T *p##_aligned, int64_t p##_offset, int64_t p##_size0, int64_t p##_size1, \
+      int64_t p##_stride0, int64_t p##_stride1
+#define MEMREF1(T, p) T *p##_allocated, T *p##_aligned, int64_t p##_offset, int64_t p##_size0, int64_t p##_stride0
+#define MAT(p, name) \
+  mat_from_desc((void*)p##_aligned, p##_offset, p##_size0, p##_size1, p##_stride0, p##_stride1, 4, name)
+#define VEC(p, name) vec_from_desc((void*)p##_aligned, p##_offset, p##_size0, p##_stride0, 4, name)
+
+extern "C" {
+
+void edsl_hip_matmul_f32(MEMREF2(float, A), MEMREF2(float, B), MEMREF2(float, C)) {
+  (void)A_allocated; (void)B_allocated; (void)C_allocated;
+  guarded([&] { sync_dense(EDSL_DTYPE_F32, EDSL_EPI_NONE, 0.f, MAT(A, "A"), MAT(B, "B"), nullptr, MAT(C, "C")); });
+}
+
+void edsl_hip_matmul_i32(MEMREF2(int32_t, A), MEMREF2(int32_t, B), MEMREF2(int32_t, C)) {
+  (void)A_allocated; (void)B_allocated; (void)C_allocated;
+  guarded([&] { sync_dense(EDSL_DTYPE_I32, EDSL_EPI_NONE, 0.f, MAT(A, "A"), MAT(B, "B"), nullptr, MAT(C, "C")); });
+}
+
+void edsl_hip_matmul_relu_f32(MEMREF2(float, A), MEMREF2(float, B), MEMREF2(float, C)) {
+  (void)A_allocated; (void)B_allocated; (void)C_allocated;
+  guarded([&] { sync_dense(EDSL_DTYPE_F32, EDSL_EPI_RELU, 0.f, MAT(A, "A"), MAT(B, "B"), nullptr, MAT(C, "C")); });
+}
+
+void edsl_hip_matmul_relu_i32(MEMREF2(int32_t, A), MEMREF2(int32_t, B), MEMREF2(int32_t, C)) {
+  (void)A_allocated; (void)B_allocated; (void)C_allocated;
+  guarded([&] { sync_dense(EDSL_DTYPE_I32, EDSL_EPI_RELU, 0.f, MAT(A, "A"), MAT(B, "B"), nullptr, MAT(C, "C")); });
+}
+
+void edsl_hip_matmul_bias_f32(MEMREF2(float, X), MEMREF2(float, W), MEMREF1(float, b), MEMREF2(float, Y)) {
+  (void)X_allocated; (void)W_allocated; (void)b_allocated; (void)Y_allocated;
+  guarded([&] {
+    const Vec bv = VEC(b, "b");
+    sync_dense(EDSL_DTYPE_F32, EDSL_EPI_BIAS, 0.f, MAT(X, "X"), MAT(W, "W"), &bv, MAT(Y, "Y"));
+  });
+}
+
+void edsl_hip_matmul_bias_i32(MEMREF2(int32_t, X), MEMREF2(int32_t, W), MEMREF1(int32_t, b),
+                              MEMREF2(int32_t, Y)) {
+  (void)X_allocated; (void)W_allocated; (void)b_allocated; (void)Y_allocated;
+  guarded([&] {
+    const Vec bv = VEC(b, "b");
+    sync_dense(EDSL_DTYPE_I32, EDSL_EPI_BIAS, 0.f, MAT(X, "X"), MAT(W, "W"), &bv, MAT(Y, "Y"));
+  });
+}
+
+void edsl_hip_dense_relu_f32(MEMREF2(float, X), MEMREF2(float, W), MEMREF1(float, b), MEMREF2(float, Y)) {
+  (void)X_allocated; (void)W_allocated; (void)b_allocated; (void)Y_allocated;
+  guarded([&] {
+    const Vec bv = VEC(b, "b");
+    sync_dense(EDSL_DTYPE_F32, EDSL_EPI_BIAS_RELU, 0.f, MAT(X, "X"), MAT(W, "W"), &bv, MAT(Y, "Y"));
+  });
+}
+
+void edsl_hip_dense_relu_i32(MEMREF2(int32_t, X), MEMREF2(int32_t, W), MEMREF1(int32_t, b),
+                             MEMREF2(int32_t, Y)) {
+  (void)X_allocated; (void)W_allocated; (void)b_allocated; (void)Y_allocated;
+  guarded([&] {
+    const Vec bv = VEC(b, "b");
+    sync_dense(EDSL_DTYPE_I32, EDSL_EPI_BIAS_RELU, 0.f, MAT(X, "X"), MAT(W, "W"), &bv, MAT(Y, "Y"));
+  });
+}
+
+void edsl_hip_dense_leaky_relu_f32(MEMREF2(float, X), MEMREF2(float, W), MEMREF1(float, b), MEMREF2(float, Y),
+                                   float alpha) {
+  (void)X_allocated; (void)W_allocated; (void)b_allocated; (void)Y_allocated;
+  guarded([&] {
+    const Vec bv = VEC(b, "b");
+    sync_dense(EDSL_DTYPE_F32, EDSL_EPI_BIAS_LEAKY, alpha, MAT(X, "X"), MAT(W, "W"), &bv, MAT(Y, "Y"));
+  });
+}
+
+int edsl_hip_execute_gpu_function(int pattern, int dtype, int num_inputs, const void* const* input_ptrs,
+                                  const int64_t* const* input_shapes, const int* input_ranks, void* output,
+                                  const int64_t* output_shape, int output_rank, size_t element_size,
+                                  float alpha) {
+  return guarded([&] {
+    if (element_size != 4) fail(kErrDtype, "element_size %zu unsupported (f32 and i32 are 4 bytes)", element_size);
+    if (dtype != EDSL_DTYPE_F32 && dtype != EDSL_DTYPE_I32) fail(kErrDtype, "bad dtype %d", dtype);
+    int epi = 0;
+    int want_inputs = 3;
+    switch (pattern) {
+      case EDSL_PATTERN_MATMUL: epi = EDSL_EPI_NONE; want_inputs = 2; break;
+      case EDSL_PATTERN_MATMUL_RELU: epi = EDSL_EPI_RELU; want_inputs = 2; break;
+      case EDSL_PATTERN_MATMUL_BIAS: epi = EDSL_EPI_BIAS; break;
+      case EDSL_PATTERN_DENSE_RELU: epi = EDSL_EPI_BIAS_RELU; break;
+      case EDSL_PATTERN_DENSE_LEAKY: epi = EDSL_EPI_BIAS_LEAKY; break;
+      default: fail(kErrArgument, "unknown pattern %d", pattern);
+    }
+    if (num_inputs != want_inputs)
+      fail(kErrArgument, "pattern %d takes %d inputs, got %d", pattern, want_inputs, num_inputs);
+    if (!input_ptrs || !input_shapes || !input_ranks || !output_shape)
+      fail(kErrArgument, "null argument array");
+    for (int i = 0; i < 2; ++i)
+      if (input_ranks[i] != 2) fail(kErrShape, "input %d must be 2-D, got rank %d", i, input_ranks[i]);
+    if (want_inputs == 3 && input_ranks[2] != 1) fail(kErrShape, "bias must be 1-D, got rank %d", input_ranks[2]);
+    if (output_rank != 2) fail(kErrShape, "output must be 2-D, got rank %d", output_rank);
+    auto contiguous = [&](const void* p, const int64_t* s, const char* name) {
+      return mat_from_desc(const_cast<void*>(p), 0, s[0], s[1], s[1], 1, 4, name);
+    };
+    const Mat X = contiguous(input_ptrs[0], input_shapes[0], "lhs");
+    const Mat W = contiguous(input_ptrs[1], input_shapes[1], "rhs");
+    const Mat Y = contiguous(output, output_shape, "output");
+    Vec b;
+    if (want_inputs == 3) b = vec_from_desc(const_cast<void*>(input_ptrs[2]), 0, input_shapes[2][0], 1, 4, "bias");
+    sync_dense(dtype, epi, alpha, X, W, want_inputs == 3 ? &b : nullptr, Y);
+  });
+}
+
+int edsl_hip_last_error(char* buf, size_t len) {
+  copy_out(t_err_msg, buf, len);
+  return t_err_code;
+}
+
+void edsl_hip_clear_error(void) {
+  t_err_code = 0;
+  t_err_msg.clear();
+}
+
+int edsl_hip_dense_f32_launch(const float* X, int64_t ldx, const float* W, int64_t ldw, const float* bias,
+                              float* Y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
+                              float alpha, void* stream) {
+  return guarded([&] {
+    if (epi_has_bias(epilogue) && !bias && N > 0) fail(kErrArgument, "epilogue adds a bias but bias is null");
+    if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) fail(kErrArgument, "null operand");
+    if (ldx < std::max<int64_t>(K, 1) && M > 1) fail(kErrStride, "ldx < K");
+    if (ldw < std::max<int64_t>(N, 1) && K > 1) fail(kErrStride, "ldw < N");
+    if (ldy < std::max<int64_t>(N, 1) && M > 1) fail(kErrStride, "ldy < N");
+    std::lock_guard<std::mutex> lock(g_mu);
+    read_env_overrides();
+    DeviceState& ds = device_state(nullptr);
+    DenseLaunch L{EDSL_DTYPE_F32, epilogue, alpha, X, ldx, W, ldw, bias, Y, ldy, M, N, K};
+    launch_dense(ds, L, static_cast<hipStream_t>(stream));
+  });
+}
+
+int edsl_hip_dense_i32_launch(const int32_t* X, int64_t ldx, const int32_t* W, int64_t ldw,
+                              const int32_t* bias, int32_t* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                              int epilogue, void* stream) {
+  return guarded([&] {
+    if (epi_has_bias(epilogue) && !bias && N > 0) fail(kErrArgument, "epilogue adds a bias but bias is null");
+    if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) fail(kErrArgument, "null operand");
+    if (ldx < std::max<int64_t>(K, 1) && M > 1) fail(kErrStride, "ldx < K");
+    if (ldw < std::max<int64_t>(N, 1) && K > 1) fail(kErrStride, "ldw < N");
+    if (ldy < std::max<int64_t>(N, 1) && M > 1) fail(kErrStride, "ldy < N");
+    std::lock_guard<std::mutex> lock(g_mu);
+    read_env_overrides();
+    DeviceState& ds = device_state(nullptr);
+    DenseLaunch L{EDSL_DTYPE_I32, epilogue, 0.f, X, ldx, W, ldw, bias, Y, ldy, M, N, K};
+    launch_dense(ds, L, static_cast<hipStream_t>(stream));
+  });
+}
+
+int edsl_hip_last_plan(char* buf, size_t len) { return copy_out(t_plan, buf, len); }
+
+void edsl_hip_set_f32_config(int cfg) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  read_env_overrides();
+  g_force_cfg = cfg;
+}
+
+void edsl_hip_set_gemv_ksplit(int ksplit) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  read_env_overrides();
+  g_force_ksplit = ksplit;
+}
+
+int edsl_hip_f32_config_count(void) { return gemm_f32_num_configs(); }
+
+int edsl_hip_f32_config_name(int cfg, char* buf, size_t len) {
+  if (cfg < 0 || cfg >= gemm_f32_num_configs()) return -1;
+  return copy_out(gemm_f32_config(cfg).name, buf, len);
+}
+
+}  // extern "C"

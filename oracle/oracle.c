@@ -1,0 +1,188 @@
+/*
+ * oracle.c -- CPU restatement of the reference CPU-JIT dense path.
+ * TEST INFRASTRUCTURE ONLY (see oracle.h for what is restated and where).
+ *
+ * Build: see oracle/Makefile. Compiled with -ffp-contract=off so that the
+ * scalar mulf+addf path is not fused behind our back; the fma path calls fmaf.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* Planted mistakes, for the tests that show the pinning checks catch them:
+ *  1  W read transposed (W[n][k] instead of W[k][n]; square shapes only)
+ *  2  bias dropped
+ *  3  ReLU as fmaxf (NaN -> 0 instead of NaN)
+ *  4  bias subtracted
+ *  5  last k term dropped
+ *  6  fma path replaced by mulf+addf rounding
+ *  7  leaky slope applied to the positive side
+ *  8  i32 accumulated in f32
+ */
+static int g_mutation = 0;
+
+void oracle_set_mutation(int mutation) { g_mutation = mutation; }
+
+enum { ACT_NONE = 0, ACT_RELU = 1, ACT_LEAKY = 2 };
+
+int oracle_static_tiles(int64_t M, int64_t N, int64_t K) {
+  /* Outer 64x64 forall tiles have static sizes when the dimension divides by
+   * 64 or fits in one tile (the single-iteration forall folds away); the
+   * inner 8x8x8 tiles are static only when the enclosing size is static and
+   * divisible by 8. LinalgMatmulToContractPass needs all three operands as
+   * static 8x8 (reference cpp/src/MLIRLoweringPasses.cpp:135-143). */
+  const int m_ok = (M <= 64 || M % 64 == 0) && M % 8 == 0;
+  const int n_ok = (N <= 64 || N % 64 == 0) && N % 8 == 0;
+  const int k_ok = K % 8 == 0;
+  return m_ok && n_ok && k_ok;
+}
+
+static inline float w_at(const float *W, int64_t k, int64_t n, int64_t N, int64_t K) {
+  if (g_mutation == 1) return W[n * K + k];
+  return W[k * N + n];
+}
+
+/* 8x8x8 micro-kernel: vector.contract lowered to outer products, each a
+ * vector.fma over a row of C (reference MLIRLoweringPasses.cpp:242-260). */
+static void micro_fma_8x8x8(const float *A, const float *W, float *C, int64_t m0, int64_t n0,
+                            int64_t k0, int64_t N, int64_t K) {
+  float c[8][8];
+  for (int m = 0; m < 8; ++m)
+    for (int n = 0; n < 8; ++n) c[m][n] = C[(m0 + m) * N + n0 + n];
+  for (int k = 0; k < 8; ++k) {
+    if (g_mutation == 5 && k0 + k == K - 1) continue;
+    for (int m = 0; m < 8; ++m) {
+      const float a = A[(m0 + m) * K + k0 + k];
+      for (int n = 0; n < 8; ++n) {
+        const float w = w_at(W, k0 + k, n0 + n, N, K);
+        if (g_mutation == 6)
+          c[m][n] = c[m][n] + a * w;
+        else
+          c[m][n] = fmaf(a, w, c[m][n]);
+      }
+    }
+  }
+  for (int m = 0; m < 8; ++m)
+    for (int n = 0; n < 8; ++n) C[(m0 + m) * N + n0 + n] = c[m][n];
+}
+
+static void matmul_f32(const float *A, const float *W, float *C, int64_t M, int64_t N, int64_t K,
+                       int threads) {
+  /* linalg.fill: runs serially before the parallel matmul. */
+  for (int64_t i = 0; i < M * N; ++i) C[i] = 0.0f;
+  const int fma_path = oracle_static_tiles(M, N, K);
+  const int64_t tiles_m = (M + 63) / 64, tiles_n = (N + 63) / 64;
+  const int64_t tiles = tiles_m * tiles_n;
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : omp_get_max_threads())
+  for (int64_t t = 0; t < tiles; ++t) {
+    const int64_t m0 = (t / tiles_n) * 64, n0 = (t % tiles_n) * 64;
+    const int64_t mh = M - m0 < 64 ? M - m0 : 64;
+    const int64_t nh = N - n0 < 64 ? N - n0 : 64;
+    for (int64_t mi = 0; mi < mh; mi += 8)
+      for (int64_t ni = 0; ni < nh; ni += 8)
+        for (int64_t ki = 0; ki < K; ki += 8) {
+          if (fma_path) {
+            micro_fma_8x8x8(A, W, C, m0 + mi, n0 + ni, ki, N, K);
+            continue;
+          }
+          /* Dynamic tile: convert-linalg-to-loops, scalar mulf then addf. */
+          const int64_t me = mi + 8 < mh ? mi + 8 : mh;
+          const int64_t ne = ni + 8 < nh ? ni + 8 : nh;
+          const int64_t ke = ki + 8 < K ? ki + 8 : K;
+          for (int64_t m = m0 + mi; m < m0 + me; ++m)
+            for (int64_t n = n0 + ni; n < n0 + ne; ++n) {
+              float c = C[m * N + n];
+              for (int64_t k = ki; k < ke; ++k) {
+                if (g_mutation == 5 && k == K - 1) continue;
+                const float p = A[m * K + k] * w_at(W, k, n, N, K);
+                c = c + p;
+              }
+              C[m * N + n] = c;
+            }
+        }
+  }
+}
+
+static inline float maximumf0(float x) {
+  if (g_mutation == 3) return fmaxf(x, 0.0f);
+  return (x > 0.0f || x != x) ? x : 0.0f; /* NaN -> NaN, -0 -> +0 */
+}
+
+static inline float minimumf0(float x) {
+  return (x < 0.0f || x != x || x == 0.0f) ? x : 0.0f; /* NaN -> NaN, -0 -> -0 */
+}
+
+int oracle_dense_f32(const float *X, const float *W, const float *b, float *Y, int64_t M,
+                     int64_t N, int64_t K, int epilogue, float alpha, int threads) {
+  if (epilogue < 0 || epilogue > 5) return -1;
+  const int has_bias = epilogue & 1;
+  const int act = (epilogue >> 1) & 3;
+  matmul_f32(X, W, Y, M, N, K, threads);
+  if (!has_bias && act == ACT_NONE) return 0;
+  /* The merged bias + activation generic: one serial elementwise pass. */
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) {
+      float y = Y[m * N + n];
+      if (has_bias && g_mutation != 2) y = (g_mutation == 4) ? y - b[n] : y + b[n];
+      if (act == ACT_RELU) {
+        y = maximumf0(y);
+      } else if (act == ACT_LEAKY) {
+        const float pos = maximumf0(y), neg = minimumf0(y);
+        if (g_mutation == 7) {
+          const float scaled = pos * alpha;
+          y = scaled + neg;
+        } else {
+          const float scaled = neg * alpha;
+          y = pos + scaled;
+        }
+      }
+      Y[m * N + n] = y;
+    }
+  return 0;
+}
+
+int oracle_dense_i32(const int32_t *X, const int32_t *W, const int32_t *b, int32_t *Y, int64_t M,
+                     int64_t N, int64_t K, int epilogue, int threads) {
+  if (epilogue < 0 || epilogue > 3) return -1; /* leaky is float-only */
+  const int has_bias = epilogue & 1;
+  const int act = (epilogue >> 1) & 3;
+  for (int64_t i = 0; i < M * N; ++i) Y[i] = 0;
+  const int64_t tiles_m = (M + 63) / 64, tiles_n = (N + 63) / 64;
+  const int64_t tiles = tiles_m * tiles_n;
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : omp_get_max_threads())
+  for (int64_t t = 0; t < tiles; ++t) {
+    const int64_t m0 = (t / tiles_n) * 64, n0 = (t % tiles_n) * 64;
+    const int64_t me = M - m0 < 64 ? M : m0 + 64;
+    const int64_t ne = N - n0 < 64 ? N : n0 + 64;
+    for (int64_t m = m0; m < me; ++m)
+      for (int64_t k = 0; k < K; ++k) {
+        if (g_mutation == 5 && k == K - 1) continue;
+        const uint32_t a = (uint32_t)X[m * K + k];
+        for (int64_t n = n0; n < ne; ++n) {
+          const uint32_t w = (uint32_t)(g_mutation == 1 ? W[n * K + k] : W[k * N + n]);
+          if (g_mutation == 8) {
+            Y[m * N + n] = (int32_t)((float)Y[m * N + n] + (float)(int32_t)a * (float)(int32_t)w);
+          } else {
+            Y[m * N + n] = (int32_t)((uint32_t)Y[m * N + n] + a * w); /* muli, addi: mod 2^32 */
+          }
+        }
+      }
+  }
+  if (!has_bias && act == ACT_NONE) return 0;
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) {
+      int32_t y = Y[m * N + n];
+      if (has_bias && g_mutation != 2)
+        y = (int32_t)(g_mutation == 4 ? (uint32_t)y - (uint32_t)b[n] : (uint32_t)y + (uint32_t)b[n]);
+      if (act == ACT_RELU) y = y > 0 ? y : 0; /* If(v > 0, v, 0) */
+      Y[m * N + n] = y;
+    }
+  return 0;
+}

@@ -1,0 +1,59 @@
+/*
+ * oracle.h -- CPU restatement of the reference's CPU-JIT lowering of the dense
+ * path (linalg.matmul, bias generic, ReLU / leaky-ReLU generic).
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the product path may link, load or call
+ * this library: only tests/, __graft_entry__.smoke() (as the checker) and the
+ * cpu_baseline leg of bench.py use it.
+ *
+ * What it restates (reference file:line):
+ *   - linalg.fill 0 then linalg.matmul (cpp/src/builders/LinalgBuilder.cpp:106-139);
+ *   - CPU pipeline (cpp/src/MLIRLowering.cpp:353-434): 64x64 output tiles run
+ *     in parallel (forall -> scf.parallel -> omp.parallel, MLIRLowering.cpp:362-375,
+ *     MLIRLoweringPasses.cpp:470-473); inside a tile, 8x8x8 tiles in m, n, k
+ *     loop order (MLIRLoweringPasses.cpp:270-319, 467-469); a static 8x8x8 tile
+ *     becomes vector.contract (MLIRLoweringPasses.cpp:103-185) -> outer
+ *     products -> vector.fma (MLIRLoweringPasses.cpp:242-260), i.e. per output
+ *     element an ascending-k fused multiply-add chain from +0.0; tiles whose
+ *     shape is dynamic fall to convert-linalg-to-loops (MLIRLowering.cpp:410):
+ *     scalar mulf then addf, each rounded;
+ *   - the bias generic (LinalgBuilder.cpp:301-339) merged with the activation
+ *     generic (LinalgBuilder.cpp:180-239) by linalg-fuse-elementwise-ops
+ *     (MLIRLowering.cpp:355) and run as one separate pass after the matmul:
+ *     y = addf(c, b[n]); relu = maximumf(y, 0); leaky = maximumf(y,0) +
+ *     alpha * minimumf(y,0);
+ *   - i32: arith.muli / arith.addi, two's complement wrapping; ReLU written
+ *     tensor_map(v -> If(v > 0, v, 0)) (LinalgBuilder.cpp:141-178).
+ *
+ * Operands are contiguous row-major: X[M][K], W[K][N], b[N], Y[M][N].
+ * epilogue: bit 0 = add bias; bits 1-2 = activation (0 none, 1 relu, 2 leaky).
+ */
+#ifndef EDSL_ORACLE_H
+#define EDSL_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* 1 when every 8x8x8 block of an MxNxK matmul is a static tile in the
+ * reference CPU lowering (so every element is an fma chain), 0 when the tiles
+ * are dynamic (every element is a mulf+addf chain). */
+int oracle_static_tiles(int64_t M, int64_t N, int64_t K);
+
+/* Returns 0, or -1 on a bad epilogue code. threads <= 0: OpenMP default. */
+int oracle_dense_f32(const float *X, const float *W, const float *b, float *Y, int64_t M,
+                     int64_t N, int64_t K, int epilogue, float alpha, int threads);
+int oracle_dense_i32(const int32_t *X, const int32_t *W, const int32_t *b, int32_t *Y,
+                     int64_t M, int64_t N, int64_t K, int epilogue, int threads);
+
+/* Test hook: plant a known mistake (0 = none) so the tests can show that the
+ * checks pinning this oracle catch it. See oracle.c for the list. */
+void oracle_set_mutation(int mutation);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,349 @@
+"""GPU parity: the HIP path, called through the C ABI, against the pinned
+oracle, the exact golden vectors and the reference's known answers.
+
+Bar: i32 bit-exact; f32 relative Frobenius error <= 1e-5 and
+max|delta| <= 1e-4*sqrt(K) (tests/conftest.py: assert_f32_parity).
+"""
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_f32_parity
+from mlir_edsl_hip import _native, backend
+from mlir_edsl_hip.inputs import WORKLOADS, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+_PATTERN = {"matmul": (False, "none"), "matmul_relu": (False, "relu"),
+            "matmul_bias": (True, "none"), "dense_relu": (True, "relu"),
+            "dense_leaky": (True, "leaky")}
+_EPI_TAG = {"none": "matmul", "bias": "matmul_bias", "relu": "dense_relu", "leaky": "dense_leaky",
+            "relu_nobias": "matmul_relu"}
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    assert torch.cuda.is_available()
+    return torch
+
+
+def to_dev(torch, arrays):
+    return [torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in arrays]
+
+
+def gpu_run(pattern, arrays, alpha=0.01, device=False):
+    if device:
+        import torch
+        out = backend.run(pattern, *to_dev(torch, arrays), alpha=alpha)
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+    return backend.run(pattern, *arrays, alpha=alpha)
+
+
+def oracle_run(pattern, arrays, alpha=0.01):
+    bias, act = _PATTERN[pattern]
+    X, W = arrays[0], arrays[1]
+    b = arrays[2] if bias else None
+    if X.dtype == np.int32:
+        return oracle.dense_i32(X, W, b, act)
+    return oracle.dense_f32(X, W, b, act, alpha)
+
+
+def check(got, ref, K):
+    if ref.dtype == np.int32:
+        assert got.dtype == np.int32
+        assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
+    else:
+        assert_f32_parity(got, ref, K)
+
+
+# ------------------------------------------------------------ known answers
+def _known():
+    with open(os.path.join(GOLDEN, "reference_known_answers.json")) as f:
+        return json.load(f)["cases"]
+
+
+@pytest.mark.parametrize("device", [False, True], ids=["host", "device"])
+@pytest.mark.parametrize("case", _known(), ids=lambda c: c["name"])
+def test_reference_known_answers(case, device, torch_cuda):
+    dt = np.float32 if case["dtype"] == "f32" else np.int32
+    ins = [np.asarray(x, dtype=dt) for x in case["inputs"]]
+    got = gpu_run(case["pattern"], ins, alpha=case["alpha"], device=device)
+    exp = np.asarray(case["expected"], dtype=dt)
+    if dt == np.int32:
+        assert np.array_equal(got, exp)
+    else:
+        np.testing.assert_allclose(got, exp, rtol=case["rtol"], atol=case["atol"])
+
+
+def test_chained_matmul_known_answer(torch_cuda):
+    # reference tests/linalg/test_matmul_execution.py:110-122: (I @ B) @ I == B
+    I = np.eye(2, dtype=np.float32)
+    B = np.array([[1, 2], [3, 4]], np.float32)
+    np.testing.assert_allclose(backend.matmul(backend.matmul(I, B), I), B, rtol=1e-4)
+
+
+# ----------------------------------------------------------- golden vectors
+def _golden_cases():
+    with open(os.path.join(GOLDEN, "dense_golden.json")) as f:
+        meta = json.load(f)["cases"]
+    return [(c, tag) for c in meta for tag in c["epilogues"]]
+
+
+@pytest.fixture(scope="module")
+def golden_data():
+    return np.load(os.path.join(GOLDEN, "dense_golden.npz"), allow_pickle=False)
+
+
+@pytest.mark.parametrize("case,tag", _golden_cases(), ids=lambda v: v["name"] if isinstance(v, dict) else v)
+def test_golden_vectors(case, tag, golden_data, torch_cuda):
+    n = case["name"]
+    X, W, b = golden_data[f"{n}/X"], golden_data[f"{n}/W"], golden_data[f"{n}/b"]
+    pattern = _EPI_TAG[tag]
+    arrays = [X, W, b] if _PATTERN[pattern][0] else [X, W]
+    exp = golden_data[f"{n}/Y_{tag}"]
+    for device in (False, True):
+        got = gpu_run(pattern, arrays, alpha=case.get("alpha", 0.01), device=device)
+        check(got, exp, case["K"])
+
+
+# ------------------------------------------- the reference's GPU test shapes
+@pytest.mark.parametrize("pattern,size", [
+    ("matmul", 8), ("matmul", 16), ("matmul", 48), ("matmul", 64), ("matmul", 96), ("matmul", 128),
+    ("dense_relu", 32), ("dense_relu", 64), ("dense_relu", 96), ("matmul_bias", 64),
+    ("matmul", 256), ("dense_relu", 128)])
+def test_reference_gpu_and_multicore_shapes(pattern, size, torch_cuda):
+    # reference tests/gpu/test_gpu_execution.py:52-210, tests/core/test_multicore.py:19-123
+    rng = np.random.default_rng(1000 + size)
+    arrays = [rng.random((size, size), dtype=np.float32), rng.random((size, size), dtype=np.float32)]
+    if _PATTERN[pattern][0]:
+        arrays.append(rng.random(size, dtype=np.float32))
+    ref = oracle_run(pattern, arrays)
+    for device in (False, True):
+        check(gpu_run(pattern, arrays, device=device), ref, size)
+
+
+# ------------------------------------------------------- BASELINE workloads
+def test_c1_matmul_256(torch_cuda):
+    w = WORKLOADS["c1"]
+    A, B = make_inputs(w)
+    check(gpu_run("matmul", [A, B], device=True), oracle.dense_f32(A, B), w.K)
+
+
+def test_c2_dense_1024(torch_cuda):
+    w = WORKLOADS["c2"]
+    X, W, b = make_inputs(w)
+    ref = oracle.dense_f32(X, W, b, "relu")
+    check(gpu_run("dense_relu", [X, W, b], device=True), ref, w.K)
+    check(gpu_run("dense_relu", [X, W, b], device=False), ref, w.K)
+
+
+def test_c3_dense_4096_sampled_rows(torch_cuda):
+    w = WORKLOADS["c3"]
+    X, W, b = make_inputs(w)
+    got = gpu_run("dense_relu", [X, W, b], device=True)
+    assert _native.last_plan().startswith("gemm_f32")
+    rows = np.sort(np.random.default_rng(0).choice(w.M, 256, replace=False))
+    ref = oracle.dense_f32(X[rows], W, b, "relu")
+    check(got[rows], ref, w.K)
+    # size-independent property over the full output: ReLU output is >= 0 or NaN-free
+    assert np.all(got >= 0) and np.isfinite(got).all()
+
+
+def test_c4_dense_small_m(torch_cuda):
+    w = WORKLOADS["c4"]
+    X, W, b = make_inputs(w)
+    ref = oracle.dense_f32(X, W, b, "relu")
+    for _ in range(2):  # the split-K counters must re-arm between calls
+        got = gpu_run("dense_relu", [X, W, b], device=True)
+        assert _native.last_plan().startswith("gemv_f32")
+        check(got, ref, w.K)
+
+
+def test_c5_int_dense_bit_exact(torch_cuda):
+    w = WORKLOADS["c5"]
+    X, W, b = make_inputs(w)
+    got = gpu_run("dense_relu", [X, W, b], device=True)
+    assert _native.last_plan().startswith("narrow_i8+gemm_i8")
+    exact = X.astype(np.float64) @ W.astype(np.float64) + b  # |sum| < 2^53: exact
+    exp = np.maximum(exact, 0).astype(np.int32)
+    assert np.array_equal(got, exp)
+    rows = np.arange(0, w.M, 37)
+    assert np.array_equal(got[rows], oracle.dense_i32(X[rows], W, b, "relu"))
+
+
+# ------------------------------------------------------------ integer path
+def test_int8_path_falls_back_when_values_leave_int8(torch_cuda):
+    rng = np.random.default_rng(9)
+    n = 256
+    X = rng.integers(-2**31, 2**31, size=(n, n), dtype=np.int64).astype(np.int32)
+    W = rng.integers(-2**31, 2**31, size=(n, n), dtype=np.int64).astype(np.int32)
+    b = rng.integers(-2**31, 2**31, size=(n,), dtype=np.int64).astype(np.int32)
+    with np.errstate(over="ignore"):
+        exp = (X.astype(np.int64) @ W.astype(np.int64) + b).astype(np.int32)
+    got = gpu_run("matmul_bias", [X, W, b], device=True)
+    assert np.array_equal(got, exp)
+    # one value out of range among int8 ones
+    X2 = rng.integers(-128, 128, size=(n, n), dtype=np.int32)
+    W2 = rng.integers(-128, 128, size=(n, n), dtype=np.int32)
+    W2[17, 201] = 300
+    exp2 = (X2.astype(np.int64) @ W2.astype(np.int64) + b.astype(np.int64) + 2**31) % 2**32 - 2**31
+    got2 = gpu_run("dense_relu", [X2, W2, b], device=True)
+    assert np.array_equal(got2, np.maximum(exp2, 0).astype(np.int32))
+    # the next in-range call takes the int8 path again and is still exact
+    W2[17, 201] = 5
+    got3 = gpu_run("matmul", [X2, W2], device=True)
+    assert np.array_equal(got3, (X2.astype(np.int64) @ W2.astype(np.int64)).astype(np.int32))
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (3, 5, 7), (65, 33, 17), (130, 128, 128), (128, 256, 384)])
+def test_int_shapes(shape, torch_cuda):
+    M, K, N = shape
+    rng = np.random.default_rng(M * 7 + K)
+    X = rng.integers(-100, 100, size=(M, K), dtype=np.int32)
+    W = rng.integers(-100, 100, size=(K, N), dtype=np.int32)
+    b = rng.integers(-1000, 1000, size=(N,), dtype=np.int32)
+    for pattern in ("matmul", "matmul_relu", "matmul_bias", "dense_relu"):
+        arrays = [X, W, b] if _PATTERN[pattern][0] else [X, W]
+        check(gpu_run(pattern, arrays, device=True), oracle_run(pattern, arrays), K)
+
+
+# ------------------------------------------------------ shapes and layouts
+@pytest.mark.parametrize("shape", [(1, 1, 1), (3, 5, 7), (65, 33, 17), (100, 200, 300),
+                                   (257, 129, 511), (64, 4, 64)])
+def test_f32_odd_shapes(shape, torch_cuda):
+    M, K, N = shape
+    rng = np.random.default_rng(M + 3 * K + 7 * N)
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    W = rng.standard_normal((K, N), dtype=np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    for pattern in ("matmul", "dense_relu", "dense_leaky"):
+        arrays = [X, W, b] if _PATTERN[pattern][0] else [X, W]
+        check(gpu_run(pattern, arrays, alpha=0.2), oracle_run(pattern, arrays, alpha=0.2), K)
+
+
+def test_k_zero_gives_activation_of_bias(torch_cuda):
+    X = np.zeros((4, 0), np.float32)
+    W = np.zeros((0, 8), np.float32)
+    b = np.linspace(-1, 1, 8, dtype=np.float32)
+    got = gpu_run("dense_relu", [X, W, b])
+    assert np.array_equal(got, np.tile(np.maximum(b, 0), (4, 1)))
+    gi = gpu_run("matmul_bias", [X.astype(np.int32), W.astype(np.int32), np.arange(8, dtype=np.int32)])
+    assert np.array_equal(gi, np.tile(np.arange(8, dtype=np.int32), (4, 1)))
+
+
+def test_empty_output(torch_cuda):
+    got = gpu_run("matmul", [np.zeros((0, 5), np.float32), np.zeros((5, 3), np.float32)])
+    assert got.shape == (0, 3)
+
+
+def test_strided_and_misaligned_device_operands(torch_cuda):
+    torch = torch_cuda
+    rng = np.random.default_rng(11)
+    M, K, N = 192, 256, 320
+    big_x = rng.standard_normal((M, K + 9), dtype=np.float32)
+    big_w = rng.standard_normal((K, N + 3), dtype=np.float32)
+    b = rng.standard_normal(N + 1, dtype=np.float32)
+    tx, tw, tb = to_dev(torch, [big_x, big_w, b])
+    X, W, bias = tx[:, 1:K + 1], tw[:, :N], tb[1:]        # row stride > cols, offset 1
+    Y = torch.empty((M, N + 5), device="cuda")[:, 2:N + 2]  # strided, misaligned output
+    from mlir_edsl_hip.device import dense_launch
+    dense_launch(X, W, bias, Y, _native.EPI_BIAS_RELU)
+    torch.cuda.synchronize()
+    ref = oracle.dense_f32(big_x[:, 1:K + 1], big_w[:, :N], b[1:], "relu")
+    check(Y.cpu().numpy(), ref, K)
+    # aligned views with a padded row stride keep the fast path
+    X2, W2 = tx[:, :K], tw[:, :N - 64]
+    Y2 = torch.empty((M, N - 64 + 4), device="cuda")[:, :N - 64]
+    dense_launch(X2, W2, None, Y2, _native.EPI_NONE)
+    torch.cuda.synchronize()
+    check(Y2.cpu().numpy(), oracle.dense_f32(big_x[:, :K], big_w[:, :N - 64]), K)
+
+
+def test_memref_offset_is_honoured(torch_cuda):
+    """aligned + offset addressing of the descriptor (host operands)."""
+    rng = np.random.default_rng(12)
+    A = rng.standard_normal(8 * 8 + 3, dtype=np.float32)
+    B = rng.standard_normal((8, 8), dtype=np.float32)
+    C = np.zeros((8, 8), np.float32)
+    L = _native.lib()
+    L.edsl_hip_matmul_f32(A.ctypes.data, A.ctypes.data, 3, 8, 8, 8, 1,
+                          B.ctypes.data, B.ctypes.data, 0, 8, 8, 8, 1,
+                          C.ctypes.data, C.ctypes.data, 0, 8, 8, 8, 1)
+    _native.raise_on_error("matmul")
+    check(C, oracle.dense_f32(A[3:].reshape(8, 8), B), 8)
+
+
+@pytest.mark.parametrize("M", [1, 2, 16, 17, 31, 48, 64])
+@pytest.mark.parametrize("ksplit", [1, 2, 4, 8])
+def test_small_m_kernel(M, ksplit, torch_cuda):
+    from mlir_edsl_hip.device import set_gemv_ksplit
+    rng = np.random.default_rng(M * 10 + ksplit)
+    K, N = 1024, 512
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.float32(32)).astype(np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    set_gemv_ksplit(ksplit)
+    try:
+        for _ in range(2):
+            got = gpu_run("dense_relu", [X, W, b], device=True)
+            assert _native.last_plan().startswith(f"gemv_f32 mb={(M + 15) // 16} ksplit={ksplit}")
+            check(got, oracle.dense_f32(X, W, b, "relu"), K)
+    finally:
+        set_gemv_ksplit(0)
+
+
+def test_every_f32_tile_config(torch_cuda):
+    from mlir_edsl_hip.device import set_f32_config
+    rng = np.random.default_rng(13)
+    M, K, N = 512, 256, 512
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    W = rng.standard_normal((K, N), dtype=np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    ref = oracle.dense_f32(X, W, b, "relu")
+    names = _native.f32_config_names()
+    try:
+        for cfg, name in enumerate(names):
+            if "guard" in name:
+                continue
+            set_f32_config(cfg)
+            got = gpu_run("dense_relu", [X, W, b], device=True)
+            assert name in _native.last_plan()
+            check(got, ref, K)
+    finally:
+        set_f32_config(-1)
+
+
+def test_nan_and_inf_propagate_like_maximumf(torch_cuda):
+    rng = np.random.default_rng(14)
+    M, K, N = 128, 128, 128
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    W = rng.standard_normal((K, N), dtype=np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    X[3, 5] = np.nan
+    b[7] = np.inf
+    b[9] = -np.inf
+    for pattern in ("dense_relu", "dense_leaky", "matmul_bias"):
+        ref = oracle_run(pattern, [X, W, b], alpha=0.1)
+        got = gpu_run(pattern, [X, W, b], alpha=0.1, device=True)
+        assert np.isnan(got[3]).all()  # fmaxf semantics would give 0 after ReLU
+        check(got, ref, K)
+
+
+def test_execute_gpu_function_host_entry(torch_cuda):
+    be = backend.get_backend()
+    w = WORKLOADS["c2"]
+    X, W, b = make_inputs(w, M=256, K=512, N=384)
+    be.compile_dense("dense_host_entry", "dense_relu",
+                     [backend.tensor_type_of(a) for a in (X, W, b)])
+    got = be.execute_gpu_function("dense_host_entry", X, W, b)
+    check(got, oracle.dense_f32(X, W, b, "relu"), 512)
+    with pytest.raises(TypeError):
+        be.execute_gpu_function("dense_host_entry", X.astype(np.float64), W, b)

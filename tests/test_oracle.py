@@ -1,0 +1,223 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is compared with it.
+
+Checks, each chosen so that a plausible mistake in the oracle fails one:
+  * the reference's own known answers (tests/golden/reference_known_answers.json);
+  * golden vectors from exact rational arithmetic (tests/golden/make_golden.py):
+    the fp32 fma chain / mulf+addf chain and the wrapping i32 sums, bit for bit;
+  * the fp64 forward-error bound |fl(x.w) - x.w| <= gamma_K * sum|x||w| at
+    sizes too large for rational arithmetic;
+  * exact wrapping i32 arithmetic via int64 products at larger sizes;
+  * IEEE special values through the ReLU / leaky epilogue (NaN propagates);
+  * planted mistakes (oracle.mutation) are each caught by the checks above.
+"""
+from __future__ import annotations
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _known_answers():
+    with open(os.path.join(GOLDEN, "reference_known_answers.json")) as f:
+        return json.load(f)["cases"]
+
+
+def _golden():
+    with open(os.path.join(GOLDEN, "dense_golden.json")) as f:
+        meta = json.load(f)["cases"]
+    data = np.load(os.path.join(GOLDEN, "dense_golden.npz"), allow_pickle=False)
+    return meta, data
+
+
+_EPI = {"none": (False, "none"), "bias": (True, "none"), "relu": (True, "relu"),
+        "leaky": (True, "leaky"), "relu_nobias": (False, "relu")}
+_PATTERN = {"matmul": (False, "none"), "matmul_relu": (False, "relu"),
+            "matmul_bias": (True, "none"), "dense_relu": (True, "relu"),
+            "dense_leaky": (True, "leaky")}
+
+
+def run_oracle(dtype, X, W, b, act, alpha=0.01):
+    if dtype == "f32":
+        return oracle.dense_f32(X, W, b, act, alpha)
+    return oracle.dense_i32(X, W, b, act)
+
+
+# ------------------------------------------------------------ the checks
+def check_known_answers():
+    failures = []
+    for c in _known_answers():
+        dt = np.float32 if c["dtype"] == "f32" else np.int32
+        ins = [np.asarray(x, dtype=dt) for x in c["inputs"]]
+        bias, act = _PATTERN[c["pattern"]]
+        got = run_oracle(c["dtype"], ins[0], ins[1], ins[2] if bias else None, act, c["alpha"])
+        exp = np.asarray(c["expected"], dtype=dt)
+        if c["dtype"] == "i32":
+            ok = np.array_equal(got, exp)
+        else:
+            ok = np.allclose(got, exp, rtol=c["rtol"], atol=c["atol"])
+        if not ok:
+            failures.append(f"known answer {c['name']} ({c['source']})")
+    return failures
+
+
+def check_golden():
+    meta, data = _golden()
+    failures = []
+    for c in meta:
+        n = c["name"]
+        X, W, b = data[f"{n}/X"], data[f"{n}/W"], data[f"{n}/b"]
+        for tag in c["epilogues"]:
+            use_b, act = _EPI[tag]
+            got = run_oracle(c["dtype"], X, W, b if use_b else None, act, c.get("alpha", 0.01))
+            exp = data[f"{n}/Y_{tag}"]
+            if got.dtype == np.float32:
+                same = np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+            else:
+                same = np.array_equal(got, exp)
+            if not same:
+                failures.append(f"golden {n}/{tag}")
+    return failures
+
+
+def check_special_values():
+    """bias injects NaN / inf / signed values into the epilogue directly."""
+    failures = []
+    vals = np.array([np.nan, -np.inf, np.inf, -1.0, 2.0, -0.0, 0.5, -3.0], dtype=np.float32)
+    N = vals.size
+    X = np.zeros((1, 8), np.float32)
+    W = np.zeros((8, N), np.float32)
+    y = oracle.dense_f32(X, W, vals, "relu")[0]
+    exp = np.array([np.nan, 0, np.inf, 0, 2, 0, 0.5, 0], np.float32)
+    if not (np.isnan(y[0]) and np.array_equal(y[1:], exp[1:]) and not np.signbit(y[5])):
+        failures.append(f"relu special values {y}")
+    yl = oracle.dense_f32(X, W, vals, "leaky", alpha=0.25)[0]
+    expl = np.array([np.nan, -np.inf, np.inf, -0.25, 2, 0, 0.5, -0.75], np.float32)
+    if not (np.isnan(yl[0]) and np.array_equal(yl[1:], expl[1:])):
+        failures.append(f"leaky special values {yl}")
+    return failures
+
+
+def check_i32_wrap():
+    rng = np.random.default_rng(5)
+    failures = []
+    for (M, K, N) in [(64, 96, 80), (7, 33, 5)]:
+        X = rng.integers(-2**31, 2**31, size=(M, K), dtype=np.int64).astype(np.int32)
+        W = rng.integers(-2**31, 2**31, size=(K, N), dtype=np.int64).astype(np.int32)
+        b = rng.integers(-2**31, 2**31, size=(N,), dtype=np.int64).astype(np.int32)
+        # int64 products / sums wrap modulo 2^64; reducing to 32 bits is exact.
+        with np.errstate(over="ignore"):
+            exp = (X.astype(np.int64) @ W.astype(np.int64) + b.astype(np.int64)).astype(np.int32)
+        got = oracle.dense_i32(X, W, b, "none")
+        if not np.array_equal(got, exp):
+            failures.append(f"i32 wrap {M}x{K}x{N}")
+        got_r = oracle.dense_i32(X, W, b, "relu")
+        if not np.array_equal(got_r, np.maximum(exp, 0)):
+            failures.append(f"i32 wrap relu {M}x{K}x{N}")
+    return failures
+
+
+def check_fp64_bound():
+    """|fl - exact| <= gamma_K * (sum|x||w|) elementwise (+ one rounding for
+    the bias add), at shapes on both the fma and the mulf+addf paths."""
+    rng = np.random.default_rng(6)
+    failures = []
+    u = 2.0 ** -24
+    for (M, K, N) in [(128, 128, 64), (96, 96, 96), (64, 256, 192), (40, 100, 30)]:
+        X = rng.standard_normal((M, K), dtype=np.float32)
+        W = rng.standard_normal((K, N), dtype=np.float32)
+        b = rng.standard_normal(N, dtype=np.float32)
+        got = oracle.dense_f32(X, W, b, "none").astype(np.float64)
+        x64, w64 = X.astype(np.float64), W.astype(np.float64)
+        exact = x64 @ w64 + b.astype(np.float64)
+        gamma = K * u / (1 - K * u)
+        bound = gamma * (np.abs(x64) @ np.abs(w64)) + u * (np.abs(exact) + np.abs(b)) + 1e-30
+        if not np.all(np.abs(got - exact) <= bound * 1.0001):
+            failures.append(f"fp64 bound {M}x{K}x{N}")
+    return failures
+
+
+ALL_CHECKS = [check_known_answers, check_golden, check_special_values, check_i32_wrap,
+              check_fp64_bound]
+
+
+def all_failures():
+    out = []
+    for chk in ALL_CHECKS:
+        out += chk()
+    return out
+
+
+# ------------------------------------------------------------- the tests
+@pytest.mark.parametrize("chk", ALL_CHECKS, ids=lambda f: f.__name__)
+def test_oracle_pinned(chk):
+    assert chk() == []
+
+
+def test_static_tile_rule():
+    # Static 8x8x8 tiles (fma chain): dims divisible by 8 and either <= 64 or
+    # divisible by 64 -- every BASELINE shape is on this path.
+    for shape in [(256, 256, 256), (1024, 1024, 1024), (4096, 4096, 4096), (16, 8192, 8192),
+                  (2048, 2048, 2048), (8, 8, 8), (48, 48, 48), (64, 128, 64)]:
+        M, K, N = shape
+        assert oracle.static_tiles(M, N, K), shape
+    # Dynamic tiles (mulf+addf chain): a partial 64-tile or a non-multiple of 8.
+    for shape in [(96, 96, 96), (2, 2, 2), (16, 12, 16), (100, 64, 64), (64, 64, 72)]:
+        M, K, N = shape
+        assert not oracle.static_tiles(M, N, K), shape
+
+
+def test_golden_paths_cover_both_chains():
+    meta, _ = _golden()
+    paths = {c["fma_path"] for c in meta if c["dtype"] == "f32"}
+    assert paths == {True, False}
+
+
+def test_fma_and_muladd_chains_differ_somewhere():
+    """The two rounding paths are distinguishable on the golden inputs, so the
+    golden check really pins which one the oracle takes."""
+    import exact
+    _, data = _golden()
+    X, W = data["f32_32x32x32/X"], data["f32_32x32x32/W"]
+    a = exact.dense_f32_exact(X[:4], W, None, "none", 0.0, fma_path=True)
+    b = exact.dense_f32_exact(X[:4], W, None, "none", 0.0, fma_path=False)
+    assert not np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("mutation", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_planted_mistake_is_caught(mutation):
+    assert all_failures() == []
+    with oracle.mutation(mutation):
+        caught = all_failures()
+    assert caught, f"planted mistake {mutation} went unnoticed"
+    assert all_failures() == []
+
+
+def test_threads_do_not_change_results():
+    rng = np.random.default_rng(7)
+    X = rng.standard_normal((192, 128), dtype=np.float32)
+    W = rng.standard_normal((128, 256), dtype=np.float32)
+    b = rng.standard_normal(256, dtype=np.float32)
+    y1 = oracle.dense_f32(X, W, b, "relu", threads=1)
+    y4 = oracle.dense_f32(X, W, b, "relu", threads=4)
+    assert np.array_equal(y1.view(np.uint32), y4.view(np.uint32))
+
+
+def test_rows_are_independent():
+    """A row subset gives the same bits as the full product (the GPU parity
+    tests rely on this to check large shapes on sampled rows)."""
+    rng = np.random.default_rng(8)
+    X = rng.standard_normal((256, 128), dtype=np.float32)
+    W = rng.standard_normal((128, 128), dtype=np.float32)
+    b = rng.standard_normal(128, dtype=np.float32)
+    full = oracle.dense_f32(X, W, b, "relu")
+    rows = np.array([0, 5, 64, 200, 255])
+    part = oracle.dense_f32(X[np.concatenate([rows, np.arange(64 - rows.size) + 1])], W, b, "relu")
+    assert np.array_equal(full[rows].view(np.uint32), part[:rows.size].view(np.uint32))
+    assert math.isfinite(float(full.sum()))
