@@ -172,8 +172,13 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--secondary", default="c4,c5,c2,c1",
+                    help="comma-separated secondary workloads to measure after c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device-to-device copy of BYTES (3 times) and exit; "
+                         "its FETCH_SIZE / WRITE_SIZE counters calibrate the traffic figures")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -186,6 +191,15 @@ def main() -> int:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        n = args.copy_calibration // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copied {n * 4} bytes x3")
+        return 0
     from mlir_edsl_hip.inputs import WORKLOADS
 
     traffic = load_traffic()
@@ -196,7 +210,9 @@ def main() -> int:
 
     secondary = []
     if not args.no_secondary:
-        for wname, steps, rot in (("c4", 200, 3), ("c5", 100, 1), ("c2", 100, 1), ("c1", 200, 1)):
+        plan = {"c4": (200, 3), "c5": (100, 1), "c2": (100, 1), "c1": (200, 1)}
+        for wname in [w.strip() for w in args.secondary.split(",") if w.strip()]:
+            steps, rot = plan[wname]
             log(f"[bench] {wname} {WORKLOADS[wname].description}")
             r = measure(wname, steps, 20, rotate=rot)
             wl = WORKLOADS[wname]

@@ -51,11 +51,15 @@ int edsl_hip_dense_i32_launch(const int32_t *X, int64_t ldx, const int32_t *W, i
 int edsl_hip_last_plan(char *buf, size_t len);
 
 /* Tuning overrides: force an f32 tile configuration (index into the table
- * reported by edsl_hip_f32_config_name; -1 = automatic) and the small-M
- * split-K factor (0 = automatic). Calls that cannot use the forced choice
- * fall back to the automatic one. */
+ * reported by edsl_hip_f32_config_name; -1 = automatic), the small-M
+ * split-K factor (0 = automatic, at most 16) and the int8 GEMM variant.
+ * Calls that cannot use the forced choice fall back to the automatic one. */
 void edsl_hip_set_f32_config(int cfg);
 void edsl_hip_set_gemv_ksplit(int ksplit);
+/* int8 GEMM pipeline variant (waves per workgroup x stages in flight), index
+ * < edsl_hip_i8_variant_count(); -1 = automatic. */
+void edsl_hip_set_i8_variant(int variant);
+int edsl_hip_i8_variant_count(void);
 int edsl_hip_f32_config_count(void);
 int edsl_hip_f32_config_name(int cfg, char *buf, size_t len);
 

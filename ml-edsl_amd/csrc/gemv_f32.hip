@@ -5,22 +5,29 @@
 // 301-339), shaped for the HBM-bound case where W dominates the traffic
 // (M=16, K=N=8192: W is 256 MiB, X and Y 512 KiB each).
 //
-// Every W element is read from HBM exactly once, with 16-byte coalesced loads,
-// and used for all M rows at once on the matrix cores:
+// Every W element is read from HBM exactly once, with 16-byte loads, and used
+// for all M rows at once on the matrix cores:
 //  * v_mfma_f32_16x16x4_f32: lane l supplies X[row l%16][k-slot l/16] and
 //    W[k-slot l/16][col l%16]. Lane group g = l/16 owns the k rows
 //    k0+4g .. k0+4g+3 of each 16-row step: it loads those 4 k of its X row with
 //    one 16-byte load and, for each k, 4 consecutive W columns with one 16-byte
-//    load. MFMA (step s, column phase c) then pairs X[.][k0+4g+s] with
+//    load. MFMA (step s, column phase c) pairs X[.][k0+4g+s] with
 //    W[k0+4g+s][n0 + 4*(l%16) + c], so lane l%16 accumulates columns
-//    n0 + 4*(l%16) + c: a wave covers 64 columns and stores float4 per row.
-//  * A workgroup is 4 waves on one 64-column group; the waves split the
-//    workgroup's K range and are summed in LDS in a fixed order.
-//  * K is additionally split over `ksplit` workgroups so that the grid fills
-//    the chip. Each writes its partial tile; the last one to arrive (device
-//    atomic counter) sums the partials in split order, applies bias and
-//    activation, stores Y, and re-arms the counter. The result is therefore
-//    independent of which workgroup finishes last.
+//    n0 + 4*(l%16) + c: a wave owns 64 columns and stores float4 per row.
+//  * A workgroup is 16 waves: WN waves side by side cover 64*WN adjacent
+//    columns (so a row is read in 64*WN*4-byte runs), and WK = 16/WN waves
+//    split the workgroup's K range. The WK slices are summed in LDS, in wave
+//    order.
+//  * K is further split over `ksplit` workgroups so that the grid fills the
+//    256 CUs. Each writes its partial tile; a second small kernel sums the
+//    partials in split order and applies bias and activation. (An in-kernel
+//    "last workgroup reduces" scheme needs device-scope fences, which on this
+//    part write back and invalidate L2 and cost more than the extra launch.)
+//  * Each wave starts its K walk at a hashed offset (wrapping), so the rows
+//    in flight at any moment are spread over the matrix and over the HBM
+//    channels instead of every wave hitting the same few rows.
+// The summation order is fixed by the shape and the configuration, so
+// results are deterministic.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -29,21 +36,37 @@
 namespace edsl {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kCols = 64;  // columns per workgroup
+constexpr int kWavesPerWG = 16;
 
-template <int MB, int EPI>
-__global__ void __launch_bounds__(kWaves * 64)
-gemv_f32_kernel(GemvF32Args a) {
+__device__ __forceinline__ float epilogue_rt(float acc, float b, float alpha, int epi) {
+  switch (epi) {
+    case epi_code(false, ACT_NONE): return apply_epilogue_f32<epi_code(false, ACT_NONE)>(acc, b, alpha);
+    case epi_code(true, ACT_NONE): return apply_epilogue_f32<epi_code(true, ACT_NONE)>(acc, b, alpha);
+    case epi_code(false, ACT_RELU): return apply_epilogue_f32<epi_code(false, ACT_RELU)>(acc, b, alpha);
+    case epi_code(true, ACT_RELU): return apply_epilogue_f32<epi_code(true, ACT_RELU)>(acc, b, alpha);
+    case epi_code(false, ACT_LEAKY): return apply_epilogue_f32<epi_code(false, ACT_LEAKY)>(acc, b, alpha);
+    default: return apply_epilogue_f32<epi_code(true, ACT_LEAKY)>(acc, b, alpha);
+  }
+}
+
+template <int MB, int WN>
+__global__ void __launch_bounds__(kWavesPerWG * 64)
+gemv_f32_kernel(GemvF32Args a, int epi) {
+  constexpr int WK = kWavesPerWG / WN;
+  // 16-row steps per loop iteration: 8 W loads in flight per lane, fewer when
+  // the accumulators of 3-4 row blocks need the registers.
+  constexpr int kU = MB <= 2 ? 2 : 1;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int groups = a.N / kCols;
+  const int wn = wave % WN;
+  const int wk = wave / WN;
+  const int groups = a.N / (64 * WN);
   const int g = blockIdx.x % groups;
   const int split = blockIdx.x / groups;
-  const int n0 = g * kCols;
+  const int n0 = g * 64 * WN + 64 * wn;
   const int kspan = a.K / a.ksplit;
-  const int kwave = kspan / kWaves;  // multiple of 16
-  const int kbeg = split * kspan + wave * kwave;
+  const int kwave = kspan / WK;  // multiple of 16
+  const int kbeg = split * kspan + wk * kwave;
   const int li = lane & 15;
   const int lg = lane >> 4;
 
@@ -53,7 +76,8 @@ gemv_f32_kernel(GemvF32Args a) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[mb][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const float* wp = a.W + (int64_t)(kbeg + 4 * lg) * a.ldw + n0 + 4 * li;
+  const int64_t ldw = a.ldw;
+  const float* wbase = a.W + (int64_t)(kbeg + 4 * lg) * ldw + n0 + 4 * li;
   const float* xp[MB];
   bool xrow[MB];
 #pragma unroll
@@ -62,12 +86,11 @@ gemv_f32_kernel(GemvF32Args a) {
     xrow[mb] = row < a.M;
     xp[mb] = a.X + (int64_t)(xrow[mb] ? row : 0) * a.ldx + kbeg + 4 * lg;
   }
-  const int64_t ldw = a.ldw;
 
-  // U steps of 16 rows per iteration: all U*4 W loads are issued before the
-  // first MFMA that needs them, keeping U KiB per wave in flight.
+  // U steps of 16 rows starting at row k of this wave's slice.
   auto steps = [&](auto u_tag, int k) {
     constexpr int U = decltype(u_tag)::value;
+    const float* wp = wbase + (int64_t)k * ldw;
     f32x4 w[U][4];
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -93,36 +116,48 @@ gemv_f32_kernel(GemvF32Args a) {
           for (int c = 0; c < 4; ++c)
             acc[mb][c] =
                 __builtin_amdgcn_mfma_f32_16x16x4f32(x[u][mb][s], w[u][s][c], acc[mb][c], 0, 0, 0);
-    wp += (int64_t)16 * U * ldw;
   };
 
-  int k = 0;
-  for (; k + 64 <= kwave; k += 64) steps(std::integral_constant<int, 4>{}, k);
-  for (; k < kwave; k += 16) steps(std::integral_constant<int, 1>{}, k);
-
-  // Sum the 4 waves' K slices in wave order.
-  __shared__ f32x4 red[kWaves - 1][MB * 4][64];
-  if (wave > 0) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) red[wave - 1][mb * 4 + c][lane] = acc[mb][c];
+  // Main iterations of kU steps, walked from a hashed start; then any
+  // remaining single steps (kwave not a multiple of 16*kU).
+  const int nit = kwave / (16 * kU);
+  if (nit > 0) {
+    const int r0 = (int)(((unsigned)blockIdx.x * 2654435761u >> 8) + (unsigned)wave * 977u) % nit;
+    for (int i = 0; i < nit; ++i) {
+      int it = i + r0;
+      if (it >= nit) it -= nit;
+      steps(std::integral_constant<int, kU>{}, it * 16 * kU);
+    }
   }
-  __syncthreads();
-  if (wave != 0) return;
+  for (int k = nit * 16 * kU; k < kwave; k += 16) steps(std::integral_constant<int, 1>{}, k);
+
+  // Sum the WK K-slices of each column block in wave order, one row block at
+  // a time to bound LDS.
+  __shared__ f32x4 red[WK > 1 ? WK - 1 : 1][WN][4][64];
+  if constexpr (WK > 1) {
 #pragma unroll
-  for (int w = 0; w < kWaves - 1; ++w)
+    for (int mb = 0; mb < MB; ++mb) {
+      if (wk > 0) {
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+        for (int c = 0; c < 4; ++c) red[wk - 1][wn][c][lane] = acc[mb][c];
+      }
+      __syncthreads();
+      if (wk == 0) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[mb][c] += red[w][mb * 4 + c][lane];
+        for (int w = 0; w < WK - 1; ++w)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc[mb][c] += red[w][wn][c][lane];
+      }
+      __syncthreads();
+    }
+    if (wk != 0) return;
+  }
 
   // Lane holds rows 16*mb + 4*lg + r and columns n0 + 4*li + c.
   const int col = n0 + 4 * li;
-  f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
-  if constexpr (epi_has_bias(EPI)) bv = *reinterpret_cast<const f32x4*>(a.bias + col);
-
   if (a.ksplit == 1) {
+    f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (epi_has_bias(epi)) bv = *reinterpret_cast<const f32x4*>(a.bias + col);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -131,82 +166,86 @@ gemv_f32_kernel(GemvF32Args a) {
         if (row < a.M) {
           f32x4 y;
 #pragma unroll
-          for (int c = 0; c < 4; ++c) y[c] = apply_epilogue_f32<EPI>(acc[mb][c][r], bv[c], a.alpha);
+          for (int c = 0; c < 4; ++c) y[c] = epilogue_rt(acc[mb][c][r], bv[c], a.alpha, epi);
           *reinterpret_cast<f32x4*>(a.Y + (int64_t)row * a.ldy + col) = y;
         }
       }
     return;
   }
-
-  // Split-K: publish this slice, then let the last arriving workgroup reduce.
   const int prow = 16 * MB;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * mb + 4 * lg + r;
-      f32x4 p = {acc[mb][0][r], acc[mb][1][r], acc[mb][2][r], acc[mb][3][r]};
-      *reinterpret_cast<f32x4*>(a.partials + ((int64_t)split * prow + row) * a.N + col) = p;
-    }
-  __threadfence();
-  unsigned prev = 0;
-  if (lane == 0) prev = atomicAdd(&a.counters[g], 1u);
-  prev = __shfl(prev, 0);
-  if (prev != (unsigned)(a.ksplit - 1)) return;
-  __threadfence();
-
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * mb + 4 * lg + r;
-      f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int sp = 0; sp < a.ksplit; ++sp)
-        s += __builtin_nontemporal_load(
-            reinterpret_cast<const f32x4*>(a.partials + ((int64_t)sp * prow + row) * a.N + col));
       if (row < a.M) {
-        f32x4 y;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) y[c] = apply_epilogue_f32<EPI>(s[c], bv[c], a.alpha);
-        *reinterpret_cast<f32x4*>(a.Y + (int64_t)row * a.ldy + col) = y;
+        f32x4 p = {acc[mb][0][r], acc[mb][1][r], acc[mb][2][r], acc[mb][3][r]};
+        *reinterpret_cast<f32x4*>(a.partials + ((int64_t)split * prow + row) * a.N + col) = p;
       }
     }
-  if (lane == 0) atomicExch(&a.counters[g], 0u);
+}
+
+// Y[m, 4j..4j+3] = epilogue(sum over splits s = 0..ksplit-1, in order).
+// All split loads are issued before the first add so their latencies overlap.
+constexpr int kMaxSplit = 16;
+
+__global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi, int prow) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over M * N/4
+  const int n4 = a.N / 4;
+  if (idx >= (int64_t)a.M * n4) return;
+  const int row = (int)(idx / n4);
+  const int col = 4 * (int)(idx % n4);
+  f32x4 v[kMaxSplit];
+#pragma unroll
+  for (int sp = 0; sp < kMaxSplit; ++sp)
+    if (sp < a.ksplit)
+      v[sp] = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4*>(a.partials + ((int64_t)sp * prow + row) * a.N + col));
+  f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (epi_has_bias(epi)) bv = *reinterpret_cast<const f32x4*>(a.bias + col);
+  f32x4 s = v[0];
+#pragma unroll
+  for (int sp = 1; sp < kMaxSplit; ++sp)
+    if (sp < a.ksplit) s += v[sp];
+  f32x4 y;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) y[c] = epilogue_rt(s[c], bv[c], a.alpha, epi);
+  *reinterpret_cast<f32x4*>(a.Y + (int64_t)row * a.ldy + col) = y;
 }
 
 template <int MB>
-hipError_t launch_mb(int epi, const GemvF32Args& a, hipStream_t stream) {
-  const dim3 grid((a.N / kCols) * a.ksplit);
-  const dim3 block(kWaves * 64);
-#define EDSL_GEMV_CASE(E)                                                                \
-  case E:                                                                                \
-    hipLaunchKernelGGL((gemv_f32_kernel<MB, E>), grid, block, 0, stream, a);            \
-    break;
-  switch (epi) {
-    EDSL_GEMV_CASE(epi_code(false, ACT_NONE))
-    EDSL_GEMV_CASE(epi_code(true, ACT_NONE))
-    EDSL_GEMV_CASE(epi_code(false, ACT_RELU))
-    EDSL_GEMV_CASE(epi_code(true, ACT_RELU))
-    EDSL_GEMV_CASE(epi_code(false, ACT_LEAKY))
-    EDSL_GEMV_CASE(epi_code(true, ACT_LEAKY))
-    default:
-      return hipErrorInvalidValue;
+hipError_t launch_mb(int wn, int epi, const GemvF32Args& a, hipStream_t stream) {
+  const dim3 grid((a.N / (64 * wn)) * a.ksplit);
+  const dim3 block(kWavesPerWG * 64);
+  switch (wn) {
+    case 1: hipLaunchKernelGGL((gemv_f32_kernel<MB, 1>), grid, block, 0, stream, a, epi); break;
+    case 2: hipLaunchKernelGGL((gemv_f32_kernel<MB, 2>), grid, block, 0, stream, a, epi); break;
+    case 4: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4>), grid, block, 0, stream, a, epi); break;
+    default: return hipErrorInvalidValue;
   }
-#undef EDSL_GEMV_CASE
   return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_gemv_f32(int epi, GemvF32Args a, hipStream_t stream) {
+int gemv_f32_waves_k(int wn) { return kWavesPerWG / wn; }
+int gemv_f32_max_ksplit() { return kMaxSplit; }
+
+hipError_t launch_gemv_f32(int epi, int wn, GemvF32Args a, hipStream_t stream) {
   const int mb = (a.M + 15) / 16;
+  hipError_t e;
   switch (mb) {
-    case 1: return launch_mb<1>(epi, a, stream);
-    case 2: return launch_mb<2>(epi, a, stream);
-    case 3: return launch_mb<3>(epi, a, stream);
-    case 4: return launch_mb<4>(epi, a, stream);
+    case 1: e = launch_mb<1>(wn, epi, a, stream); break;
+    case 2: e = launch_mb<2>(wn, epi, a, stream); break;
+    case 3: e = launch_mb<3>(wn, epi, a, stream); break;
+    case 4: e = launch_mb<4>(wn, epi, a, stream); break;
     default: return hipErrorInvalidValue;
   }
+  if (e != hipSuccess || a.ksplit == 1) return e;
+  const int64_t items = (int64_t)a.M * (a.N / 4);
+  hipLaunchKernelGGL(gemv_reduce_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, stream, a,
+                     epi, 16 * mb);
+  return hipGetLastError();
 }
 
 }  // namespace edsl

@@ -38,15 +38,18 @@ struct GemvF32Args {
   float* Y;           // [M][N], row stride ldy
   int64_t ldx, ldw, ldy;
   int M, N, K;
-  int ksplit;         // K slices reduced across workgroups (1 = none)
+  int ksplit;         // K slices reduced by a second kernel (1 = none)
   float alpha;
-  float* partials;    // [ksplit][16*mblocks][N] when ksplit > 1
-  unsigned* counters; // [N/64], all zero between calls
+  float* partials;    // [ksplit][16*ceil(M/16)][N] when ksplit > 1
 };
 
-// Requirements (checked by the caller): 1 <= M <= 64, N % 64 == 0,
-// K % (64*ksplit) == 0, 16-byte aligned X/W/Y/bias and row strides % 4 == 0.
-hipError_t launch_gemv_f32(int epi, GemvF32Args args, hipStream_t stream);
+// A workgroup is 16 waves: `wn` (1, 2 or 4) side by side over 64*wn columns,
+// 16/wn splitting K. Requirements (checked by the caller): 1 <= M <= 64,
+// N % (64*wn) == 0, K % (16 * (16/wn) * ksplit) == 0, 16-byte aligned
+// X/W/Y/bias and row strides % 4 == 0.
+hipError_t launch_gemv_f32(int epi, int wn, GemvF32Args args, hipStream_t stream);
+int gemv_f32_waves_k(int wn);
+int gemv_f32_max_ksplit();
 constexpr int kGemvMaxM = 64;
 
 // ------------------------------------------------------------- integer path
@@ -77,7 +80,11 @@ struct GemmI32Args {
 
 constexpr int kI8Tile = 128;   // M, N, K multiples of this for the int8 MFMA path
 hipError_t launch_narrow_i8(NarrowI8Args args, hipStream_t stream);
-hipError_t launch_gemm_i8(int epi, GemmI32Args args, hipStream_t stream);
+// variant (waves x K bytes per stage): 0 = 4x128, 1 = 4x256, 2 = 8x128, 3 = 8x256, 4 = 4x64;
+// -1 = default. Variants with 256-byte stages need K % 256 == 0.
+constexpr int kI8Variants = 5;
+constexpr int kI8DefaultVariant = 3;
+hipError_t launch_gemm_i8(int epi, GemmI32Args args, hipStream_t stream, int variant = -1);
 // Exact wrapping i32 GEMM on the vector ALUs: any shape, any alignment.
 hipError_t launch_gemm_i32_valu(int epi, GemmI32Args args, hipStream_t stream);
 

@@ -131,7 +131,6 @@ struct DeviceState {
   int cus = 256;
   DevBuf stage[4];  // host-operand staging: X/A, W/B, bias, Y/C
   DevBuf gemv_partials;
-  DevBuf gemv_counters;
   DevBuf i8_x, i8_w, i8_flag;
   unsigned epoch = 0;
 };
@@ -141,6 +140,7 @@ std::mutex g_mu;
 DeviceState g_dev[kMaxDevices];
 int g_force_cfg = -1;
 int g_force_ksplit = 0;
+int g_force_i8 = -1;
 
 void read_env_overrides() {
   static bool done = false;
@@ -148,6 +148,7 @@ void read_env_overrides() {
   done = true;
   if (const char* s = getenv("EDSL_HIP_F32_CONFIG")) g_force_cfg = atoi(s);
   if (const char* s = getenv("EDSL_HIP_GEMV_KSPLIT")) g_force_ksplit = atoi(s);
+  if (const char* s = getenv("EDSL_HIP_I8_VARIANT")) g_force_i8 = atoi(s);
 }
 
 DeviceState& device_state(int* dev_out) {
@@ -247,12 +248,29 @@ void check_dims(int64_t M, int64_t N, int64_t K) {
          (long long)K);
 }
 
-int choose_gemv_ksplit(const DeviceState& ds, int64_t N, int64_t K) {
-  const int64_t groups = N / 64;
-  if (g_force_ksplit > 0 && K % (64LL * g_force_ksplit) == 0) return g_force_ksplit;
-  int ks = 1;
-  while (groups * ks < 2LL * ds.cus && K % (64LL * ks * 2) == 0 && K / (ks * 2) >= 256) ks *= 2;
-  return ks;
+// Small-M plan: the widest column block (wn) whose K split fits the shape,
+// then the smallest power-of-two ksplit that gives at least one workgroup per
+// CU while every wave keeps >= 2 steps of 16 rows.
+bool plan_gemv(const DeviceState& ds, int64_t N, int64_t K, int* wn_out, int* ks_out) {
+  static const int kWn[] = {4, 2, 1};
+  for (int wn : kWn) {
+    const int64_t wk = gemv_f32_waves_k(wn);
+    if (N % (64 * wn) != 0 || K % (16 * wk) != 0 || K < 32 * wk) continue;
+    const int64_t groups = N / (64 * wn);
+    int ks = 1;
+    if (g_force_ksplit > 0 && g_force_ksplit <= gemv_f32_max_ksplit() &&
+        K % (16 * wk * g_force_ksplit) == 0) {
+      ks = g_force_ksplit;
+    } else {
+      while (groups * ks < ds.cus && ks * 2 <= gemv_f32_max_ksplit() && K % (16 * wk * ks * 2) == 0 &&
+             K / (ks * 2) >= 32 * wk)
+        ks *= 2;
+    }
+    *wn_out = wn;
+    *ks_out = ks;
+    return true;
+  }
+  return false;
 }
 
 void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
@@ -261,7 +279,8 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
                        L.ldx % 4 == 0 && L.ldw % 4 == 0 && L.ldy % 4 == 0;
   const int M = (int)L.M, N = (int)L.N, K = (int)L.K;
 
-  if (aligned && M >= 1 && M <= kGemvMaxM && N % 64 == 0 && K % 64 == 0 && K > 0) {
+  int gemv_wn = 0, gemv_ks = 0;
+  if (aligned && M >= 1 && M <= kGemvMaxM && K > 0 && plan_gemv(ds, N, K, &gemv_wn, &gemv_ks)) {
     GemvF32Args a{};
     a.X = static_cast<const float*>(L.x);
     a.W = static_cast<const float*>(L.w);
@@ -274,15 +293,14 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     a.N = N;
     a.K = K;
     a.alpha = L.alpha;
-    a.ksplit = choose_gemv_ksplit(ds, N, K);
+    a.ksplit = gemv_ks;
     const int mb = (M + 15) / 16;
-    if (a.ksplit > 1) {
+    if (a.ksplit > 1)
       a.partials = static_cast<float*>(
           ds.gemv_partials.ensure((size_t)a.ksplit * 16 * mb * N * sizeof(float), false));
-      a.counters = static_cast<unsigned*>(ds.gemv_counters.ensure((size_t)(N / 64) * sizeof(unsigned), true));
-    }
-    check_hip(launch_gemv_f32(L.epi, a, stream), "gemv_f32 launch");
-    set_plan("gemv_f32 mb=%d ksplit=%d grid=%d", mb, a.ksplit, (N / 64) * a.ksplit);
+    check_hip(launch_gemv_f32(L.epi, gemv_wn, a, stream), "gemv_f32 launch");
+    set_plan("gemv_f32 mb=%d ksplit=%d wn=%d grid=%d%s", mb, a.ksplit, gemv_wn,
+             (N / (64 * gemv_wn)) * a.ksplit, a.ksplit > 1 ? " +reduce" : "");
     return;
   }
 
@@ -295,7 +313,7 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     if (g_force_cfg >= 0 && g_force_cfg < gemm_f32_num_configs() && fits(g_force_cfg)) {
       cfg = g_force_cfg;
     } else {
-      static const int kOrder[] = {0, 6, 2, 3};
+      static const int kOrder[] = {5, 0, 6, 2, 3};
       int best = -1;
       int64_t best_tiles = 0;
       for (int c : kOrder) {
@@ -372,8 +390,10 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     a.B8t = w8;
     a.flag = flag;
     a.epoch = ds.epoch;
-    check_hip(launch_gemm_i8(L.epi, a, stream), "gemm_i8 launch");
-    set_plan("narrow_i8+gemm_i8 grid=%d", (a.M / kI8Tile) * (a.N / kI8Tile));
+    int variant = (g_force_i8 >= 0 && g_force_i8 < kI8Variants) ? g_force_i8 : kI8DefaultVariant;
+    if (a.K % 256 != 0 && (variant == 1 || variant == 3)) variant = (variant == 1) ? 0 : 2;
+    check_hip(launch_gemm_i8(L.epi, a, stream, variant), "gemm_i8 launch");
+    set_plan("narrow_i8+gemm_i8 variant=%d grid=%d", variant, (a.M / kI8Tile) * (a.N / kI8Tile));
   } else {
     check_hip(launch_gemm_i32_valu(L.epi, a, stream), "gemm_i32_valu launch");
     set_plan("gemm_i32_valu grid=%d", ((a.M + 127) / 128) * ((a.N + 127) / 128));
@@ -645,6 +665,14 @@ void edsl_hip_set_gemv_ksplit(int ksplit) {
   read_env_overrides();
   g_force_ksplit = ksplit;
 }
+
+void edsl_hip_set_i8_variant(int variant) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  read_env_overrides();
+  g_force_i8 = variant;
+}
+
+int edsl_hip_i8_variant_count(void) { return kI8Variants; }
 
 int edsl_hip_f32_config_count(void) { return gemm_f32_num_configs(); }
 

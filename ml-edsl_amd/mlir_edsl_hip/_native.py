@@ -65,6 +65,10 @@ def _declare(L: ctypes.CDLL) -> None:
     L.edsl_hip_set_f32_config.restype = None
     L.edsl_hip_set_gemv_ksplit.argtypes = [c_int]
     L.edsl_hip_set_gemv_ksplit.restype = None
+    L.edsl_hip_set_i8_variant.argtypes = [c_int]
+    L.edsl_hip_set_i8_variant.restype = None
+    L.edsl_hip_i8_variant_count.argtypes = []
+    L.edsl_hip_i8_variant_count.restype = c_int
     L.edsl_hip_f32_config_count.argtypes = []
     L.edsl_hip_f32_config_count.restype = c_int
     L.edsl_hip_f32_config_name.argtypes = [c_int, ctypes.c_char_p, ctypes.c_size_t]

@@ -56,3 +56,7 @@ def set_f32_config(cfg: int) -> None:
 
 def set_gemv_ksplit(ksplit: int) -> None:
     _native.lib().edsl_hip_set_gemv_ksplit(ksplit)
+
+
+def set_i8_variant(variant: int) -> None:
+    _native.lib().edsl_hip_set_i8_variant(variant)

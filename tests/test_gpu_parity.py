@@ -203,6 +203,27 @@ def test_int8_path_falls_back_when_values_leave_int8(torch_cuda):
     assert np.array_equal(got3, (X2.astype(np.int64) @ W2.astype(np.int64)).astype(np.int32))
 
 
+def test_every_int8_variant(torch_cuda):
+    from mlir_edsl_hip.device import set_i8_variant
+    rng = np.random.default_rng(15)
+    M, K, N = 256, 512, 384
+    X = rng.integers(-128, 128, size=(M, K), dtype=np.int32)
+    W = rng.integers(-128, 128, size=(K, N), dtype=np.int32)
+    b = rng.integers(-2**20, 2**20, size=(N,), dtype=np.int32)
+    Xbig = X.copy()
+    Xbig[5, 7] = 1000  # forces the exact i32 fallback inside the same kernel
+    n = _native.lib().edsl_hip_i8_variant_count()
+    try:
+        for v in range(n):
+            set_i8_variant(v)
+            for Xc in (X, Xbig):
+                got = gpu_run("dense_relu", [Xc, W, b], device=True)
+                assert f"variant={v}" in _native.last_plan()
+                assert np.array_equal(got, oracle.dense_i32(Xc, W, b, "relu"))
+    finally:
+        set_i8_variant(-1)
+
+
 @pytest.mark.parametrize("shape", [(1, 1, 1), (3, 5, 7), (65, 33, 17), (130, 128, 128), (128, 256, 384)])
 def test_int_shapes(shape, torch_cuda):
     M, K, N = shape
