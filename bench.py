@@ -93,7 +93,9 @@ def measure(wname: str, steps: int, warmup: int, rotate: int = 1) -> dict:
 
 
 def load_traffic() -> dict:
-    p = os.path.join(ROOT, "profiles", "traffic.json")
+    """HBM bytes per launch from the committed rocprofv3 PMC passes
+    (FETCH_SIZE and WRITE_SIZE, copy-calibrated), keyed by workload."""
+    p = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.json")
     if os.path.exists(p):
         with open(p) as f:
             return json.load(f)
@@ -137,33 +139,63 @@ def cpu_model() -> str:
 
 def cpu_baseline(wname: str, budget_s: float) -> dict:
     """The oracle (C restatement of the reference CPU-JIT schedule: OpenMP
-    over 64x64 tiles, 8x8x8 fma micro-kernel, separate bias+ReLU pass) on the
-    first R rows of the workload; R is sized so that one run takes about a
-    third of the budget, and the median of 3 runs is reported."""
+    over 64x64 tiles, 8x8x8 fma micro-kernel, separate bias+ReLU pass; exact
+    wrapping i32 for c5) on the first R rows of the workload, in the
+    workload's unit. R is sized so that one run takes about a third of the
+    budget; the median of 3 runs is reported."""
     import oracle
     from mlir_edsl_hip.inputs import WORKLOADS, make_inputs
 
     w = WORKLOADS[wname]
-    X, W, b = make_inputs(w)
+    arrays = make_inputs(w)
     threads = oracle.cpu_threads()
-    R = 64
+    bias = w.pattern != "matmul"
+
+    def run(R: int) -> None:
+        X = arrays[0][:R]
+        if w.dtype == "i32":
+            oracle.dense_i32(X, arrays[1], arrays[2], "relu", threads=threads)
+        elif bias:
+            oracle.dense_f32(X, arrays[1], arrays[2], "relu", threads=threads)
+        else:
+            oracle.dense_f32(X, arrays[1], None, "none", threads=threads)
+
+    unit = min(64, w.M)
     t0 = time.perf_counter()
-    oracle.dense_f32(X[:R], W, b, "relu", threads=threads)
-    t_probe = time.perf_counter() - t0
-    per_row = t_probe / R
-    R = int(max(64, min(w.M, (budget_s / 3) / max(per_row, 1e-9))) // 64 * 64)
+    run(unit)
+    per_row = (time.perf_counter() - t0) / unit
+    R = int(max(unit, min(w.M, (budget_s / 3) / max(per_row, 1e-9))) // unit * unit)
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
-        oracle.dense_f32(X[:R], W, b, "relu", threads=threads)
+        run(R)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
-    flops = 2 * R * w.N * w.K
-    return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": f"rows 0..{R - 1} of {wname} (X[{R},{w.K}] @ W[{w.K},{w.N}] + b, ReLU), "
-                      f"median of 3 runs, {t:.2f} s each",
+    if UNITS[wname] == "GB/s":
+        work = 4 * (R * w.K + w.K * w.N + (w.N if bias else 0) + R * w.N)
+        value = work / t / 1e9
+    else:
+        value = 2 * R * w.N * w.K / t / 1e12
+    what = "X[R,K] @ W[K,N]" + (" + b, ReLU" if bias else "")
+    return {"value": round(value, 5), "unit": UNITS[wname], "cores": threads, "kind": "port",
+            "sample": f"rows 0..{R - 1} of {wname} ({what}, R={R}, K={w.K}, N={w.N}), "
+                      f"median of 3 runs, {t:.3f} s each",
             "host_cpu": cpu_model()}
+
+
+UNITS = {"c1": "TFLOP/s", "c2": "TFLOP/s", "c3": "TFLOP/s", "c4": "GB/s", "c5": "TOP/s"}
+# (steps, warmup, W buffers rotated) of each workload when it is not the headline
+SECONDARY_PLAN = {"c4": (200, 20, 3), "c5": (100, 20, 1), "c2": (100, 20, 1), "c1": (200, 20, 1),
+                  "c3": (50, 10, 1)}
+
+
+def step_value(wname: str, step_s: float) -> float:
+    """Whole-step throughput in the workload's unit."""
+    from mlir_edsl_hip.inputs import WORKLOADS
+    wl = WORKLOADS[wname]
+    if UNITS[wname] == "GB/s":
+        return wl.compulsory_bytes / step_s / 1e9
+    return wl.flops / step_s / 1e12
 
 
 def main() -> int:
@@ -171,9 +203,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="c3", choices=sorted(UNITS),
+                    help="workload of the headline line (default c3, the BASELINE metric's config)")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--secondary", default="c4,c5,c2,c1",
-                    help="comma-separated secondary workloads to measure after c3")
+                    help="comma-separated workloads measured after the headline one")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -183,7 +217,8 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures the dense path on one GPU only: this build has no multi-GPU "
-              "path (column-sharding design in DESIGN.md); run with --gpus 1.", file=sys.stderr)
+              "path (the column-sharding design is described in DESIGN.md); run with --gpus 1.",
+              file=sys.stderr)
         return 2
 
     import torch
@@ -203,42 +238,42 @@ def main() -> int:
     from mlir_edsl_hip.inputs import WORKLOADS
 
     traffic = load_traffic()
-    w = WORKLOADS["c3"]
-    log(f"[bench] c3 {w.description}: warmup {args.warmup}, steps {args.steps}")
-    head = measure("c3", args.steps, args.warmup)
-    log(f"[bench] c3 done: {head['ms_per_step']:.3f} ms/step, kernel {head['kernel_ms_mean']:.3f} ms [{head['plan']}]")
+    head_name = args.workload
+    w = WORKLOADS[head_name]
+    rotate = SECONDARY_PLAN[head_name][2]
+    log(f"[bench] {head_name} {w.description}: warmup {args.warmup}, steps {args.steps}")
+    head = measure(head_name, args.steps, args.warmup, rotate=rotate)
+    log(f"[bench] {head_name} done: {head['ms_per_step']:.4f} ms/step, kernel "
+        f"{head['kernel_ms_mean'] * 1e3:.1f} us [{head['plan']}]")
 
     secondary = []
     if not args.no_secondary:
-        plan = {"c4": (200, 3), "c5": (100, 1), "c2": (100, 1), "c1": (200, 1)}
-        for wname in [w.strip() for w in args.secondary.split(",") if w.strip()]:
-            steps, rot = plan[wname]
+        for wname in [x.strip() for x in args.secondary.split(",") if x.strip()]:
+            if wname == head_name:
+                continue
+            steps, warm, rot = SECONDARY_PLAN[wname]
             log(f"[bench] {wname} {WORKLOADS[wname].description}")
-            r = measure(wname, steps, 20, rotate=rot)
+            r = measure(wname, steps, warm, rotate=rot)
             wl = WORKLOADS[wname]
-            step_s = r["ms_per_step"] * 1e-3
-            if wname == "c4":
-                val, unit = wl.compulsory_bytes / step_s / 1e9, "GB/s"
-            elif wname == "c5":
-                val, unit = wl.flops / step_s / 1e12, "TOP/s"
-            else:
-                val, unit = wl.flops / step_s / 1e12, "TFLOP/s"
-            r.update({"value": round(val, 3), "unit": unit, "roofline": roofline_for(wname, r, traffic),
+            val = step_value(wname, r["ms_per_step"] * 1e-3)
+            r.update({"value": round(val, 3), "unit": UNITS[wname],
+                      "roofline": roofline_for(wname, r, traffic),
                       "config": {"M": wl.M, "K": wl.K, "N": wl.N, "seed": wl.seed, "dtype": wl.dtype}})
-            log(f"[bench] {wname} done: {val:.2f} {unit}, kernel {r['kernel_ms_mean'] * 1e3:.1f} us [{r['plan']}]")
+            log(f"[bench] {wname} done: {val:.2f} {UNITS[wname]}, kernel {r['kernel_ms_mean'] * 1e3:.1f} us "
+                f"[{r['plan']}]")
             secondary.append(r)
 
     cpu = None
     if not args.no_cpu_baseline:
-        log("[bench] cpu baseline (oracle, row sample of c3)")
-        cpu = cpu_baseline("c3", args.cpu_seconds)
-        log(f"[bench] cpu baseline: {cpu['value']} TFLOP/s on {cpu['cores']} threads")
+        log(f"[bench] cpu baseline (oracle, row sample of {head_name})")
+        cpu = cpu_baseline(head_name, args.cpu_seconds)
+        log(f"[bench] cpu baseline: {cpu['value']} {cpu['unit']} on {cpu['cores']} threads")
 
-    value = w.flops / (head["ms_per_step"] * 1e-3) / 1e12
+    value = step_value(head_name, head["ms_per_step"] * 1e-3)
     line = {
         "metric": METRIC,
         "value": round(value, 3),
-        "unit": "TFLOP/s",
+        "unit": UNITS[head_name],
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -246,11 +281,13 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic: numpy PCG64 default_rng(seed); X~N(0,1), W~N(0,1/K), b~U[-0.1,0.1)",
-        "config": {"workload": "c3: fp32 dense relu(X@W+b), M=N=K=4096", "M": w.M, "N": w.N,
-                   "K": w.K, "seed": w.seed, "parallelism": "single GPU", "plan": head["plan"]},
-        "roofline": roofline_for("c3", head, traffic),
+        "dtype": "f32" if w.dtype == "f32" else "i32 (int8 MFMA)",
+        "data": "synthetic: numpy PCG64 default_rng(seed); X~N(0,1), W~N(0,1/K), b~U[-0.1,0.1) "
+                "(c5: ints in [-8,7], b in [-512,511])",
+        "config": {"workload": f"{head_name}: {w.description}", "M": w.M, "N": w.N, "K": w.K,
+                   "seed": w.seed, "parallelism": "single GPU", "plan": head["plan"],
+                   "w_buffers_rotated": rotate},
+        "roofline": roofline_for(head_name, head, traffic),
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

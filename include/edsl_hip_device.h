@@ -56,6 +56,9 @@ int edsl_hip_last_plan(char *buf, size_t len);
  * Calls that cannot use the forced choice fall back to the automatic one. */
 void edsl_hip_set_f32_config(int cfg);
 void edsl_hip_set_gemv_ksplit(int ksplit);
+/* Small-M column block: columns per workgroup, one of 32, 64, 128, 256;
+ * 0 = automatic. */
+void edsl_hip_set_gemv_cols(int cols);
 /* int8 GEMM pipeline variant (waves per workgroup x stages in flight), index
  * < edsl_hip_i8_variant_count(); -1 = automatic. */
 void edsl_hip_set_i8_variant(int variant);

@@ -5,24 +5,26 @@
 // 301-339), shaped for the HBM-bound case where W dominates the traffic
 // (M=16, K=N=8192: W is 256 MiB, X and Y 512 KiB each).
 //
-// Every W element is read from HBM exactly once, with 16-byte loads, and used
-// for all M rows at once on the matrix cores:
+// Every W element is read from HBM exactly once and used for all M rows at
+// once on the matrix cores:
 //  * v_mfma_f32_16x16x4_f32: lane l supplies X[row l%16][k-slot l/16] and
 //    W[k-slot l/16][col l%16]. Lane group g = l/16 owns the k rows
-//    k0+4g .. k0+4g+3 of each 16-row step: it loads those 4 k of its X row with
-//    one 16-byte load and, for each k, 4 consecutive W columns with one 16-byte
-//    load. MFMA (step s, column phase c) pairs X[.][k0+4g+s] with
-//    W[k0+4g+s][n0 + 4*(l%16) + c], so lane l%16 accumulates columns
-//    n0 + 4*(l%16) + c: a wave owns 64 columns and stores float4 per row.
-//  * A workgroup is 16 waves: WN waves side by side cover 64*WN adjacent
-//    columns (so a row is read in 64*WN*4-byte runs), and WK = 16/WN waves
-//    split the workgroup's K range. The WK slices are summed in LDS, in wave
-//    order.
-//  * K is further split over `ksplit` workgroups so that the grid fills the
-//    256 CUs. Each writes its partial tile; a second small kernel sums the
-//    partials in split order and applies bias and activation. (An in-kernel
-//    "last workgroup reduces" scheme needs device-scope fences, which on this
-//    part write back and invalidate L2 and cost more than the extra launch.)
+//    k0+4g .. k0+4g+3 of each 16-row step: it loads those 4 k of its X row
+//    with one 16-byte load and, for each k, CPL consecutive W columns with one
+//    4*CPL-byte load. MFMA (step s, column phase c) pairs X[.][k0+4g+s] with
+//    W[k0+4g+s][n0 + CPL*(l%16) + c], so lane l%16 accumulates columns
+//    n0 + CPL*(l%16) + c: a wave owns 16*CPL columns and stores CPL per row.
+//  * A workgroup is 16 waves covering `cols` adjacent columns: WN waves side
+//    by side (cols = 16*CPL*WN), and WK = 16/WN waves splitting the
+//    workgroup's K range. The WK slices are summed in LDS, in wave order.
+//    cols = 32 (CPL 2, WN 1) gives N/32 workgroups that each own the full K:
+//    at N = 8192 that is one per CU and no cross-workgroup reduction at all.
+//  * Wider column blocks read longer row runs but give fewer workgroups;
+//    they split K over `ksplit` workgroups to fill the chip. Each writes its
+//    partial tile, and a second small kernel sums the partials in split order
+//    and applies bias and activation. (A "last workgroup to arrive reduces"
+//    variant, with the partials exchanged through agent-scope atomics, was
+//    measured: it costs as much as the extra launch, so it is not used.)
 //  * Each wave starts its K walk at a hashed offset (wrapping), so the rows
 //    in flight at any moment are spread over the matrix and over the HBM
 //    channels instead of every wave hitting the same few rows.
@@ -37,6 +39,7 @@ namespace edsl {
 namespace {
 
 constexpr int kWavesPerWG = 16;
+constexpr int kMaxSplit = 16;
 
 __device__ __forceinline__ float epilogue_rt(float acc, float b, float alpha, int epi) {
   switch (epi) {
@@ -49,10 +52,13 @@ __device__ __forceinline__ float epilogue_rt(float acc, float b, float alpha, in
   }
 }
 
-template <int MB, int WN>
+template <int MB, int CPL, int WN>
 __global__ void __launch_bounds__(kWavesPerWG * 64)
 gemv_f32_kernel(GemvF32Args a, int epi) {
+  using vec = typename std::conditional<CPL == 4, f32x4, f32x2>::type;
   constexpr int WK = kWavesPerWG / WN;
+  constexpr int kWaveCols = 16 * CPL;
+  constexpr int kGroupCols = kWaveCols * WN;
   // 16-row steps per loop iteration: 8 W loads in flight per lane, fewer when
   // the accumulators of 3-4 row blocks need the registers.
   constexpr int kU = MB <= 2 ? 2 : 1;
@@ -60,24 +66,24 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
   const int wave = threadIdx.x >> 6;
   const int wn = wave % WN;
   const int wk = wave / WN;
-  const int groups = a.N / (64 * WN);
+  const int groups = a.N / kGroupCols;
   const int g = blockIdx.x % groups;
   const int split = blockIdx.x / groups;
-  const int n0 = g * 64 * WN + 64 * wn;
+  const int n0 = g * kGroupCols + kWaveCols * wn;
   const int kspan = a.K / a.ksplit;
   const int kwave = kspan / WK;  // multiple of 16
   const int kbeg = split * kspan + wk * kwave;
   const int li = lane & 15;
   const int lg = lane >> 4;
 
-  f32x4 acc[MB][4];
+  f32x4 acc[MB][CPL];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[mb][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < CPL; ++c) acc[mb][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int64_t ldw = a.ldw;
-  const float* wbase = a.W + (int64_t)(kbeg + 4 * lg) * ldw + n0 + 4 * li;
+  const float* wbase = a.W + (int64_t)(kbeg + 4 * lg) * ldw + n0 + CPL * li;
   const float* xp[MB];
   bool xrow[MB];
 #pragma unroll
@@ -91,13 +97,12 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
   auto steps = [&](auto u_tag, int k) {
     constexpr int U = decltype(u_tag)::value;
     const float* wp = wbase + (int64_t)k * ldw;
-    f32x4 w[U][4];
+    vec w[U][4];
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        w[u][s] = __builtin_nontemporal_load(
-            reinterpret_cast<const f32x4*>(wp + (int64_t)(16 * u + s) * ldw));
+        w[u][s] = __builtin_nontemporal_load(reinterpret_cast<const vec*>(wp + (int64_t)(16 * u + s) * ldw));
     f32x4 x[U][MB];
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -113,7 +118,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-          for (int c = 0; c < 4; ++c)
+          for (int c = 0; c < CPL; ++c)
             acc[mb][c] =
                 __builtin_amdgcn_mfma_f32_16x16x4f32(x[u][mb][s], w[u][s][c], acc[mb][c], 0, 0, 0);
   };
@@ -133,41 +138,43 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
 
   // Sum the WK K-slices of each column block in wave order, one row block at
   // a time to bound LDS.
-  __shared__ f32x4 red[WK > 1 ? WK - 1 : 1][WN][4][64];
+  __shared__ f32x4 red[WK > 1 ? WK - 1 : 1][WN][CPL][64];
   if constexpr (WK > 1) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       if (wk > 0) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) red[wk - 1][wn][c][lane] = acc[mb][c];
+        for (int c = 0; c < CPL; ++c) red[wk - 1][wn][c][lane] = acc[mb][c];
       }
       __syncthreads();
       if (wk == 0) {
 #pragma unroll
         for (int w = 0; w < WK - 1; ++w)
 #pragma unroll
-          for (int c = 0; c < 4; ++c) acc[mb][c] += red[w][wn][c][lane];
+          for (int c = 0; c < CPL; ++c) acc[mb][c] += red[w][wn][c][lane];
       }
       __syncthreads();
     }
     if (wk != 0) return;
   }
 
-  // Lane holds rows 16*mb + 4*lg + r and columns n0 + 4*li + c.
-  const int col = n0 + 4 * li;
+  // Lane holds rows 16*mb + 4*lg + r and columns n0 + CPL*li + c.
+  const int col = n0 + CPL * li;
   if (a.ksplit == 1) {
-    f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (epi_has_bias(epi)) bv = *reinterpret_cast<const f32x4*>(a.bias + col);
+    vec bv;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) bv[c] = 0.0f;
+    if (epi_has_bias(epi)) bv = *reinterpret_cast<const vec*>(a.bias + col);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mb + 4 * lg + r;
         if (row < a.M) {
-          f32x4 y;
+          vec y;
 #pragma unroll
-          for (int c = 0; c < 4; ++c) y[c] = epilogue_rt(acc[mb][c][r], bv[c], a.alpha, epi);
-          *reinterpret_cast<f32x4*>(a.Y + (int64_t)row * a.ldy + col) = y;
+          for (int c = 0; c < CPL; ++c) y[c] = epilogue_rt(acc[mb][c][r], bv[c], a.alpha, epi);
+          *reinterpret_cast<vec*>(a.Y + (int64_t)row * a.ldy + col) = y;
         }
       }
     return;
@@ -179,16 +186,16 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * mb + 4 * lg + r;
       if (row < a.M) {
-        f32x4 p = {acc[mb][0][r], acc[mb][1][r], acc[mb][2][r], acc[mb][3][r]};
-        *reinterpret_cast<f32x4*>(a.partials + ((int64_t)split * prow + row) * a.N + col) = p;
+        vec p;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) p[c] = acc[mb][c][r];
+        *reinterpret_cast<vec*>(a.partials + ((int64_t)split * prow + row) * a.N + col) = p;
       }
     }
 }
 
 // Y[m, 4j..4j+3] = epilogue(sum over splits s = 0..ksplit-1, in order).
 // All split loads are issued before the first add so their latencies overlap.
-constexpr int kMaxSplit = 16;
-
 __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi, int prow) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over M * N/4
   const int n4 = a.N / 4;
@@ -214,13 +221,14 @@ __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi
 }
 
 template <int MB>
-hipError_t launch_mb(int wn, int epi, const GemvF32Args& a, hipStream_t stream) {
-  const dim3 grid((a.N / (64 * wn)) * a.ksplit);
+hipError_t launch_mb(int cols, int epi, const GemvF32Args& a, hipStream_t stream) {
+  const dim3 grid((a.N / cols) * a.ksplit);
   const dim3 block(kWavesPerWG * 64);
-  switch (wn) {
-    case 1: hipLaunchKernelGGL((gemv_f32_kernel<MB, 1>), grid, block, 0, stream, a, epi); break;
-    case 2: hipLaunchKernelGGL((gemv_f32_kernel<MB, 2>), grid, block, 0, stream, a, epi); break;
-    case 4: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4>), grid, block, 0, stream, a, epi); break;
+  switch (cols) {
+    case 32: hipLaunchKernelGGL((gemv_f32_kernel<MB, 2, 1>), grid, block, 0, stream, a, epi); break;
+    case 64: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 1>), grid, block, 0, stream, a, epi); break;
+    case 128: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 2>), grid, block, 0, stream, a, epi); break;
+    case 256: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 4>), grid, block, 0, stream, a, epi); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -228,17 +236,17 @@ hipError_t launch_mb(int wn, int epi, const GemvF32Args& a, hipStream_t stream) 
 
 }  // namespace
 
-int gemv_f32_waves_k(int wn) { return kWavesPerWG / wn; }
+int gemv_f32_waves_k(int cols) { return cols <= 64 ? kWavesPerWG : kWavesPerWG / (cols / 64); }
 int gemv_f32_max_ksplit() { return kMaxSplit; }
 
-hipError_t launch_gemv_f32(int epi, int wn, GemvF32Args a, hipStream_t stream) {
+hipError_t launch_gemv_f32(int epi, int cols, GemvF32Args a, hipStream_t stream) {
   const int mb = (a.M + 15) / 16;
   hipError_t e;
   switch (mb) {
-    case 1: e = launch_mb<1>(wn, epi, a, stream); break;
-    case 2: e = launch_mb<2>(wn, epi, a, stream); break;
-    case 3: e = launch_mb<3>(wn, epi, a, stream); break;
-    case 4: e = launch_mb<4>(wn, epi, a, stream); break;
+    case 1: e = launch_mb<1>(cols, epi, a, stream); break;
+    case 2: e = launch_mb<2>(cols, epi, a, stream); break;
+    case 3: e = launch_mb<3>(cols, epi, a, stream); break;
+    case 4: e = launch_mb<4>(cols, epi, a, stream); break;
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess || a.ksplit == 1) return e;

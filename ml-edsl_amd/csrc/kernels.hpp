@@ -43,12 +43,12 @@ struct GemvF32Args {
   float* partials;    // [ksplit][16*ceil(M/16)][N] when ksplit > 1
 };
 
-// A workgroup is 16 waves: `wn` (1, 2 or 4) side by side over 64*wn columns,
-// 16/wn splitting K. Requirements (checked by the caller): 1 <= M <= 64,
-// N % (64*wn) == 0, K % (16 * (16/wn) * ksplit) == 0, 16-byte aligned
-// X/W/Y/bias and row strides % 4 == 0.
-hipError_t launch_gemv_f32(int epi, int wn, GemvF32Args args, hipStream_t stream);
-int gemv_f32_waves_k(int wn);
+// A workgroup is 16 waves over `cols` adjacent columns (32, 64, 128 or 256);
+// the waves not side by side split K. Requirements (checked by the caller):
+// 1 <= M <= 64, N % cols == 0, K % (16 * gemv_f32_waves_k(cols) * ksplit) == 0,
+// 16-byte aligned X/W/Y/bias and row strides % 4 == 0.
+hipError_t launch_gemv_f32(int epi, int cols, GemvF32Args args, hipStream_t stream);
+int gemv_f32_waves_k(int cols);
 int gemv_f32_max_ksplit();
 constexpr int kGemvMaxM = 64;
 

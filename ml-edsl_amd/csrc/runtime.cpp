@@ -120,7 +120,11 @@ struct DevBuf {
     }
     const size_t want = std::max<size_t>((bytes + 255) & ~size_t(255), 256);
     check_hip(hipMalloc(&p, want), "hipMalloc");
-    if (zero_fill) check_hip(hipMemset(p, 0, want), "hipMemset");
+    if (zero_fill) {
+      // Finished before any stream (blocking or not) can use the buffer.
+      check_hip(hipMemset(p, 0, want), "hipMemset");
+      check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    }
     cap = want;
     return p;
   }
@@ -140,6 +144,7 @@ std::mutex g_mu;
 DeviceState g_dev[kMaxDevices];
 int g_force_cfg = -1;
 int g_force_ksplit = 0;
+int g_force_cols = 0;
 int g_force_i8 = -1;
 
 void read_env_overrides() {
@@ -148,6 +153,7 @@ void read_env_overrides() {
   done = true;
   if (const char* s = getenv("EDSL_HIP_F32_CONFIG")) g_force_cfg = atoi(s);
   if (const char* s = getenv("EDSL_HIP_GEMV_KSPLIT")) g_force_ksplit = atoi(s);
+  if (const char* s = getenv("EDSL_HIP_GEMV_COLS")) g_force_cols = atoi(s);
   if (const char* s = getenv("EDSL_HIP_I8_VARIANT")) g_force_i8 = atoi(s);
 }
 
@@ -248,29 +254,46 @@ void check_dims(int64_t M, int64_t N, int64_t K) {
          (long long)K);
 }
 
-// Small-M plan: the widest column block (wn) whose K split fits the shape,
-// then the smallest power-of-two ksplit that gives at least one workgroup per
-// CU while every wave keeps >= 2 steps of 16 rows.
-bool plan_gemv(const DeviceState& ds, int64_t N, int64_t K, int* wn_out, int* ks_out) {
-  static const int kWn[] = {4, 2, 1};
-  for (int wn : kWn) {
-    const int64_t wk = gemv_f32_waves_k(wn);
-    if (N % (64 * wn) != 0 || K % (16 * wk) != 0 || K < 32 * wk) continue;
-    const int64_t groups = N / (64 * wn);
+// Small-M plan. Widths are tried in the order 128, 256, 64, 32 columns per
+// workgroup; for each, the K split is the smallest power of two that gives at
+// least one workgroup per CU (every wave keeping >= 2 steps of 16 rows). The
+// first width that fills the chip is taken; when none does, the plan with the
+// most workgroups. The order is measured (M=16, K=N=8192 on MI355X): 128
+// columns x 4 splits beat 256 x 8 (more partial traffic), 64 x 2 (256-byte row
+// runs) and 32 x 1 (8-byte loads: the per-CU request rate, not the byte
+// count, limits a streaming workgroup). A forced split
+// (edsl_hip_set_gemv_ksplit) limits the choice to the widths that can take it.
+bool plan_gemv(const DeviceState& ds, int64_t N, int64_t K, int* cols_out, int* ks_out) {
+  static const int kCols[] = {128, 256, 64, 32};
+  int best_cols = 0, best_ks = 0;
+  int64_t best_wgs = 0;
+  for (int cols : kCols) {
+    if (g_force_cols > 0 && cols != g_force_cols) continue;
+    const int64_t wk = gemv_f32_waves_k(cols);
+    if (N % cols != 0 || K % (16 * wk) != 0 || K < 32 * wk) continue;
+    const int64_t groups = N / cols;
     int ks = 1;
-    if (g_force_ksplit > 0 && g_force_ksplit <= gemv_f32_max_ksplit() &&
-        K % (16 * wk * g_force_ksplit) == 0) {
+    if (g_force_ksplit > 0) {
+      // A forced split is taken only by widths that can honour it.
+      if (g_force_ksplit > gemv_f32_max_ksplit() || K % (16 * wk * g_force_ksplit) != 0) continue;
       ks = g_force_ksplit;
     } else {
       while (groups * ks < ds.cus && ks * 2 <= gemv_f32_max_ksplit() && K % (16 * wk * ks * 2) == 0 &&
              K / (ks * 2) >= 32 * wk)
         ks *= 2;
     }
-    *wn_out = wn;
-    *ks_out = ks;
-    return true;
+    const int64_t wgs = groups * ks;
+    if (wgs > best_wgs) {
+      best_cols = cols;
+      best_ks = ks;
+      best_wgs = wgs;
+    }
+    if (wgs >= ds.cus) break;
   }
-  return false;
+  if (best_cols == 0) return false;
+  *cols_out = best_cols;
+  *ks_out = best_ks;
+  return true;
 }
 
 void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
@@ -279,8 +302,8 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
                        L.ldx % 4 == 0 && L.ldw % 4 == 0 && L.ldy % 4 == 0;
   const int M = (int)L.M, N = (int)L.N, K = (int)L.K;
 
-  int gemv_wn = 0, gemv_ks = 0;
-  if (aligned && M >= 1 && M <= kGemvMaxM && K > 0 && plan_gemv(ds, N, K, &gemv_wn, &gemv_ks)) {
+  int gemv_cols = 0, gemv_ks = 0;
+  if (aligned && M >= 1 && M <= kGemvMaxM && K > 0 && plan_gemv(ds, N, K, &gemv_cols, &gemv_ks)) {
     GemvF32Args a{};
     a.X = static_cast<const float*>(L.x);
     a.W = static_cast<const float*>(L.w);
@@ -298,9 +321,9 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     if (a.ksplit > 1)
       a.partials = static_cast<float*>(
           ds.gemv_partials.ensure((size_t)a.ksplit * 16 * mb * N * sizeof(float), false));
-    check_hip(launch_gemv_f32(L.epi, gemv_wn, a, stream), "gemv_f32 launch");
-    set_plan("gemv_f32 mb=%d ksplit=%d wn=%d grid=%d%s", mb, a.ksplit, gemv_wn,
-             (N / (64 * gemv_wn)) * a.ksplit, a.ksplit > 1 ? " +reduce" : "");
+    check_hip(launch_gemv_f32(L.epi, gemv_cols, a, stream), "gemv_f32 launch");
+    set_plan("gemv_f32 mb=%d ksplit=%d cols=%d grid=%d%s", mb, a.ksplit, gemv_cols,
+             (N / gemv_cols) * a.ksplit, a.ksplit > 1 ? " +reduce" : "");
     return;
   }
 
@@ -664,6 +687,12 @@ void edsl_hip_set_gemv_ksplit(int ksplit) {
   std::lock_guard<std::mutex> lock(g_mu);
   read_env_overrides();
   g_force_ksplit = ksplit;
+}
+
+void edsl_hip_set_gemv_cols(int cols) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  read_env_overrides();
+  g_force_cols = cols;
 }
 
 void edsl_hip_set_i8_variant(int variant) {

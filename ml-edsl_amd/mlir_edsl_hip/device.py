@@ -58,5 +58,9 @@ def set_gemv_ksplit(ksplit: int) -> None:
     _native.lib().edsl_hip_set_gemv_ksplit(ksplit)
 
 
+def set_gemv_cols(cols: int) -> None:
+    _native.lib().edsl_hip_set_gemv_cols(cols)
+
+
 def set_i8_variant(variant: int) -> None:
     _native.lib().edsl_hip_set_i8_variant(variant)

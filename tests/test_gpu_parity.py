@@ -321,6 +321,30 @@ def test_small_m_kernel(M, ksplit, torch_cuda):
         set_gemv_ksplit(0)
 
 
+@pytest.mark.parametrize("cols", [32, 64, 128, 256])
+@pytest.mark.parametrize("ksplit", [1, 2, 4, 8, 16])
+def test_small_m_column_blocks_and_splits(cols, ksplit, torch_cuda):
+    """Every column-block width and K split, on back-to-back calls with
+    different inputs and row counts (the partial buffer is reused)."""
+    from mlir_edsl_hip.device import set_gemv_cols, set_gemv_ksplit
+    K, N = 4096, 1024
+    set_gemv_cols(cols)
+    set_gemv_ksplit(ksplit)
+    try:
+        for trial, M in enumerate((16, 5, 33, 64)):
+            rng = np.random.default_rng(1000 * cols + 10 * ksplit + trial)
+            X = rng.standard_normal((M, K), dtype=np.float32)
+            W = (rng.standard_normal((K, N), dtype=np.float32) / np.float32(64)).astype(np.float32)
+            b = rng.standard_normal(N, dtype=np.float32)
+            got = gpu_run("dense_relu", [X, W, b], device=True)
+            plan = _native.last_plan()
+            assert f"ksplit={ksplit} cols={cols}" in plan, plan
+            check(got, oracle.dense_f32(X, W, b, "relu"), K)
+    finally:
+        set_gemv_cols(0)
+        set_gemv_ksplit(0)
+
+
 def test_every_f32_tile_config(torch_cuda):
     from mlir_edsl_hip.device import set_f32_config
     rng = np.random.default_rng(13)
