@@ -92,6 +92,24 @@ def measure(wname: str, steps: int, warmup: int, rotate: int = 1) -> dict:
     return res
 
 
+def measure_host_path(wname: str, calls: int) -> dict:
+    """The reference's GPU calling pattern: host arrays in, host array out,
+    through the memref-descriptor C ABI (include/edsl_hip.h). Each call copies
+    the operands to the device, runs the kernels and copies Y back."""
+    from mlir_edsl_hip import backend
+    from mlir_edsl_hip.inputs import WORKLOADS, make_inputs
+
+    w = WORKLOADS[wname]
+    arrays = make_inputs(w)
+    backend.run(w.pattern, *arrays)  # first call sizes the staging buffers
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        backend.run(w.pattern, *arrays)
+    t = (time.perf_counter() - t0) / calls
+    return {"value": round(step_value(wname, t), 3), "unit": UNITS[wname], "ms_per_call": round(t * 1e3, 4),
+            "calls": calls, "what": "host numpy buffers through the memref-ABI entry: H2D + kernels + D2H"}
+
+
 def load_traffic() -> dict:
     """HBM bytes per launch from the committed rocprofv3 PMC passes
     (FETCH_SIZE and WRITE_SIZE, copy-calibrated), keyed by workload."""
@@ -210,6 +228,10 @@ def main() -> int:
                     help="comma-separated workloads measured after the headline one")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--host-path", action="store_true",
+                    help="also time the memref-ABI entry on host (numpy) buffers for the headline "
+                         "workload: H2D copies + kernels + D2H, as the reference GPU path does "
+                         "(reported as host_path, never as value)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES (3 times) and exit; "
                          "its FETCH_SIZE / WRITE_SIZE counters calibrate the traffic figures")
@@ -263,6 +285,11 @@ def main() -> int:
                 f"[{r['plan']}]")
             secondary.append(r)
 
+    host = None
+    if args.host_path:
+        host = measure_host_path(head_name, max(3, args.steps // 5))
+        log(f"[bench] host path: {host['value']:.2f} {host['unit']} ({host['ms_per_call']:.3f} ms/call)")
+
     cpu = None
     if not args.no_cpu_baseline:
         log(f"[bench] cpu baseline (oracle, row sample of {head_name})")
@@ -291,6 +318,8 @@ def main() -> int:
         "cpu_baseline": cpu,
         "secondary": secondary,
     }
+    if host is not None:
+        line["host_path"] = host
     print(json.dumps(line), flush=True)
     return 0
 

@@ -25,6 +25,16 @@
  *   - i32: arith.muli / arith.addi, two's complement wrapping; ReLU written
  *     tensor_map(v -> If(v > 0, v, 0)) (LinalgBuilder.cpp:141-178).
  *
+ * Pinning (tests/test_oracle.py): the reference's known answers, exact
+ * rational golden vectors (tests/golden/make_golden.py), the fp64 forward-error
+ * bound, exact wrapping i32 arithmetic, IEEE special values, and eight planted
+ * mistakes that those checks must catch.
+ * Parity unpinned: oracle_static_tiles, i.e. WHICH rounding chain (fma or
+ * mulf+addf) the reference JIT takes for a given shape. Deciding it needs the
+ * MLIR vectorizer itself, which is absent here. Both chains are pinned bit for
+ * bit by the golden vectors and by value through the fp64 bound, and they
+ * differ by a few ulp, far inside the fp32 parity tolerance.
+ *
  * Operands are contiguous row-major: X[M][K], W[K][N], b[N], Y[M][N].
  * epilogue: bit 0 = add bias; bits 1-2 = activation (0 none, 1 relu, 2 leaky).
  */
