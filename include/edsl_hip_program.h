@@ -1,0 +1,99 @@
+/*
+ * edsl_hip_program.h -- compile the reference front end's serialized
+ * FunctionDef and run it on the gfx950 dense-path kernels.
+ *
+ * These entry points are what the reference's pybind module `_mlir_backend`
+ * (reference cpp/src/python_bindings.cpp:8-98) binds on its MLIRCompiler
+ * (reference cpp/include/mlir_edsl/MLIRCompiler.h, cpp/src/MLIRCompiler.cpp),
+ * restated as a C ABI over an opaque module handle, for the dense-path
+ * programs only:
+ *
+ *   matmul(A, B) / A @ B, relu(A @ B), X @ W + b, relu(X @ W + b),
+ *   leaky_relu(X @ W + b, alpha), and tensor_map(X @ W [+ b],
+ *   lambda v: If(v > 0, v, 0)) over i32 -- X, W, b being parameters with
+ *   static tensor types.
+ *
+ * Any other program is rejected at compile time with an error that names
+ * what was found. Errors: functions returning int return 0 on success or an
+ * error code (the message is in edsl_hip_last_error(), include/edsl_hip.h),
+ * as the reference raises std::runtime_error from the same calls.
+ */
+#ifndef EDSL_HIP_PROGRAM_H
+#define EDSL_HIP_PROGRAM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* A set of compiled functions (the reference's MLIRCompiler instance). */
+typedef struct edsl_hip_module edsl_hip_module;
+
+/* MLIRCompiler() / ~MLIRCompiler(). create returns NULL on allocation failure. */
+edsl_hip_module *edsl_hip_module_create(void);
+void edsl_hip_module_destroy(edsl_hip_module *m);
+
+/* MLIRCompiler::compileFunction (reference cpp/src/MLIRCompiler.cpp:184-216),
+ * bound as compile_function(bytes) (cpp/src/python_bindings.cpp:13-23):
+ * `bytes` is a serialized mlir_edsl.FunctionDef (cpp/schemas/ast.proto:473-478).
+ * Dynamic (-1) dimensions are rejected like the reference's convertTensorType
+ * (cpp/src/MLIRBuilder.cpp:478-486). Compiling a name twice is an error. */
+int edsl_hip_module_compile_function(edsl_hip_module *m, const void *bytes, size_t len);
+
+/* MLIRCompiler::hasFunction / listFunctions (cpp/src/MLIRCompiler.cpp:314-320).
+ * list writes the names in sorted order, '\n'-separated, NUL-terminated
+ * (truncated to len) and returns the full length. */
+int edsl_hip_module_has_function(edsl_hip_module *m, const char *name);
+int edsl_hip_module_list_functions(edsl_hip_module *m, char *buf, size_t len);
+
+/* MLIRCompiler::clear: forget every function. Function pointers handed out
+ * before stop being bound (calling one records an error). */
+void edsl_hip_module_clear(edsl_hip_module *m);
+
+/* MLIRCompiler::getFunctionPointer (cpp/src/MLIRCompiler.cpp:277-280): an
+ * entry point with the calling convention of the reference's JIT'd symbol
+ * for this function -- each parameter's expanded memref descriptor in the
+ * FunctionDef's parameter order, then the out-param descriptor, void return
+ * (reference mlir_edsl/backend.py:162-198). NULL (with an error recorded) for
+ * an unknown name ("Function not compiled: <name>", as
+ * cpp/src/MLIRExecutor.cpp:109-115). The pointer records errors for
+ * edsl_hip_last_error() and prints them to stderr, the JIT'd symbol having no
+ * error channel. Pointers exist for the 14-, 19-, 21- and 26-argument forms
+ * (every dense program whose parameters are all used); at most 256 functions
+ * hold one at a time per process. */
+void *edsl_hip_module_get_function_pointer(edsl_hip_module *m, const char *name);
+
+/* MLIRCompiler::executeGPUFunction (cpp/src/MLIRCompiler.cpp:352-461), bound
+ * as execute_gpu_function(name, inputs, output_shape, element_size)
+ * (cpp/src/python_bindings.cpp:69-97): contiguous row-major inputs given as
+ * (pointer, shape) pairs in parameter order, one contiguous output; host or
+ * device memory; synchronous on return. */
+int edsl_hip_module_execute_gpu_function(edsl_hip_module *m, const char *name, int num_inputs,
+                                         const void *const *input_ptrs,
+                                         const int64_t *const *input_shapes, const int *input_ranks,
+                                         void *output, const int64_t *output_shape, int output_rank,
+                                         size_t element_size);
+
+/* MLIRCompiler::getModuleIR counterpart: a text listing of the compiled
+ * functions (signature and the dense form each was matched to). */
+int edsl_hip_module_describe(edsl_hip_module *m, char *buf, size_t len);
+
+/* MLIRCompiler::getFailureIR counterpart: the message of the last failed
+ * compile_function on this module, empty after a success or clear(). */
+int edsl_hip_module_last_failure(edsl_hip_module *m, char *buf, size_t len);
+
+/* How a compiled function was matched: dtype (EDSL_DTYPE_*), epilogue
+ * (EDSL_EPI_*), leaky alpha, the parameter indices of X, W and b (-1 when
+ * there is no bias), and the form as text ("relu(X @ W + b)"). Any output
+ * pointer may be NULL. No reference counterpart: for tests and tools. */
+int edsl_hip_module_function_form(edsl_hip_module *m, const char *name, int *dtype, int *epilogue,
+                                  float *alpha, int *x_param, int *w_param, int *b_param, char *form,
+                                  size_t form_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EDSL_HIP_PROGRAM_H */

@@ -29,26 +29,12 @@
 #include "../../include/edsl_hip_device.h"
 #include "common.hpp"
 #include "kernels.hpp"
+#include "runtime_internal.hpp"
 
-namespace {
-
-using namespace edsl;
+namespace edsl {
+namespace rt {
 
 // ------------------------------------------------------------------ errors
-enum ErrorCode : int {
-  kErrShape = -1,     // sizes inconsistent with the op
-  kErrStride = -2,    // unsupported stride / layout
-  kErrDtype = -3,     // element type / size
-  kErrArgument = -4,  // null pointer, bad pattern, bad epilogue
-  kErrLimit = -5,     // size beyond what the kernels index
-  kErrInternal = -6,
-};
-
-struct Failure {
-  int code;
-  std::string msg;
-};
-
 thread_local int t_err_code = 0;
 thread_local std::string t_err_msg;
 thread_local std::string t_plan;
@@ -64,26 +50,6 @@ thread_local std::string t_plan;
 
 void check_hip(hipError_t e, const char* what) {
   if (e != hipSuccess) fail((int)e, "%s failed: %s", what, hipGetErrorString(e));
-}
-
-template <typename F>
-int guarded(F&& f) {
-  t_err_code = 0;
-  t_err_msg.clear();
-  try {
-    f();
-    return 0;
-  } catch (const Failure& e) {
-    t_err_code = e.code;
-    t_err_msg = e.msg;
-  } catch (const std::exception& e) {
-    t_err_code = kErrInternal;
-    t_err_msg = e.what();
-  } catch (...) {
-    t_err_code = kErrInternal;
-    t_err_msg = "unknown error";
-  }
-  return t_err_code;
 }
 
 void set_plan(const char* fmt, ...) {
@@ -173,16 +139,6 @@ DeviceState& device_state(int* dev_out) {
 }
 
 // ---------------------------------------------------------- operand views
-struct Mat {
-  char* base = nullptr;  // aligned + offset
-  int64_t rows = 0, cols = 0, ld = 0;
-};
-
-struct Vec {
-  char* base = nullptr;
-  int64_t n = 0;
-};
-
 Mat mat_from_desc(void* aligned, int64_t offset, int64_t d0, int64_t d1, int64_t s0, int64_t s1,
                   size_t esize, const char* name) {
   if (d0 < 0 || d1 < 0) fail(kErrShape, "%s: negative size (%lld, %lld)", name, (long long)d0, (long long)d1);
@@ -518,7 +474,11 @@ void sync_dense(int dtype, int epi, float alpha, const Mat& X, const Mat& W, con
   check_hip(hipGetLastError(), "kernel execution");
 }
 
-}  // namespace
+}  // namespace rt
+}  // namespace edsl
+
+using namespace edsl;
+using namespace edsl::rt;
 
 // ====================================================================== ABI
 #define MEMREF2(T, p) \

@@ -1,0 +1,81 @@
+// Internal interface between the C-ABI runtime (runtime.cpp) and the
+// FunctionDef front end (program.cpp). Not installed; not part of the ABI.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <exception>
+#include <string>
+
+namespace edsl {
+namespace rt {
+
+// Error codes returned by the C ABI (edsl_hip_last_error). HIP errors are
+// reported with their positive hipError_t value.
+enum ErrorCode : int {
+  kErrShape = -1,     // sizes inconsistent with the op
+  kErrStride = -2,    // unsupported stride / layout
+  kErrDtype = -3,     // element type / size
+  kErrArgument = -4,  // null pointer, bad pattern, bad epilogue
+  kErrLimit = -5,     // size beyond what the kernels index
+  kErrInternal = -6,
+  kErrProgram = -7,   // FunctionDef that is malformed or not a dense-path program
+  kErrUnknown = -8,   // function name not compiled in the module
+};
+
+struct Failure {
+  int code;
+  std::string msg;
+};
+
+extern thread_local int t_err_code;
+extern thread_local std::string t_err_msg;
+
+[[noreturn]] void fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Runs f, turning a thrown Failure (or any exception) into the thread's last
+// error; returns 0 or the error code.
+template <typename F>
+int guarded(F&& f) {
+  t_err_code = 0;
+  t_err_msg.clear();
+  try {
+    f();
+    return 0;
+  } catch (const Failure& e) {
+    t_err_code = e.code;
+    t_err_msg = e.msg;
+  } catch (const std::exception& e) {
+    t_err_code = kErrInternal;
+    t_err_msg = e.what();
+  } catch (...) {
+    t_err_code = kErrInternal;
+    t_err_msg = "unknown error";
+  }
+  return t_err_code;
+}
+
+int copy_out(const std::string& s, char* buf, size_t len);
+
+// A 2-D operand: element (r, c) at base + (r*ld + c) * element size.
+struct Mat {
+  char* base = nullptr;  // aligned + offset
+  int64_t rows = 0, cols = 0, ld = 0;
+};
+
+struct Vec {
+  char* base = nullptr;
+  int64_t n = 0;
+};
+
+Mat mat_from_desc(void* aligned, int64_t offset, int64_t d0, int64_t d1, int64_t s0, int64_t s1,
+                  size_t esize, const char* name);
+Vec vec_from_desc(void* aligned, int64_t offset, int64_t d0, int64_t s0, size_t esize, const char* name);
+
+// Y = epilogue(X @ W (+ b)) on the current device, host or device operands,
+// synchronous on return. dtype is EDSL_DTYPE_*, epi an EDSL_EPI_* code.
+void sync_dense(int dtype, int epi, float alpha, const Mat& X, const Mat& W, const Vec* b, const Mat& Y);
+
+}  // namespace rt
+}  // namespace edsl

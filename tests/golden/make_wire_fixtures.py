@@ -1,0 +1,379 @@
+"""Writes tests/golden/wire/*.pb and tests/golden/wire_fixtures.json.
+
+Wire fixtures for the FunctionDef front end (ml-edsl_amd/csrc/program.cpp):
+the exact bytes the reference Python front end serializes for dense-path
+programs (and for programs outside the path, which must be rejected), plus
+the arguments its backend passes to execute_gpu_function.
+
+Nothing else pins those bytes (node-id numbering, LetBinding reuse, proto3
+default-value omission), so this script -- run once, in the container that
+holds the reference, never by the tests -- imports the reference front end
+from /root/reference and drives it end to end: @ml_function(target="gpu"),
+the first call, signature specialisation, AST validation, serialization in
+CppMLIRBackend (reference mlir_edsl/backend.py:123-151). The pybind module is
+replaced by a recorder that keeps the FunctionDef bytes and the
+execute_gpu_function arguments (reference mlir_edsl/backend.py:248-271).
+
+The reference's generated protobuf module (ast_pb2, made by protoc at the
+reference's build time) is rebuilt here from the schema text
+cpp/schemas/ast.proto with the protobuf runtime: a small parser turns the
+.proto file into a FileDescriptorProto, so field numbers and enum values
+come from the schema itself. Only data is written: the .pb files and a JSON
+index with each program's source text and the dense form it must decode to.
+
+Run from the repository root:  python tests/golden/make_wire_fixtures.py
+"""
+
+import inspect
+import json
+import os
+import re
+import sys
+import textwrap
+import types
+
+import numpy as np
+from google.protobuf import descriptor_pb2, descriptor_pool, message_factory
+from google.protobuf.internal import enum_type_wrapper
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REFERENCE = os.environ.get("EDSL_REFERENCE", "/root/reference")
+SCHEMA = os.path.join(REFERENCE, "cpp", "schemas", "ast.proto")
+OUT_DIR = os.path.join(HERE, "wire")
+
+_SCALARS = {
+    "int32": descriptor_pb2.FieldDescriptorProto.TYPE_INT32,
+    "int64": descriptor_pb2.FieldDescriptorProto.TYPE_INT64,
+    "float": descriptor_pb2.FieldDescriptorProto.TYPE_FLOAT,
+    "bool": descriptor_pb2.FieldDescriptorProto.TYPE_BOOL,
+    "string": descriptor_pb2.FieldDescriptorProto.TYPE_STRING,
+}
+
+
+# ------------------------------------------------------------ .proto parser
+def _tokens(text: str) -> list[str]:
+    text = re.sub(r"//[^\n]*", " ", text)
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    return re.findall(r'"[^"]*"|[A-Za-z_][\w.]*|\d+|[{}=;\[\]<>,-]', text)
+
+
+def parse_proto(text: str) -> descriptor_pb2.FileDescriptorProto:
+    """proto3 subset used by the schema: package, messages (nested enums,
+    oneofs, repeated, reserved), top-level enums."""
+    toks = _tokens(text)
+    fdp = descriptor_pb2.FileDescriptorProto(name="ast.proto", syntax="proto3")
+    pos = 0
+
+    def take(expected=None):
+        nonlocal pos
+        t = toks[pos]
+        pos += 1
+        if expected is not None and t != expected:
+            raise SyntaxError(f"expected {expected!r}, got {t!r} at token {pos}")
+        return t
+
+    def parse_enum(ed):
+        take("{")
+        while toks[pos] != "}":
+            name = take()
+            take("=")
+            neg = toks[pos] == "-"
+            if neg:
+                take()
+            num = int(take())
+            take(";")
+            ed.value.add(name=name, number=-num if neg else num)
+        take("}")
+
+    def parse_message(md):
+        take("{")
+        oneof_index = None
+        depth_stack = []
+        while True:
+            t = take()
+            if t == "}":
+                if depth_stack:
+                    depth_stack.pop()
+                    oneof_index = None
+                    continue
+                return
+            if t == "enum":
+                parse_enum(md.enum_type.add(name=take()))
+            elif t == "message":
+                parse_message(md.nested_type.add(name=take()))
+            elif t == "oneof":
+                md.oneof_decl.add(name=take())
+                take("{")
+                oneof_index = len(md.oneof_decl) - 1
+                depth_stack.append("oneof")
+            elif t == "reserved":
+                while take() != ";":
+                    pass
+            else:
+                label = descriptor_pb2.FieldDescriptorProto.LABEL_OPTIONAL
+                ftype = t
+                if t == "repeated":
+                    label = descriptor_pb2.FieldDescriptorProto.LABEL_REPEATED
+                    ftype = take()
+                fname = take()
+                take("=")
+                num = int(take())
+                take(";")
+                fd = md.field.add(name=fname, number=num, label=label)
+                if ftype in _SCALARS:
+                    fd.type = _SCALARS[ftype]
+                else:
+                    fd.type_name = ftype  # resolved below
+                if oneof_index is not None:
+                    fd.oneof_index = oneof_index
+
+    while pos < len(toks):
+        t = take()
+        if t == "syntax":
+            take("=")
+            take()
+            take(";")
+        elif t == "package":
+            fdp.package = take()
+            take(";")
+        elif t == "enum":
+            parse_enum(fdp.enum_type.add(name=take()))
+        elif t == "message":
+            parse_message(fdp.message_type.add(name=take()))
+        else:
+            raise SyntaxError(f"unexpected token {t!r}")
+
+    # resolve type names: message, top-level enum, or enum nested in this message
+    enums = {e.name for e in fdp.enum_type}
+    messages = {m.name for m in fdp.message_type}
+    for md in fdp.message_type:
+        nested = {e.name for e in md.enum_type}
+        for fd in md.field:
+            if not fd.type_name:
+                continue
+            n = fd.type_name
+            if n in nested:
+                fd.type = descriptor_pb2.FieldDescriptorProto.TYPE_ENUM
+                fd.type_name = f".{fdp.package}.{md.name}.{n}"
+            elif n in enums:
+                fd.type = descriptor_pb2.FieldDescriptorProto.TYPE_ENUM
+                fd.type_name = f".{fdp.package}.{n}"
+            elif n in messages:
+                fd.type = descriptor_pb2.FieldDescriptorProto.TYPE_MESSAGE
+                fd.type_name = f".{fdp.package}.{n}"
+            else:
+                raise SyntaxError(f"unknown type {n} in {md.name}.{fd.name}")
+    return fdp
+
+
+def build_ast_pb2(schema_path: str) -> types.ModuleType:
+    """A stand-in for the protoc-generated module: message classes, top-level
+    enum wrappers and their values as module attributes."""
+    with open(schema_path) as f:
+        fdp = parse_proto(f.read())
+    pool = descriptor_pool.DescriptorPool()
+    fd = pool.Add(fdp)
+    mod = types.ModuleType("mlir_edsl.ast_pb2")
+    for md in fdp.message_type:
+        cls = message_factory.GetMessageClass(pool.FindMessageTypeByName(f"{fdp.package}.{md.name}"))
+        for ed in md.enum_type:  # nested enum values as class attributes, as protoc emits them
+            for v in ed.value:
+                if not hasattr(cls, v.name):
+                    setattr(cls, v.name, v.number)
+        setattr(mod, md.name, cls)
+    for ed in fdp.enum_type:
+        setattr(mod, ed.name, enum_type_wrapper.EnumTypeWrapper(pool.FindEnumTypeByName(f"{fdp.package}.{ed.name}")))
+        for v in ed.value:
+            setattr(mod, v.name, v.number)
+    mod.DESCRIPTOR = fd
+    return mod
+
+
+# ------------------------------------------------------ recording backend
+class Recorder:
+    """Stands in for the pybind MLIRCompiler: keeps what the front end sends."""
+
+    compiled: dict[str, bytes] = {}
+    gpu_calls: dict[str, dict] = {}
+
+    def __init__(self):
+        self._names: set[str] = set()
+
+    def compile_function(self, function_def_bytes):
+        from mlir_edsl import ast_pb2
+        fd = ast_pb2.FunctionDef()
+        fd.ParseFromString(function_def_bytes)
+        Recorder.compiled[fd.name] = bytes(function_def_bytes)
+        self._names.add(fd.name)
+
+    def has_function(self, name):
+        return name in self._names
+
+    def list_functions(self):
+        return sorted(self._names)
+
+    def set_target(self, target):
+        pass
+
+    def set_optimization_level(self, level):
+        pass
+
+    def clear(self):
+        self._names.clear()
+
+    def execute_gpu_function(self, name, inputs, output_shape, element_size):
+        Recorder.gpu_calls[name] = {"input_shapes": [list(s) for _, s in inputs],
+                                    "output_shape": list(output_shape), "element_size": element_size}
+        n = 1
+        for d in output_shape:
+            n *= d
+        return bytes(n * element_size)
+
+
+def load_reference_front_end():
+    sys.modules["mlir_edsl.ast_pb2"] = build_ast_pb2(SCHEMA)
+    sys.path.insert(0, REFERENCE)
+    import mlir_edsl
+    import mlir_edsl.backend as be
+    mlir_edsl.ast_pb2 = sys.modules["mlir_edsl.ast_pb2"]
+    be._mlir_backend = types.SimpleNamespace(MLIRCompiler=Recorder)
+    be.HAS_CPP_BACKEND = True
+    be._global_backend = None
+    return mlir_edsl
+
+
+# ---------------------------------------------------------------- programs
+def programs(E):
+    """(fixture name, python function, expected decode or rejection)."""
+    Tensor, f32, i32 = E.Tensor, E.f32, E.i32
+    relu, leaky_relu, tensor_map, If, matmul = E.relu, E.leaky_relu, E.tensor_map, E.If, E.matmul
+    out = []
+
+    def dense_relu(X: Tensor[f32, 16, 64], W: Tensor[f32, 64, 32], b: Tensor[f32, 32]) -> Tensor[f32, 16, 32]:
+        return relu(X @ W + b)
+    out.append(("dense_relu_f32", dense_relu, {"form": "relu(X @ W + b)", "dtype": "f32", "x": 0, "w": 1, "b": 2, "epilogue": 3}))
+
+    def dense_bias(X: Tensor[f32, 8, 24], W: Tensor[f32, 24, 40], b: Tensor[f32, 40]) -> Tensor[f32, 8, 40]:
+        return matmul(X, W) + b
+    out.append(("matmul_bias_f32", dense_bias, {"form": "X @ W + b", "dtype": "f32", "x": 0, "w": 1, "b": 2, "epilogue": 1}))
+
+    def mm(A: Tensor[f32, 32, 48], B: Tensor[f32, 48, 16]) -> Tensor[f32, 32, 16]:
+        return matmul(A, B)
+    out.append(("matmul_f32", mm, {"form": "A @ B", "dtype": "f32", "x": 0, "w": 1, "b": -1, "epilogue": 0}))
+
+    def mm_op(A: Tensor[i32, 4, 4], B: Tensor[i32, 4, 4]) -> Tensor[i32, 4, 4]:
+        return A @ B
+    out.append(("matmul_i32", mm_op, {"form": "A @ B", "dtype": "i32", "x": 0, "w": 1, "b": -1, "epilogue": 0}))
+
+    def mm_relu(A: Tensor[f32, 64, 64], B: Tensor[f32, 64, 64]) -> Tensor[f32, 64, 64]:
+        return relu(A @ B)
+    out.append(("matmul_relu_f32", mm_relu, {"form": "relu(A @ B)", "dtype": "f32", "x": 0, "w": 1, "b": -1, "epilogue": 2}))
+
+    def leaky(X: Tensor[f32, 16, 32], W: Tensor[f32, 32, 64], b: Tensor[f32, 64]) -> Tensor[f32, 16, 64]:
+        return leaky_relu(X @ W + b, 0.2)
+    out.append(("dense_leaky_f32", leaky, {"form": "leaky_relu(X @ W + b, 0.2)", "dtype": "f32", "x": 0, "w": 1, "b": 2, "epilogue": 5, "alpha": 0.2}))
+
+    def leaky_default(X: Tensor[f32, 16, 32], W: Tensor[f32, 32, 64], b: Tensor[f32, 64]) -> Tensor[f32, 16, 64]:
+        return leaky_relu(X @ W + b)
+    out.append(("dense_leaky_default_f32", leaky_default, {"dtype": "f32", "x": 0, "w": 1, "b": 2, "epilogue": 5}))
+
+    def int_relu(X: Tensor[i32, 32, 64], W: Tensor[i32, 64, 32], b: Tensor[i32, 32]) -> Tensor[i32, 32, 32]:
+        return tensor_map(X @ W + b, lambda v: If(v > 0, v, 0))
+    out.append(("dense_relu_i32_tensor_map", int_relu, {"form": "relu(X @ W + b)", "dtype": "i32", "x": 0, "w": 1, "b": 2, "epilogue": 3}))
+
+    def int_relu_mm(A: Tensor[i32, 16, 16], B: Tensor[i32, 16, 16]) -> Tensor[i32, 16, 16]:
+        return tensor_map(A @ B, lambda v: If(v < 0, 0, v))
+    out.append(("matmul_relu_i32_tensor_map", int_relu_mm, {"form": "relu(A @ B)", "dtype": "i32", "x": 0, "w": 1, "b": -1, "epilogue": 2}))
+
+    def bias_left(b: Tensor[f32, 32], X: Tensor[f32, 16, 8], W: Tensor[f32, 8, 32]) -> Tensor[f32, 16, 32]:
+        return relu(b + X @ W)
+    out.append(("dense_relu_bias_left_params_reordered", bias_left, {"form": "relu(X @ W + b)", "dtype": "f32", "x": 1, "w": 2, "b": 0, "epilogue": 3}))
+
+    def shared_operand(A: Tensor[f32, 32, 32]) -> Tensor[f32, 32, 32]:
+        return relu(A @ A)
+    out.append(("matmul_relu_same_operand", shared_operand, {"form": "relu(A @ A)", "dtype": "f32", "x": 0, "w": 0, "b": -1, "epilogue": 2}))
+
+    def bench_dense(X: Tensor[f32, 1024, 1024], W: Tensor[f32, 1024, 1024], b: Tensor[f32, 1024]) -> Tensor[f32, 1024, 1024]:
+        return relu(X @ W + b)
+    out.append(("dense_relu_f32_1024", bench_dense, {"form": "relu(X @ W + b)", "dtype": "f32", "x": 0, "w": 1, "b": 2, "epilogue": 3}))
+
+    # outside the dense path: must be rejected at compile time
+    def sub_bias(X: Tensor[f32, 4, 4], W: Tensor[f32, 4, 4], b: Tensor[f32, 4]) -> Tensor[f32, 4, 4]:
+        return X @ W - b
+    out.append(("reject_sub_bias", sub_bias, {"reject": "only the bias add is fused"}))
+
+    def map_scale(X: Tensor[f32, 4, 4], W: Tensor[f32, 4, 4]) -> Tensor[f32, 4, 4]:
+        return tensor_map(X @ W, lambda v: v * 2.0)
+    out.append(("reject_map_scale", map_scale, {"reject": "tensor_map body is not If"}))
+
+    def f32_if_relu(X: Tensor[f32, 4, 4], W: Tensor[f32, 4, 4]) -> Tensor[f32, 4, 4]:
+        return tensor_map(X @ W, lambda v: If(v > 0.0, v, 0.0))
+    out.append(("reject_f32_if_relu", f32_if_relu, {"reject": "maps NaN to 0"}))
+
+    def relu_of_param(X: Tensor[f32, 4, 4]) -> Tensor[f32, 4, 4]:
+        return relu(X)
+    out.append(("reject_relu_of_parameter", relu_of_param, {"reject": "not a dense-path program"}))
+
+    def int_relu_activation(X: Tensor[i32, 4, 4], W: Tensor[i32, 4, 4]) -> Tensor[i32, 4, 4]:
+        return relu(X @ W)
+    out.append(("reject_i32_relu_activation", int_relu_activation, {"reject": "float-only"}))
+
+    def chained(X: Tensor[f32, 4, 4], W1: Tensor[f32, 4, 4], W2: Tensor[f32, 4, 4]) -> Tensor[f32, 4, 4]:
+        return relu(relu(X @ W1) @ W2)
+    out.append(("reject_two_layers", chained, {"reject": "not a function parameter"}))
+
+    def scalar_add(x: int) -> int:
+        return E.add(x, 1)
+    out.append(("reject_scalar_function", scalar_add, {"reject": "not a dense-path program"}))
+    return out
+
+
+def sample_args(fn):
+    args = []
+    for name, t in list(fn.__annotations__.items()):
+        if name == "return":
+            continue
+        if t is int:
+            args.append(3)
+            continue
+        shape = tuple(t.shape)
+        dt = np.float32 if t.element_type.name == "f32" else np.int32
+        args.append(np.zeros(shape, dtype=dt))
+    return args
+
+
+def main():
+    E = load_reference_front_end()
+    os.makedirs(OUT_DIR, exist_ok=True)
+    index = []
+    for fixture, pyfn, expected in programs(E):
+        mlfn = E.ml_function(target="gpu")(pyfn)
+        args = sample_args(pyfn)
+        err = None
+        try:
+            mlfn(*args)
+        except Exception as e:  # the recorder still saw compile_function
+            err = f"{type(e).__name__}: {e}"
+        name = mlfn.signature.name
+        data = Recorder.compiled.get(name)
+        if data is None:
+            raise RuntimeError(f"{fixture}: the front end did not serialize {name} ({err})")
+        with open(os.path.join(OUT_DIR, f"{fixture}.pb"), "wb") as f:
+            f.write(data)
+        entry = {"fixture": fixture, "file": f"wire/{fixture}.pb", "function": name,
+                 "source": textwrap.dedent(inspect.getsource(pyfn)).strip(),
+                 "param_shapes": [list(a.shape) if hasattr(a, "shape") else [] for a in args],
+                 "param_dtypes": [str(a.dtype) if hasattr(a, "dtype") else "int" for a in args],
+                 "expected": expected}
+        if name in Recorder.gpu_calls:
+            entry["execute_gpu_function"] = Recorder.gpu_calls[name]
+        index.append(entry)
+        print(f"{fixture}: {name}, {len(data)} bytes", flush=True)
+    with open(os.path.join(HERE, "wire_fixtures.json"), "w") as f:
+        json.dump({"generator": "tests/golden/make_wire_fixtures.py (reference front end, "
+                                "mlir_edsl/backend.py serialization)",
+                   "schema": "cpp/schemas/ast.proto", "cases": index}, f, indent=1)
+
+
+if __name__ == "__main__":
+    main()

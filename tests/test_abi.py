@@ -22,7 +22,8 @@ def declared_functions():
     for h in HEADERS:
         text = open(h).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-        names += re.findall(r"^\s*(?:void|int)\s+(edsl_hip_\w+)\s*\(", text, flags=re.M)
+        names += re.findall(r"^\s*(?:void|int|edsl_hip_module)\s*\**\s*(edsl_hip_\w+)\s*\(", text,
+                            flags=re.M)
     return names
 
 
@@ -32,6 +33,9 @@ def test_headers_declare_the_boundary():
         assert n in names
     assert "edsl_hip_execute_gpu_function" in names
     assert "edsl_hip_last_error" in names
+    for n in ("edsl_hip_module_create", "edsl_hip_module_get_function_pointer",
+              "edsl_hip_module_compile_function", "edsl_hip_module_execute_gpu_function"):
+        assert n in names
     assert len(names) == len(set(names))
 
 

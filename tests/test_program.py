@@ -1,0 +1,253 @@
+"""FunctionDef front end (include/edsl_hip_program.h), host side only.
+
+The fixtures are the exact bytes the reference Python front end serializes
+(tests/golden/make_wire_fixtures.py drove it end to end); each must decode to
+the dense form its program spells, or be rejected with a reason. Nothing here
+touches a GPU: decoding, matching, descriptor and shape validation all happen
+before any device call.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+
+import numpy as np
+import pytest
+
+from mlir_edsl_hip import _native
+from mlir_edsl_hip._mlir_backend import MLIRCompiler
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _cases():
+    with open(os.path.join(GOLDEN, "wire_fixtures.json")) as f:
+        return json.load(f)["cases"]
+
+
+def _bytes(case) -> bytes:
+    with open(os.path.join(GOLDEN, case["file"]), "rb") as f:
+        return f.read()
+
+
+DENSE = [c for c in _cases() if "reject" not in c["expected"]]
+REJECT = [c for c in _cases() if "reject" in c["expected"]]
+
+
+@pytest.fixture
+def compiler():
+    c = MLIRCompiler()
+    yield c
+    c.clear()
+
+
+@pytest.mark.parametrize("case", DENSE, ids=lambda c: c["fixture"])
+def test_reference_front_end_bytes_decode_to_their_dense_form(case, compiler):
+    compiler.compile_function(_bytes(case))
+    assert compiler.has_function(case["function"])
+    got = compiler.function_form(case["function"])
+    exp = case["expected"]
+    for key in ("form", "dtype", "x", "w", "b", "epilogue"):
+        if key in exp:
+            assert got[key] == exp[key], (key, got, exp)
+    if "alpha" in exp:
+        assert got["alpha"] == pytest.approx(exp["alpha"], rel=1e-7)
+    assert compiler.get_function_pointer(case["function"]) != 0
+
+
+@pytest.mark.parametrize("case", REJECT, ids=lambda c: c["fixture"])
+def test_programs_outside_the_dense_path_are_rejected(case, compiler):
+    with pytest.raises(RuntimeError, match=case["expected"]["reject"]):
+        compiler.compile_function(_bytes(case))
+    assert not compiler.has_function(case["function"])
+    assert case["expected"]["reject"] in compiler.get_failure_ir()
+
+
+def test_leaky_default_alpha_is_the_front_end_default(compiler):
+    case = next(c for c in DENSE if c["fixture"] == "dense_leaky_default_f32")
+    compiler.compile_function(_bytes(case))
+    assert compiler.function_form(case["function"])["alpha"] == pytest.approx(0.01, rel=1e-7)
+
+
+def test_registry_semantics(compiler):
+    for c in DENSE[:4]:
+        compiler.compile_function(_bytes(c))
+    names = compiler.list_functions()
+    assert names == sorted(c["function"] for c in DENSE[:4])
+    with pytest.raises(RuntimeError, match="already compiled"):
+        compiler.compile_function(_bytes(DENSE[0]))
+    ptrs = {compiler.get_function_pointer(n) for n in names}
+    assert len(ptrs) == len(names)
+    ir = compiler.get_module_ir()
+    assert all(f"func @{n}(" in ir for n in names)
+    compiler.clear()
+    assert compiler.list_functions() == [] and not compiler.has_function(names[0])
+
+
+def test_unknown_function_pointer(compiler):
+    with pytest.raises(RuntimeError, match="Function not compiled: nope"):
+        compiler.get_function_pointer("nope")
+
+
+def test_injected_failure_like_the_reference(compiler):
+    # reference tests/core/test_ir_inspection.py:22-36
+    case = DENSE[0]
+    compiler.compile_function(_bytes(case))
+    assert compiler.get_failure_ir() == ""
+    compiler.inject_test_failure()
+    with pytest.raises(RuntimeError, match="Lowering pipeline failed"):
+        compiler.get_function_pointer(case["function"])
+    fir = compiler.get_failure_ir()
+    assert "__test_failure_inject__" in fir and case["function"] in fir
+    assert case["function"] in compiler.get_module_ir()
+    compiler.clear()
+    assert compiler.get_failure_ir() == ""
+
+
+def test_every_truncation_is_an_error_never_a_crash(compiler):
+    data = _bytes(next(c for c in DENSE if c["fixture"] == "dense_relu_i32_tensor_map"))
+    for n in range(len(data)):
+        try:
+            compiler.compile_function(data[:n])
+        except RuntimeError:
+            pass
+        compiler.clear()
+
+
+def test_random_corruption_is_an_error_never_a_crash(compiler):
+    rng = np.random.default_rng(0)
+    cases = [_bytes(c) for c in _cases()]
+    for trial in range(3000):
+        data = bytearray(cases[trial % len(cases)])
+        for _ in range(1 + trial % 3):
+            data[rng.integers(len(data))] = rng.integers(256)
+        try:
+            compiler.compile_function(bytes(data))
+        except RuntimeError:
+            pass
+        compiler.clear()
+
+
+def _varint(v: int) -> bytes:
+    out = bytearray()
+    while True:
+        b = v & 0x7F
+        v >>= 7
+        out.append(b | (0x80 if v else 0))
+        if not v:
+            return bytes(out)
+
+
+def test_unknown_fields_are_skipped(compiler):
+    case = next(c for c in DENSE if c["fixture"] == "dense_relu_f32")
+    data = _bytes(case)
+    extra = (_varint(15 << 3 | 0) + _varint(123456789)           # varint
+             + _varint(16 << 3 | 1) + bytes(8)                    # fixed64
+             + _varint(17 << 3 | 2) + _varint(3) + b"abc"         # length-delimited
+             + _varint(18 << 3 | 5) + bytes(4))                   # fixed32
+    compiler.compile_function(extra + data)
+    assert compiler.function_form(case["function"])["form"] == case["expected"]["form"]
+
+
+def test_group_wire_type_is_rejected(compiler):
+    with pytest.raises(RuntimeError, match="wire type"):
+        compiler.compile_function(_varint(15 << 3 | 3) + _bytes(DENSE[0]))
+
+
+def test_execute_checks_shapes_before_any_device_call(compiler):
+    case = next(c for c in DENSE if c["fixture"] == "dense_relu_f32")
+    compiler.compile_function(_bytes(case))
+    X = np.zeros((16, 64), np.float32)
+    W = np.zeros((64, 33), np.float32)  # compiled for 64 x 32
+    b = np.zeros(32, np.float32)
+    with pytest.raises(RuntimeError, match="shape"):
+        compiler.execute_gpu_function(case["function"], [(a.ctypes.data, list(a.shape)) for a in (X, W, b)],
+                                      [16, 32], 4)
+    with pytest.raises(RuntimeError, match="element_size"):
+        compiler.execute_gpu_function(case["function"], [(a.ctypes.data, list(a.shape)) for a in (X, X, b)],
+                                      [16, 32], 8)
+    with pytest.raises(RuntimeError, match="takes 3 inputs"):
+        compiler.execute_gpu_function(case["function"], [(X.ctypes.data, [16, 64])], [16, 32], 4)
+
+
+def _descriptor(a):
+    return [a.ctypes.data, a.ctypes.data, 0] + list(a.shape) + [s // a.itemsize for s in a.strides]
+
+
+def test_function_pointer_validates_descriptors_before_any_device_call(compiler):
+    case = next(c for c in DENSE if c["fixture"] == "dense_relu_f32")
+    compiler.compile_function(_bytes(case))
+    ptr = compiler.get_function_pointer(case["function"])
+    X = np.zeros((16, 64), np.float32)
+    W = np.zeros((64, 40), np.float32)  # wrong N
+    b = np.zeros(32, np.float32)
+    Y = np.zeros((16, 32), np.float32)
+    args = _descriptor(X) + _descriptor(W) + _descriptor(b) + _descriptor(Y)
+    assert len(args) == 26
+    ctypes.CFUNCTYPE(None, *([ctypes.c_int64] * 26))(ptr)(*args)
+    code, msg = _native.last_error()
+    assert code == -1 and "compiled for 32" in msg
+
+
+def test_stale_function_pointer_after_clear(compiler):
+    case = next(c for c in DENSE if c["fixture"] == "matmul_f32")
+    compiler.compile_function(_bytes(case))
+    ptr = compiler.get_function_pointer(case["function"])
+    compiler.clear()
+    A = np.zeros((32, 48), np.float32)
+    B = np.zeros((48, 16), np.float32)
+    C = np.zeros((32, 16), np.float32)
+    ctypes.CFUNCTYPE(None, *([ctypes.c_int64] * 21))(ptr)(*(_descriptor(A) + _descriptor(B) + _descriptor(C)))
+    code, msg = _native.last_error()
+    assert code == -8 and "no longer bound" in msg
+
+
+def _ld(field: int, payload: bytes) -> bytes:
+    return _varint(field << 3 | 2) + _varint(len(payload)) + payload
+
+
+def _tensor_type(shape, kind) -> bytes:
+    # TypeSpec{tensor: TensorTypeSpec{shape (packed int64), element_type: TypeSpec{scalar{kind}}}}
+    packed = b"".join(_varint(d & ((1 << 64) - 1)) for d in shape)
+    scalar = _ld(1, _varint(1 << 3 | 0) + _varint(kind)) if kind else _ld(1, b"")
+    return _ld(3, _ld(1, packed) + _ld(2, scalar))
+
+
+def _param_node(name, shape, kind) -> bytes:
+    # ASTNode{function: FunctionNode{parameter: Parameter{name, type}}}
+    return _ld(4, _ld(1, _ld(1, name.encode()) + _ld(2, _tensor_type(shape, kind))))
+
+
+def _matmul_def(name, a_shape, b_shape, out_shape, kind=1) -> bytes:
+    body = _ld(7, _ld(2, _ld(1, _param_node("A", a_shape, kind)) + _ld(2, _param_node("B", b_shape, kind))
+                      + _ld(3, _tensor_type(out_shape, kind))))
+    return (_ld(1, name.encode())
+            + _ld(2, _ld(1, b"A") + _ld(2, _tensor_type(a_shape, kind)))
+            + _ld(2, _ld(1, b"B") + _ld(2, _tensor_type(b_shape, kind)))
+            + _ld(3, _tensor_type(out_shape, kind)) + _ld(4, body))
+
+
+def test_hand_encoded_matmul_decodes(compiler):
+    """Cross-check of the field layout with an encoder written from the
+    schema (not the reference front end): same result as the fixtures."""
+    compiler.compile_function(_matmul_def("hand_mm", [8, 4], [4, 2], [8, 2]))
+    f = compiler.function_form("hand_mm")
+    assert (f["form"], f["dtype"], f["x"], f["w"], f["b"]) == ("A @ B", "f32", 0, 1, -1)
+    compiler.compile_function(_matmul_def("hand_mm_i32", [8, 4], [4, 2], [8, 2], kind=0))
+    assert compiler.function_form("hand_mm_i32")["dtype"] == "i32"
+
+
+def test_dynamic_dimensions_are_rejected_like_the_reference(compiler):
+    # reference cpp/src/MLIRBuilder.cpp:478-486
+    with pytest.raises(RuntimeError, match="Dynamic tensor dimensions not supported"):
+        compiler.compile_function(_matmul_def("dyn_mm", [-1, 4], [4, 2], [-1, 2]))
+
+
+def test_shape_mismatches_are_rejected(compiler):
+    with pytest.raises(RuntimeError, match="inner dimensions must match"):
+        compiler.compile_function(_matmul_def("bad_k", [8, 4], [5, 2], [8, 2]))
+    with pytest.raises(RuntimeError, match="return type"):
+        compiler.compile_function(_matmul_def("bad_ret", [8, 4], [4, 2], [8, 3]))
+    with pytest.raises(RuntimeError, match="f32 or i32"):
+        compiler.compile_function(_matmul_def("bad_elem", [8, 4], [4, 2], [8, 2], kind=2))
