@@ -9,9 +9,11 @@
  * programs only:
  *
  *   matmul(A, B) / A @ B, relu(A @ B), X @ W + b, relu(X @ W + b),
- *   leaky_relu(X @ W + b, alpha), and tensor_map(X @ W [+ b],
- *   lambda v: If(v > 0, v, 0)) over i32 -- X, W, b being parameters with
- *   static tensor types.
+ *   leaky_relu(X @ W + b, alpha), tensor_map(X @ W [+ b],
+ *   lambda v: If(v > 0, v, 0)) over i32, and chains of such layers whose
+ *   input is the previous layer (h = relu(X @ W1 + b1); relu(h @ W2 + b2)),
+ *   run with the intermediates in device memory -- X, W, b being parameters
+ *   with static tensor types.
  *
  * Any other program is rejected at compile time with an error that names
  * what was found. Errors: functions returning int return 0 on success or an
@@ -84,13 +86,17 @@ int edsl_hip_module_describe(edsl_hip_module *m, char *buf, size_t len);
  * compile_function on this module, empty after a success or clear(). */
 int edsl_hip_module_last_failure(edsl_hip_module *m, char *buf, size_t len);
 
-/* How a compiled function was matched: dtype (EDSL_DTYPE_*), epilogue
- * (EDSL_EPI_*), leaky alpha, the parameter indices of X, W and b (-1 when
- * there is no bias), and the form as text ("relu(X @ W + b)"). Any output
- * pointer may be NULL. No reference counterpart: for tests and tools. */
-int edsl_hip_module_function_form(edsl_hip_module *m, const char *name, int *dtype, int *epilogue,
-                                  float *alpha, int *x_param, int *w_param, int *b_param, char *form,
-                                  size_t form_len);
+/* How a compiled function was matched (no reference counterpart: for tests
+ * and tools). function_form gives the element type (EDSL_DTYPE_*), the number
+ * of dense layers and the whole program as text ("relu(relu(X @ W1 + b1) @ W2
+ * + b2)"); function_layer gives layer i (execution order): the parameter
+ * indices of its input (-1: the previous layer's output), weight and bias
+ * (-1: none), its EDSL_EPI_* epilogue and leaky alpha. Output pointers may be
+ * NULL. */
+int edsl_hip_module_function_form(edsl_hip_module *m, const char *name, int *dtype, int *num_layers,
+                                  char *form, size_t form_len);
+int edsl_hip_module_function_layer(edsl_hip_module *m, const char *name, int layer, int *x_param,
+                                   int *w_param, int *b_param, int *epilogue, float *alpha);
 
 #ifdef __cplusplus
 }

@@ -535,22 +535,30 @@ struct Param {
   TypeSpec type;
 };
 
+// One dense layer: H = epilogue(input @ W (+ b)). The input is a parameter
+// for the first layer of a chain and the previous layer's output after it.
+struct Layer {
+  int x = -1;  // parameter index of the input; -1: the previous layer's output
+  int w = -1, b = -1;
+  int epi = EDSL_EPI_NONE;
+  float alpha = 0.0f;
+};
+
 struct Program {
   std::string name;
   std::vector<Param> params;
   TypeSpec ret;
   int dtype = EDSL_DTYPE_F32;
-  int epi = EDSL_EPI_NONE;
-  float alpha = 0.0f;
-  int x = -1, w = -1, b = -1;  // parameter indices
+  std::vector<Layer> layers;   // in execution order
   int slot = -1;               // trampoline slot
   int nargs = 0;               // flat scalar arguments of the memref calling convention
-  std::string form;            // e.g. "relu(X @ W + b)"
+  std::string form;            // e.g. "relu(relu(X @ W1 + b1) @ W2 + b2)"
 };
 
 const char* kDenseForms =
-    "matmul(A, B), relu(A @ B), X @ W + b, relu(X @ W + b), leaky_relu(X @ W + b, alpha), or "
-    "tensor_map(X @ W [+ b], lambda v: If(v > 0, v, 0)) over i32, with A, B, X, W, b parameters";
+    "matmul(A, B), relu(A @ B), X @ W + b, relu(X @ W + b), leaky_relu(X @ W + b, alpha), "
+    "tensor_map(X @ W [+ b], lambda v: If(v > 0, v, 0)) over i32, and chains of these layers "
+    "(h @ W2 + b2 with h a previous layer), with A, B, X, W, b parameters";
 
 struct Matcher {
   const Ast& ast;
@@ -610,30 +618,41 @@ struct Matcher {
          prog.name.c_str());
   }
 
-  void matmul(const Node& n) {
+  // The lhs of a matmul is a parameter or, in a chain, a whole earlier
+  // layer, which is appended to prog.layers before the layer that reads it.
+  void matmul(const Node& n, Layer& L, int depth) {
     if (n.k != K::Matmul) reject("expected a matmul, found: %s", kind_name(n));
-    prog.x = param_index(res(n.a), "matmul lhs");
-    prog.w = param_index(res(n.b), "matmul rhs");
+    const Node& lhs = res(n.a);
+    if (lhs.k == K::Parameter) {
+      L.x = param_index(lhs, "matmul lhs");
+    } else if (lhs.k == K::Activation || lhs.k == K::Map || lhs.k == K::BinaryOp || lhs.k == K::Matmul) {
+      layer(lhs, depth + 1);
+      L.x = -1;
+    } else {
+      reject("the matmul lhs operand is not a function parameter or a dense layer (found: %s)",
+             kind_name(lhs));
+    }
+    L.w = param_index(res(n.b), "matmul rhs");
   }
 
   // matmul, or matmul + bias (bias on either side: addf / addi commute bit for bit)
-  void affine(const Node& n) {
+  void affine(const Node& n, Layer& L, int depth) {
     if (n.k == K::Matmul) {
-      matmul(n);
+      matmul(n, L, depth);
       return;
     }
     if (n.k != K::BinaryOp) reject("expected matmul or matmul + bias, found: %s", kind_name(n));
     if (n.op != kOpAdd) reject("element-wise op %d: only the bias add is fused", n.op);
     if (n.bcast == kBiasRight) {
-      matmul(res(n.a));
-      prog.b = param_index(res(n.b), "bias");
+      matmul(res(n.a), L, depth);
+      L.b = param_index(res(n.b), "bias");
     } else if (n.bcast == kBiasLeft) {
-      prog.b = param_index(res(n.a), "bias");
-      matmul(res(n.b));
+      L.b = param_index(res(n.a), "bias");
+      matmul(res(n.b), L, depth);
     } else {
       reject("element-wise add with broadcast mode %d: only the [M,N] + [N] bias is fused", n.bcast);
     }
-    prog.epi |= EDSL_EPI_BIAS;
+    L.epi |= EDSL_EPI_BIAS;
   }
 
   bool is_elem(const Node& n, int64_t id) const { return n.k == K::MapElement && n.id == id; }
@@ -667,30 +686,38 @@ struct Matcher {
     return v_pos_selects_v ? (is_elem(t, id) && is_zero(e)) : (is_zero(t) && is_elem(e, id));
   }
 
-  void root(const Node& n) {
+  // One layer rooted at n (activation / tensor_map ReLU / affine); its
+  // input layers are appended first, then the layer itself.
+  void layer(const Node& n, int depth) {
+    if (depth > 64) reject("more than 64 chained layers");
+    Layer L;
     if (n.k == K::Activation) {
       if (n.op == kActRelu) {
-        prog.epi |= EDSL_EPI_RELU;
+        L.epi |= EDSL_EPI_RELU;
+        if (prog.dtype == EDSL_DTYPE_I32)
+          fail(kErrProgram,
+               "function '%s': relu() emits arith.maximumf, which is float-only; write the integer ReLU "
+               "as tensor_map(y, lambda v: If(v > 0, v, 0))",
+               prog.name.c_str());
       } else if (n.op == kActLeaky) {
-        prog.epi |= EDSL_EPI_LEAKY;
-        prog.alpha = n.fval;
+        L.epi |= EDSL_EPI_LEAKY;
+        L.alpha = n.fval;
       } else {
         reject("activation type %d", n.op);
       }
-      affine(res(n.a));
-      return;
-    }
-    if (n.k == K::Map) {
+      affine(res(n.a), L, depth);
+    } else if (n.k == K::Map) {
       if (!relu_body(res(n.b), n.id))
         reject("tensor_map body is not If(v > 0, v, 0) (or an equivalent integer ReLU)");
-      prog.epi |= EDSL_EPI_RELU;
-      affine(res(n.a));
       if (prog.dtype != EDSL_DTYPE_I32)
         reject("tensor_map If-ReLU over f32 maps NaN to 0, which the fused maximumf epilogue does not; "
                "use relu()");
-      return;
+      L.epi |= EDSL_EPI_RELU;
+      affine(res(n.a), L, depth);
+    } else {
+      affine(n, L, depth);
     }
-    affine(n);
+    prog.layers.push_back(L);
   }
 };
 
@@ -704,47 +731,60 @@ void check_types(Program& p) {
       if (d < 0) fail(kErrProgram, "Dynamic tensor dimensions not supported");
     return t;
   };
-  const TypeSpec& X = tensor(p.x, 2, "matmul lhs");
-  const TypeSpec& W = tensor(p.w, 2, "matmul rhs");
-  if (X.elem != W.elem)
-    fail(kErrProgram, "function '%s': matmul operand element types must match, got %s and %s", p.name.c_str(),
-         type_str(X).c_str(), type_str(W).c_str());
+  const TypeSpec& X = tensor(p.layers[0].x, 2, "matmul lhs");
   if (X.elem == kF32)
     p.dtype = EDSL_DTYPE_F32;
   else if (X.elem == kI32)
     p.dtype = EDSL_DTYPE_I32;
   else
     fail(kErrProgram, "function '%s': element type %s is not f32 or i32", p.name.c_str(), scalar_name(X.elem));
-  if (X.shape[1] != W.shape[0])
-    fail(kErrProgram, "function '%s': matmul inner dimensions must match, got lhs shape %s and rhs shape %s",
-         p.name.c_str(), type_str(X).c_str(), type_str(W).c_str());
-  if (p.b >= 0) {
-    const TypeSpec& B = tensor(p.b, 1, "bias");
-    if (B.elem != X.elem || B.shape[0] != W.shape[1])
-      fail(kErrProgram, "function '%s': bias %s does not broadcast over [%lld, %lld]", p.name.c_str(),
-           type_str(B).c_str(), (long long)X.shape[0], (long long)W.shape[1]);
+  const int64_t M = X.shape[0];
+  int64_t K = X.shape[1];
+  std::string lhs = type_str(X);
+  for (const Layer& L : p.layers) {
+    const TypeSpec& W = tensor(L.w, 2, "matmul rhs");
+    if (W.elem != X.elem)
+      fail(kErrProgram, "function '%s': matmul operand element types must match, got %s and %s",
+           p.name.c_str(), lhs.c_str(), type_str(W).c_str());
+    if (W.shape[0] != K)
+      fail(kErrProgram, "function '%s': matmul inner dimensions must match, got lhs shape %s and rhs shape %s",
+           p.name.c_str(), lhs.c_str(), type_str(W).c_str());
+    const int64_t N = W.shape[1];
+    if (L.b >= 0) {
+      const TypeSpec& B = tensor(L.b, 1, "bias");
+      if (B.elem != X.elem || B.shape[0] != N)
+        fail(kErrProgram, "function '%s': bias %s does not broadcast over [%lld, %lld]", p.name.c_str(),
+             type_str(B).c_str(), (long long)M, (long long)N);
+    }
+    if ((L.epi >> 1) == 2 && p.dtype != EDSL_DTYPE_F32)
+      fail(kErrProgram, "function '%s': leaky_relu is float-only", p.name.c_str());
+    K = N;
+    lhs = "tensor<" + std::to_string(M) + "x" + std::to_string(N) + "x" + scalar_name(X.elem) + ">";
   }
-  if (p.ret.kind != 3 || p.ret.shape.size() != 2 || p.ret.shape[0] != X.shape[0] ||
-      p.ret.shape[1] != W.shape[1] || p.ret.elem != X.elem)
+  if (p.ret.kind != 3 || p.ret.shape.size() != 2 || p.ret.shape[0] != M || p.ret.shape[1] != K ||
+      p.ret.elem != X.elem)
     fail(kErrProgram, "function '%s': return type %s does not match the result tensor<%lldx%lldx%s>",
-         p.name.c_str(), type_str(p.ret).c_str(), (long long)X.shape[0], (long long)W.shape[1],
-         scalar_name(X.elem));
-  if ((p.epi >> 1) == 2 && p.dtype != EDSL_DTYPE_F32)
-    fail(kErrProgram, "function '%s': leaky_relu is float-only", p.name.c_str());
+         p.name.c_str(), type_str(p.ret).c_str(), (long long)M, (long long)K, scalar_name(X.elem));
 }
 
 std::string form_of(const Program& p) {
-  const std::string xw = p.params[p.x].name + " @ " + p.params[p.w].name;
-  const std::string aff = p.b >= 0 ? xw + " + " + p.params[p.b].name : xw;
-  switch (p.epi >> 1) {
-    case 1: return "relu(" + aff + ")";
-    case 2: {
-      char a[32];
-      snprintf(a, sizeof(a), "%g", (double)p.alpha);
-      return "leaky_relu(" + aff + ", " + a + ")";
+  std::string h;
+  for (const Layer& L : p.layers) {
+    const std::string in = L.x >= 0 ? p.params[L.x].name : h;
+    std::string aff = in + " @ " + p.params[L.w].name;
+    if (L.b >= 0) aff += " + " + p.params[L.b].name;
+    switch (L.epi >> 1) {
+      case 1: h = "relu(" + aff + ")"; break;
+      case 2: {
+        char a[32];
+        snprintf(a, sizeof(a), "%g", (double)L.alpha);
+        h = "leaky_relu(" + aff + ", " + a + ")";
+        break;
+      }
+      default: h = L.x >= 0 || p.layers.size() == 1 ? aff : "(" + aff + ")"; break;
     }
-    default: return aff;
   }
+  return h;
 }
 
 Program decode_function_def(const void* bytes, size_t len) {
@@ -794,19 +834,10 @@ Program decode_function_def(const void* bytes, size_t len) {
       if (p.params[i].name == p.params[j].name)
         fail(kErrProgram, "function '%s': parameter '%s' declared twice", p.name.c_str(), p.params[i].name.c_str());
   Matcher m{ast, p};
-  // Element type first: the integer tensor_map form depends on it.
-  {
-    const Node& r = m.res(body);
-    const TypeSpec& t = p.ret;
-    p.dtype = (t.kind == 3 && t.elem == kI32) ? EDSL_DTYPE_I32 : EDSL_DTYPE_F32;
-    m.root(r);
-  }
+  // Element type first (from the result): the integer ReLU forms depend on it.
+  p.dtype = (p.ret.kind == 3 && p.ret.elem == kI32) ? EDSL_DTYPE_I32 : EDSL_DTYPE_F32;
+  m.layer(m.res(body), 0);
   check_types(p);
-  if ((p.epi >> 1) == 1 && p.dtype == EDSL_DTYPE_I32 && m.res(body).k == K::Activation)
-    fail(kErrProgram,
-         "function '%s': relu() emits arith.maximumf, which is float-only; write the integer ReLU as "
-         "tensor_map(y, lambda v: If(v > 0, v, 0))",
-         p.name.c_str());
   p.nargs = 7;  // out-param memref
   for (const Param& prm : p.params) p.nargs += 3 + 2 * (int)prm.type.shape.size();
   p.form = form_of(p);
@@ -814,15 +845,38 @@ Program decode_function_def(const void* bytes, size_t len) {
 }
 
 // ============================================================ trampolines
-constexpr int kSlots = 256;
+// Flat argument counts served by function pointers: X (7) + out (7) plus, per
+// layer, W (7) and an optional bias (5), for 1 to 4 layers with all parameters
+// distinct; a parameter used twice (A @ A) lowers the count, giving 14 and 19.
+// Programs of any other count run through execute_gpu_function.
+constexpr int kNumArities = 16;
+constexpr int kArities[kNumArities] = {14, 19, 21, 26, 28, 33, 35, 38, 40, 42, 45, 47, 50, 52, 57, 62};
+constexpr int kSlots = 64;  // function pointers per arity
 std::mutex g_slot_mu;
-std::shared_ptr<const Program> g_slot[kSlots];
+std::shared_ptr<const Program> g_slot[kNumArities][kSlots];
 
-void run_slot(int s, const int64_t* v, int n) {
+int arity_index(int nargs) {
+  for (int a = 0; a < kNumArities; ++a)
+    if (kArities[a] == nargs) return a;
+  return -1;
+}
+
+// The layer operations of p over its bound operands (mats / vecs indexed by
+// parameter), run with the chain executor.
+void run_program(const Program& p, const std::vector<Mat>& mats, const std::vector<Vec>& vecs, const Mat& Y) {
+  std::vector<LayerOp> ops;
+  ops.reserve(p.layers.size());
+  for (const Layer& L : p.layers)
+    ops.push_back(LayerOp{L.x >= 0 ? &mats[L.x] : nullptr, &mats[L.w], L.b >= 0 ? &vecs[L.b] : nullptr, L.epi,
+                          L.alpha});
+  sync_dense_chain(p.dtype, ops.data(), (int)ops.size(), Y);
+}
+
+void run_slot(int a, int s, const int64_t* v, int n) {
   std::shared_ptr<const Program> p;
   {
     std::lock_guard<std::mutex> lock(g_slot_mu);
-    p = g_slot[s];
+    p = g_slot[a][s];
   }
   const int rc = guarded([&] {
     if (!p) fail(kErrUnknown, "function pointer slot %d is no longer bound (the module was cleared)", s);
@@ -848,58 +902,57 @@ void run_slot(int s, const int64_t* v, int n) {
       else if (r == 1)
         vecs[i] = vec_from_desc(ptr(d[1]), d[2], d[3], d[4], 4, nm);
     }
-    sync_dense(p->dtype, p->epi, p->alpha, mats[p->x], mats[p->w], p->b >= 0 ? &vecs[p->b] : nullptr, mats[np]);
+    run_program(*p, mats, vecs, mats[np]);
   });
   if (rc != 0)  // the memref calling convention has no error channel
     fprintf(stderr, "[edsl_hip] %s: %s\n", p ? p->name.c_str() : "?", t_err_msg.c_str());
 }
 
-template <int S, typename Seq>
+template <int A, int S, typename Seq>
 struct Tramp;
-template <int S, size_t... I>
-struct Tramp<S, std::index_sequence<I...>> {
+template <int A, int S, size_t... I>
+struct Tramp<A, S, std::index_sequence<I...>> {
   static void fn(decltype((void)I, int64_t{})... a) {
     const int64_t v[] = {a...};
-    run_slot(S, v, (int)sizeof...(I));
+    run_slot(A, S, v, (int)sizeof...(I));
   }
 };
 
-template <size_t N, size_t... S>
-std::array<void*, sizeof...(S)> tramp_table(std::index_sequence<S...>) {
-  return {reinterpret_cast<void*>(&Tramp<(int)S, std::make_index_sequence<N>>::fn)...};
+template <int A, size_t... S>
+std::array<void*, kSlots> arity_table(std::index_sequence<S...>) {
+  return {reinterpret_cast<void*>(&Tramp<A, (int)S, std::make_index_sequence<kArities[A]>>::fn)...};
 }
 
-// Flat argument counts of the dense forms: one 2-D parameter used twice
-// (A @ A: 7 + out 7), plus a bias (19), two 2-D parameters (21), two 2-D
-// parameters and a bias (26).
-void* trampoline(int slot, int nargs) {
-  static const std::array<void*, kSlots> t14 = tramp_table<14>(std::make_index_sequence<kSlots>{});
-  static const std::array<void*, kSlots> t19 = tramp_table<19>(std::make_index_sequence<kSlots>{});
-  static const std::array<void*, kSlots> t21 = tramp_table<21>(std::make_index_sequence<kSlots>{});
-  static const std::array<void*, kSlots> t26 = tramp_table<26>(std::make_index_sequence<kSlots>{});
-  switch (nargs) {
-    case 14: return t14[slot];
-    case 19: return t19[slot];
-    case 21: return t21[slot];
-    case 26: return t26[slot];
-    default: return nullptr;
-  }
+template <size_t... A>
+std::array<std::array<void*, kSlots>, kNumArities> all_tables(std::index_sequence<A...>) {
+  return {arity_table<(int)A>(std::make_index_sequence<kSlots>{})...};
 }
 
+void* trampoline(int a, int slot) {
+  static const std::array<std::array<void*, kSlots>, kNumArities> tables =
+      all_tables(std::make_index_sequence<kNumArities>{});
+  return tables[a][slot];
+}
+
+// Binds p to a free slot of its arity; returns the slot, or -1 when the arity
+// has no trampolines or all its slots are taken.
 int acquire_slot(const std::shared_ptr<const Program>& p) {
+  const int a = arity_index(p->nargs);
+  if (a < 0) return -1;
   std::lock_guard<std::mutex> lock(g_slot_mu);
   for (int s = 0; s < kSlots; ++s)
-    if (!g_slot[s]) {
-      g_slot[s] = p;
+    if (!g_slot[a][s]) {
+      g_slot[a][s] = p;
       return s;
     }
   return -1;
 }
 
-void release_slot(int s) {
-  if (s < 0) return;
+void release_slot(const Program& p) {
+  const int a = arity_index(p.nargs);
+  if (a < 0 || p.slot < 0) return;
   std::lock_guard<std::mutex> lock(g_slot_mu);
-  g_slot[s].reset();
+  g_slot[a][p.slot].reset();
 }
 
 }  // namespace
@@ -917,7 +970,7 @@ struct edsl_hip_module {
 namespace {
 
 void release_all(edsl_hip_module* m) {
-  for (auto& kv : m->fns) release_slot(kv.second->slot);
+  for (auto& kv : m->fns) release_slot(*kv.second);
   m->fns.clear();
 }
 
@@ -994,15 +1047,16 @@ void* edsl_hip_module_get_function_pointer(edsl_hip_module* m, const char* name)
       std::lock_guard<std::mutex> lock(m->mu);
       p = lookup(m, name);
     }
-    if (p->slot < 0)
-      fail(kErrLimit, "function '%s': all %d function-pointer slots are in use; clear() the module",
-           p->name.c_str(), kSlots);
-    fp = trampoline(p->slot, p->nargs);
-    if (!fp)
+    const int a = arity_index(p->nargs);
+    if (a < 0)
       fail(kErrProgram,
-           "function '%s' takes %d flat memref arguments; function pointers serve the 14-, 19-, 21- and "
-           "26-argument dense forms (parameters the body does not use are not; use execute_gpu_function)",
+           "function '%s' takes %d flat memref arguments; function pointers serve the dense forms with 1 to "
+           "4 layers and every parameter used (use execute_gpu_function)",
            p->name.c_str(), p->nargs);
+    if (p->slot < 0)
+      fail(kErrLimit, "function '%s': all %d function-pointer slots of its form are in use; clear() the module",
+           p->name.c_str(), kSlots);
+    fp = trampoline(a, p->slot);
   });
   return fp;
 }
@@ -1035,8 +1089,8 @@ int edsl_hip_module_last_failure(edsl_hip_module* m, char* buf, size_t len) {
   return copy_out(s, buf, len);
 }
 
-int edsl_hip_module_function_form(edsl_hip_module* m, const char* name, int* dtype, int* epilogue, float* alpha,
-                                  int* x_param, int* w_param, int* b_param, char* form, size_t form_len) {
+int edsl_hip_module_function_form(edsl_hip_module* m, const char* name, int* dtype, int* num_layers, char* form,
+                                  size_t form_len) {
   return guarded([&] {
     std::shared_ptr<Program> p;
     {
@@ -1045,12 +1099,28 @@ int edsl_hip_module_function_form(edsl_hip_module* m, const char* name, int* dty
       p = lookup(m, name);
     }
     if (dtype) *dtype = p->dtype;
-    if (epilogue) *epilogue = p->epi;
-    if (alpha) *alpha = p->alpha;
-    if (x_param) *x_param = p->x;
-    if (w_param) *w_param = p->w;
-    if (b_param) *b_param = p->b;
+    if (num_layers) *num_layers = (int)p->layers.size();
     copy_out(p->form, form, form_len);
+  });
+}
+
+int edsl_hip_module_function_layer(edsl_hip_module* m, const char* name, int layer, int* x_param, int* w_param,
+                                   int* b_param, int* epilogue, float* alpha) {
+  return guarded([&] {
+    std::shared_ptr<Program> p;
+    {
+      if (!m) fail(kErrArgument, "null module");
+      std::lock_guard<std::mutex> lock(m->mu);
+      p = lookup(m, name);
+    }
+    if (layer < 0 || layer >= (int)p->layers.size())
+      fail(kErrArgument, "function '%s' has %zu layers, no layer %d", p->name.c_str(), p->layers.size(), layer);
+    const Layer& L = p->layers[layer];
+    if (x_param) *x_param = L.x;
+    if (w_param) *w_param = L.w;
+    if (b_param) *b_param = L.b;
+    if (epilogue) *epilogue = L.epi;
+    if (alpha) *alpha = L.alpha;
   });
 }
 
@@ -1089,7 +1159,7 @@ int edsl_hip_module_execute_gpu_function(edsl_hip_module* m, const char* name, i
     if (output_rank != 2 || output_shape[0] != p->ret.shape[0] || output_shape[1] != p->ret.shape[1])
       fail(kErrShape, "output shape does not match %s", type_str(p->ret).c_str());
     const Mat Y = mat_from_desc(output, 0, p->ret.shape[0], p->ret.shape[1], p->ret.shape[1], 1, 4, "output");
-    sync_dense(p->dtype, p->epi, p->alpha, mats[p->x], mats[p->w], p->b >= 0 ? &vecs[p->b] : nullptr, Y);
+    run_program(*p, mats, vecs, Y);
   });
 }
 

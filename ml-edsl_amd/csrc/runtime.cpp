@@ -100,6 +100,7 @@ struct DeviceState {
   bool ready = false;
   int cus = 256;
   DevBuf stage[4];  // host-operand staging: X/A, W/B, bias, Y/C
+  DevBuf chain[2];  // intermediate activations of multi-layer programs (ping-pong)
   DevBuf gemv_partials;
   DevBuf i8_x, i8_w, i8_flag;
   unsigned epoch = 0;
@@ -396,18 +397,49 @@ void launch_dense(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
 
 // ------------------------------------------------- synchronous host entry
 // Shapes: X [M,K], W [K,N], bias [N] (when the epilogue adds one), Y [M,N].
-void sync_dense(int dtype, int epi, float alpha, const Mat& X, const Mat& W, const Vec* b, const Mat& Y) {
-  const int64_t M = X.rows, K = X.cols, N = W.cols;
-  if (W.rows != K)
-    fail(kErrShape, "matmul inner dimensions must match: lhs K=%lld, rhs K=%lld", (long long)K,
-         (long long)W.rows);
-  if (Y.rows != M || Y.cols != N)
+// Copies a host matrix into a device buffer with rows padded to a multiple
+// of 4 elements; one contiguous copy when neither side is padded.
+void copy_h2d(void* d, int64_t dld, const Mat& m, size_t es, hipStream_t stream) {
+  if (m.ld == m.cols && dld == m.cols)
+    check_hip(hipMemcpyAsync(d, m.base, (size_t)m.rows * m.cols * es, hipMemcpyHostToDevice, stream),
+              "hipMemcpyAsync H2D");
+  else
+    check_hip(hipMemcpy2DAsync(d, dld * es, m.base, m.ld * es, m.cols * es, m.rows, hipMemcpyHostToDevice,
+                               stream),
+              "hipMemcpy2DAsync H2D");
+}
+
+void copy_d2h(const Mat& m, const void* d, int64_t dld, size_t es, hipStream_t stream) {
+  if (m.ld == m.cols && dld == m.cols)
+    check_hip(hipMemcpyAsync(m.base, d, (size_t)m.rows * m.cols * es, hipMemcpyDeviceToHost, stream),
+              "hipMemcpyAsync D2H");
+  else
+    check_hip(hipMemcpy2DAsync(m.base, m.ld * es, d, dld * es, m.cols * es, m.rows, hipMemcpyDeviceToHost,
+                               stream),
+              "hipMemcpy2DAsync D2H");
+}
+
+void sync_dense_chain(int dtype, const LayerOp* layers, int n, const Mat& Y) {
+  if (n < 1 || !layers || !layers[0].X) fail(kErrArgument, "a chain needs at least one layer and an input");
+  const int64_t M = layers[0].X->rows;
+  int64_t K = layers[0].X->cols;
+  for (int i = 0; i < n; ++i) {
+    const LayerOp& L = layers[i];
+    if (i > 0 && L.X) fail(kErrArgument, "layer %d: only the first layer reads a parameter as its input", i);
+    if (!L.W) fail(kErrArgument, "layer %d: null weight", i);
+    if (L.W->rows != K)
+      fail(kErrShape, "matmul inner dimensions must match: lhs K=%lld, rhs K=%lld", (long long)K,
+           (long long)L.W->rows);
+    const int64_t N = L.W->cols;
+    if (epi_has_bias(L.epi) && (!L.b || L.b->n != N))
+      fail(kErrShape, "bias length %lld does not match N=%lld", (long long)(L.b ? L.b->n : -1), (long long)N);
+    check_dims(M, N, K);
+    K = N;
+  }
+  if (Y.rows != M || Y.cols != K)
     fail(kErrShape, "output shape [%lld,%lld] does not match [%lld,%lld]", (long long)Y.rows,
-         (long long)Y.cols, (long long)M, (long long)N);
-  if (epi_has_bias(epi) && (!b || b->n != N))
-    fail(kErrShape, "bias length %lld does not match N=%lld", (long long)(b ? b->n : -1), (long long)N);
-  check_dims(M, N, K);
-  if (M == 0 || N == 0) {
+         (long long)Y.cols, (long long)M, (long long)K);
+  if (M == 0 || K == 0) {
     set_plan("empty");
     return;
   }
@@ -420,58 +452,89 @@ void sync_dense(int dtype, int epi, float alpha, const Mat& X, const Mat& W, con
   const size_t es = 4;
 
   // Host operands are staged through persistent device buffers with 16-byte
-  // aligned rows so the fast kernels stay eligible.
+  // aligned rows so the fast kernels stay eligible. The stream orders each
+  // layer's staging copies after the previous layer's kernels, so one set of
+  // staging buffers serves every layer.
   auto stage_in = [&](const Mat& m, DevBuf& buf, int64_t* ld) -> const void* {
-    if (m.rows == 0 || m.cols == 0) {
-      *ld = m.ld;
-      return m.base;
-    }
-    if (is_device_pointer(m.base, dev)) {
+    if (m.rows == 0 || m.cols == 0 || is_device_pointer(m.base, dev)) {
       *ld = m.ld;
       return m.base;
     }
     const int64_t dld = (m.cols + 3) & ~int64_t(3);
     void* d = buf.ensure((size_t)m.rows * dld * es, false);
-    check_hip(hipMemcpy2DAsync(d, dld * es, m.base, m.ld * es, m.cols * es, m.rows,
-                               hipMemcpyHostToDevice, stream),
-              "hipMemcpy2DAsync H2D");
+    copy_h2d(d, dld, m, es, stream);
     *ld = dld;
     return d;
   };
 
-  DenseLaunch L{};
-  L.dtype = dtype;
-  L.epi = epi;
-  L.alpha = alpha;
-  L.M = M;
-  L.N = N;
-  L.K = K;
-  L.x = stage_in(X, ds.stage[0], &L.ldx);
-  L.w = stage_in(W, ds.stage[1], &L.ldw);
-  if (epi_has_bias(epi)) {
-    if (is_device_pointer(b->base, dev)) {
-      L.bias = b->base;
-    } else {
-      void* d = ds.stage[2].ensure((size_t)N * es, false);
-      check_hip(hipMemcpyAsync(d, b->base, (size_t)N * es, hipMemcpyHostToDevice, stream), "hipMemcpyAsync H2D");
-      L.bias = d;
-    }
+  // Intermediate activations ping-pong between two device buffers sized up
+  // front, so no buffer is reallocated while a kernel may still use it.
+  int64_t inter = 0;
+  for (int i = 0; i + 1 < n; ++i) inter = std::max(inter, M * ((layers[i].W->cols + 3) & ~int64_t(3)));
+  void* hbuf[2] = {nullptr, nullptr};
+  if (n > 1) {
+    hbuf[0] = ds.chain[0].ensure((size_t)inter * es, false);
+    if (n > 2) hbuf[1] = ds.chain[1].ensure((size_t)inter * es, false);
   }
   const bool y_dev = is_device_pointer(Y.base, dev);
-  if (y_dev) {
-    L.y = Y.base;
-    L.ldy = Y.ld;
-  } else {
-    L.ldy = (N + 3) & ~int64_t(3);
-    L.y = ds.stage[3].ensure((size_t)M * L.ldy * es, false);
-  }
+  const int64_t N_last = Y.cols;
+  void* ystage = nullptr;
+  int64_t ystage_ld = (N_last + 3) & ~int64_t(3);
+  if (!y_dev) ystage = ds.stage[3].ensure((size_t)M * ystage_ld * es, false);
 
-  launch_dense(ds, L, stream);
-  if (!y_dev)
-    check_hip(hipMemcpy2DAsync(Y.base, Y.ld * es, L.y, L.ldy * es, N * es, M, hipMemcpyDeviceToHost, stream),
-              "hipMemcpy2DAsync D2H");
+  std::string plans;
+  const void* prev = nullptr;
+  int64_t prev_ld = 0;
+  for (int i = 0; i < n; ++i) {
+    const LayerOp& op = layers[i];
+    DenseLaunch L{};
+    L.dtype = dtype;
+    L.epi = op.epi;
+    L.alpha = op.alpha;
+    L.M = M;
+    L.K = op.W->rows;
+    L.N = op.W->cols;
+    if (i == 0) {
+      L.x = stage_in(*op.X, ds.stage[0], &L.ldx);
+    } else {
+      L.x = prev;
+      L.ldx = prev_ld;
+    }
+    L.w = stage_in(*op.W, ds.stage[1], &L.ldw);
+    if (epi_has_bias(op.epi)) {
+      if (is_device_pointer(op.b->base, dev)) {
+        L.bias = op.b->base;
+      } else {
+        void* d = ds.stage[2].ensure((size_t)L.N * es, false);
+        check_hip(hipMemcpyAsync(d, op.b->base, (size_t)L.N * es, hipMemcpyHostToDevice, stream),
+                  "hipMemcpyAsync H2D");
+        L.bias = d;
+      }
+    }
+    if (i + 1 < n) {
+      L.y = hbuf[i % 2];
+      L.ldy = (L.N + 3) & ~int64_t(3);
+    } else if (y_dev) {
+      L.y = Y.base;
+      L.ldy = Y.ld;
+    } else {
+      L.y = ystage;
+      L.ldy = ystage_ld;
+    }
+    launch_dense(ds, L, stream);
+    if (n > 1) plans += (i ? " | " : "") + t_plan;
+    prev = L.y;
+    prev_ld = L.ldy;
+  }
+  if (n > 1) t_plan = plans;
+  if (!y_dev) copy_d2h(Y, ystage, ystage_ld, es, stream);
   check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
   check_hip(hipGetLastError(), "kernel execution");
+}
+
+void sync_dense(int dtype, int epi, float alpha, const Mat& X, const Mat& W, const Vec* b, const Mat& Y) {
+  const LayerOp op{&X, &W, b, epi, alpha};
+  sync_dense_chain(dtype, &op, 1, Y);
 }
 
 }  // namespace rt

@@ -77,5 +77,20 @@ Vec vec_from_desc(void* aligned, int64_t offset, int64_t d0, int64_t s0, size_t 
 // synchronous on return. dtype is EDSL_DTYPE_*, epi an EDSL_EPI_* code.
 void sync_dense(int dtype, int epi, float alpha, const Mat& X, const Mat& W, const Vec* b, const Mat& Y);
 
+// One layer of a chain: H_i = epilogue(H_{i-1} @ W (+ b)). Only the first
+// layer has an input X; later layers read the previous layer's output.
+struct LayerOp {
+  const Mat* X;  // first layer only, else nullptr
+  const Mat* W;
+  const Vec* b;  // when epi adds a bias
+  int epi;
+  float alpha;
+};
+
+// Runs the layers in order with the intermediates in device memory (host
+// operands staged, only the last layer's output copied back), synchronous on
+// return.
+void sync_dense_chain(int dtype, const LayerOp* layers, int n, const Mat& Y);
+
 }  // namespace rt
 }  // namespace edsl

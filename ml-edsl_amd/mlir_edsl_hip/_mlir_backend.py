@@ -15,8 +15,8 @@ unchanged front end (``@ml_function`` / ``CppMLIRBackend``) run dense-path
 functions on the GPU, for either ``target``.
 
 Only dense-path programs compile (matmul, relu(matmul), matmul + bias,
-relu / leaky_relu of it, and the integer tensor_map If-ReLU); anything else
-raises RuntimeError naming what was found.
+relu / leaky_relu of it, the integer tensor_map If-ReLU, and chains of such
+layers); anything else raises RuntimeError naming what was found.
 """
 from __future__ import annotations
 
@@ -56,10 +56,12 @@ def _L() -> ctypes.CDLL:
         L.edsl_hip_module_last_failure.argtypes = [vp, ctypes.c_char_p, sz]
         L.edsl_hip_module_last_failure.restype = c_int
         L.edsl_hip_module_function_form.argtypes = [
-            vp, ctypes.c_char_p, ctypes.POINTER(c_int), ctypes.POINTER(c_int),
-            ctypes.POINTER(ctypes.c_float), ctypes.POINTER(c_int), ctypes.POINTER(c_int),
-            ctypes.POINTER(c_int), ctypes.c_char_p, sz]
+            vp, ctypes.c_char_p, ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.c_char_p, sz]
         L.edsl_hip_module_function_form.restype = c_int
+        L.edsl_hip_module_function_layer.argtypes = [
+            vp, ctypes.c_char_p, c_int, ctypes.POINTER(c_int), ctypes.POINTER(c_int),
+            ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(ctypes.c_float)]
+        L.edsl_hip_module_function_layer.restype = c_int
         _lib = L
     return _lib
 
@@ -191,14 +193,25 @@ class MLIRCompiler:
 
     # ----------------------------------------------------------- extension
     def function_form(self, name: str) -> dict:
-        """How a compiled function was matched (no reference counterpart)."""
-        dt, epi, x, w, b = (ctypes.c_int() for _ in range(5))
-        alpha = ctypes.c_float()
-        buf = ctypes.create_string_buffer(256)
-        if _L().edsl_hip_module_function_form(self._m, name.encode(), ctypes.byref(dt), ctypes.byref(epi),
-                                              ctypes.byref(alpha), ctypes.byref(x), ctypes.byref(w),
-                                              ctypes.byref(b), buf, len(buf)) != 0:
+        """How a compiled function was matched (no reference counterpart):
+        dtype, the program as text, and its layers in execution order (x = -1
+        reads the previous layer's output). The top-level x is the first
+        layer's input; w, b, epilogue and alpha are the last layer's."""
+        L = _L()
+        dt, nl = ctypes.c_int(), ctypes.c_int()
+        buf = ctypes.create_string_buffer(512)
+        if L.edsl_hip_module_function_form(self._m, name.encode(), ctypes.byref(dt), ctypes.byref(nl), buf,
+                                           len(buf)) != 0:
             _raise("function_form")
-        return {"dtype": "f32" if dt.value == _native.DTYPE_F32 else "i32", "epilogue": epi.value,
-                "alpha": alpha.value, "x": x.value, "w": w.value, "b": b.value,
-                "form": buf.value.decode()}
+        layers = []
+        for i in range(nl.value):
+            x, w, b, epi = (ctypes.c_int() for _ in range(4))
+            alpha = ctypes.c_float()
+            if L.edsl_hip_module_function_layer(self._m, name.encode(), i, ctypes.byref(x), ctypes.byref(w),
+                                                ctypes.byref(b), ctypes.byref(epi), ctypes.byref(alpha)) != 0:
+                _raise("function_layer")
+            layers.append({"x": x.value, "w": w.value, "b": b.value, "epilogue": epi.value,
+                           "alpha": alpha.value})
+        return {"dtype": "f32" if dt.value == _native.DTYPE_F32 else "i32", "form": buf.value.decode(),
+                "layers": layers, "x": layers[0]["x"], "w": layers[-1]["w"], "b": layers[-1]["b"],
+                "epilogue": layers[-1]["epilogue"], "alpha": layers[-1]["alpha"]}

@@ -318,9 +318,56 @@ def programs(E):
         return relu(X @ W)
     out.append(("reject_i32_relu_activation", int_relu_activation, {"reject": "float-only"}))
 
+    def rhs_layer(X: Tensor[f32, 4, 4], A: Tensor[f32, 4, 4], B: Tensor[f32, 4, 4]) -> Tensor[f32, 4, 4]:
+        return X @ relu(A @ B)
+    out.append(("reject_layer_as_rhs", rhs_layer, {"reject": "matmul rhs operand is not a function parameter"}))
+
+    # chains (reference tests/linalg/test_binary_op_execution.py:223-268 and variants)
+    def two_layer(X: Tensor[f32, 2, 4], W1: Tensor[f32, 4, 8], b1: Tensor[f32, 8],
+                  W2: Tensor[f32, 8, 3], b2: Tensor[f32, 3]) -> Tensor[f32, 2, 3]:
+        h = relu(X @ W1 + b1)
+        return relu(h @ W2 + b2)
+    out.append(("chain_two_layer_net", two_layer, {
+        "form": "relu(relu(X @ W1 + b1) @ W2 + b2)", "dtype": "f32",
+        "layers": [{"x": 0, "w": 1, "b": 2, "epilogue": 3}, {"x": -1, "w": 3, "b": 4, "epilogue": 3}]}))
+
+    def three_layer(X: Tensor[f32, 4, 8], W1: Tensor[f32, 8, 16], b1: Tensor[f32, 16],
+                    W2: Tensor[f32, 16, 8], b2: Tensor[f32, 8],
+                    W3: Tensor[f32, 8, 4], b3: Tensor[f32, 4]) -> Tensor[f32, 4, 4]:
+        h1 = relu(X @ W1 + b1)
+        h2 = relu(h1 @ W2 + b2)
+        return relu(h2 @ W3 + b3)
+    out.append(("chain_three_layer_net", three_layer, {
+        "form": "relu(relu(relu(X @ W1 + b1) @ W2 + b2) @ W3 + b3)", "dtype": "f32",
+        "layers": [{"x": 0, "w": 1, "b": 2, "epilogue": 3}, {"x": -1, "w": 3, "b": 4, "epilogue": 3},
+                   {"x": -1, "w": 5, "b": 6, "epilogue": 3}]}))
+
     def chained(X: Tensor[f32, 4, 4], W1: Tensor[f32, 4, 4], W2: Tensor[f32, 4, 4]) -> Tensor[f32, 4, 4]:
         return relu(relu(X @ W1) @ W2)
-    out.append(("reject_two_layers", chained, {"reject": "not a function parameter"}))
+    out.append(("chain_relu_no_bias", chained, {
+        "form": "relu(relu(X @ W1) @ W2)", "dtype": "f32",
+        "layers": [{"x": 0, "w": 1, "b": -1, "epilogue": 2}, {"x": -1, "w": 2, "b": -1, "epilogue": 2}]}))
+
+    def mixed(X: Tensor[f32, 64, 128], W1: Tensor[f32, 128, 256], b1: Tensor[f32, 256],
+              W2: Tensor[f32, 256, 64]) -> Tensor[f32, 64, 64]:
+        return leaky_relu(relu(X @ W1 + b1) @ W2, 0.1)
+    out.append(("chain_relu_then_leaky", mixed, {
+        "form": "leaky_relu(relu(X @ W1 + b1) @ W2, 0.1)", "dtype": "f32",
+        "layers": [{"x": 0, "w": 1, "b": 2, "epilogue": 3}, {"x": -1, "w": 3, "b": -1, "epilogue": 4}]}))
+
+    def int_chain(X: Tensor[i32, 32, 64], W1: Tensor[i32, 64, 128], b1: Tensor[i32, 128],
+                  W2: Tensor[i32, 128, 32], b2: Tensor[i32, 32]) -> Tensor[i32, 32, 32]:
+        h = tensor_map(X @ W1 + b1, lambda v: If(v > 0, v, 0))
+        return tensor_map(h @ W2 + b2, lambda v: If(v > 0, v, 0))
+    out.append(("chain_int_two_layer", int_chain, {
+        "form": "relu(relu(X @ W1 + b1) @ W2 + b2)", "dtype": "i32",
+        "layers": [{"x": 0, "w": 1, "b": 2, "epilogue": 3}, {"x": -1, "w": 3, "b": 4, "epilogue": 3}]}))
+
+    def shared_weights(X: Tensor[f32, 16, 32], W: Tensor[f32, 32, 32], b: Tensor[f32, 32]) -> Tensor[f32, 16, 32]:
+        return relu(relu(X @ W + b) @ W + b)
+    out.append(("chain_shared_weights", shared_weights, {
+        "form": "relu(relu(X @ W + b) @ W + b)", "dtype": "f32",
+        "layers": [{"x": 0, "w": 1, "b": 2, "epilogue": 3}, {"x": -1, "w": 1, "b": 2, "epilogue": 3}]}))
 
     def scalar_add(x: int) -> int:
         return E.add(x, 1)

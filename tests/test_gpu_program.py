@@ -1,6 +1,6 @@
 """GPU parity of the FunctionDef front end: the exact bytes the reference
-front end serializes, compiled by the `_mlir_backend`-compatible compiler
-and run three ways -- through the function pointer with host (numpy)
+front end serializes (single layers and chains of layers), compiled by the
+`_mlir_backend`-compatible compiler and run three ways -- through the function pointer with host (numpy)
 descriptors, as the reference's execute_function calls its JIT'd symbol
 (reference mlir_edsl/backend.py:162-198); through the same pointer with
 device tensors; and through execute_gpu_function with (pointer, shape)
@@ -42,12 +42,19 @@ def _inputs(case, seed, wide=False):
 
 
 def _reference(form, args):
-    X, W = args[form["x"]], args[form["w"]]
-    b = args[form["b"]] if form["b"] >= 0 else None
-    act = {0: "none", 1: "relu", 2: "leaky"}[form["epilogue"] >> 1]
-    if form["dtype"] == "i32":
-        return oracle.dense_i32(X, W, b, act)
-    return oracle.dense_f32(X, W, b, act, form["alpha"])
+    """Layer by layer, as the reference lowering computes a chain: each
+    layer's matmul in full, then its bias + activation, then the next."""
+    h = None
+    for L in form["layers"]:
+        X = args[L["x"]] if L["x"] >= 0 else h
+        W = args[L["w"]]
+        b = args[L["b"]] if L["b"] >= 0 else None
+        act = {0: "none", 1: "relu", 2: "leaky"}[L["epilogue"] >> 1]
+        if form["dtype"] == "i32":
+            h = oracle.dense_i32(X, W, b, act)
+        else:
+            h = oracle.dense_f32(X, W, b, act, L["alpha"])
+    return h
 
 
 def _check(got, ref, K):
@@ -81,7 +88,7 @@ def test_reference_program_runs_three_ways(case, torch_cuda):
     comp.compile_function(open(os.path.join(GOLDEN, case["file"]), "rb").read())
     name = case["function"]
     form = comp.function_form(name)
-    K = case["param_shapes"][form["x"]][1]
+    K = max(case["param_shapes"][L["w"]][0] for L in form["layers"])
     ptr = comp.get_function_pointer(name)
     for seed, wide in ((1, False), (2, True)):
         args = _inputs(case, seed, wide)

@@ -53,6 +53,12 @@ def test_reference_front_end_bytes_decode_to_their_dense_form(case, compiler):
             assert got[key] == exp[key], (key, got, exp)
     if "alpha" in exp:
         assert got["alpha"] == pytest.approx(exp["alpha"], rel=1e-7)
+    if "layers" in exp:
+        assert len(got["layers"]) == len(exp["layers"])
+        for g, e in zip(got["layers"], exp["layers"]):
+            assert {k: g[k] for k in e} == e, (got["layers"], exp["layers"])
+    else:
+        assert len(got["layers"]) == 1
     assert compiler.get_function_pointer(case["function"]) != 0
 
 
