@@ -35,7 +35,6 @@
 // (reference mlir_edsl/backend.py:162-198). Every such argument is a pointer
 // or an int64 (the x86-64 SysV INTEGER class), so one trampoline taking N
 // int64 arguments serves every parameter order of an N-argument function.
-#include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <array>
