@@ -31,8 +31,12 @@ namespace {
 
 template <int KCH>
 __device__ __forceinline__ int a_swizzle(int row) {
-  // A row holds KCH 16-byte chunks; 8/KCH rows fill the 32 four-byte banks.
-  return (row / (8 / KCH)) % KCH;
+  // A row holds KCH 16-byte chunks. Fewer than 8 chunks: 8/KCH rows share a
+  // 128-byte bank line, so consecutive groups of rows rotate the chunks;
+  // 8 or more: XOR with the row index (mod KCH) so that the rows read by one
+  // ds_read_b128 phase land on distinct 16-byte bank groups.
+  if constexpr (KCH >= 8) return row % KCH;
+  else return (row / (8 / KCH)) % KCH;
 }
 
 template <int CP>
@@ -48,10 +52,11 @@ __device__ __forceinline__ void load_b_frag(const float* p, float (&v)[CP]) {
   }
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int EPI, bool GUARD>
-__global__ void __launch_bounds__(WAVES_M * WAVES_N * 64)
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int WAVES_K, int EPI, bool GUARD>
+__global__ void __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64)
 gemm_f32_kernel(GemmF32Args args) {
-  constexpr int NT = WAVES_M * WAVES_N * 64;
+  constexpr int NT = WAVES_M * WAVES_N * WAVES_K * 64;
+  constexpr int WMN = WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M;
   constexpr int WN = BN / WAVES_N;
   constexpr int CP = WN / 32;
@@ -59,7 +64,9 @@ gemm_f32_kernel(GemmF32Args args) {
   constexpr int KCH = BK / 4;
   static_assert(WM % 32 == 0, "wave tile rows must be a multiple of 32");
   static_assert(WN == 32 * CP && (CP == 1 || CP == 2 || CP == 4), "wave tile cols");
-  static_assert(BK % 8 == 0 && KCH <= 8, "BK");
+  static_assert(BK % 8 == 0 && KCH <= 16, "BK");
+  static_assert((BK / 8) % WAVES_K == 0, "waves splitting K need equal shares of a K step");
+  constexpr int JP = BK / 8 / WAVES_K;  // 8-k groups of a K step per wave
   constexpr int A_F4 = BM * KCH;
   constexpr int B_F4 = BK * BN / 4;
   static_assert(A_F4 % NT == 0 && B_F4 % NT == 0, "tile loads must divide evenly");
@@ -72,7 +79,8 @@ gemm_f32_kernel(GemmF32Args args) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wave_m = wave / WAVES_N;
+  const int wave_k = wave / WMN;
+  const int wave_m = (wave % WMN) / WAVES_N;
   const int wave_n = wave % WAVES_N;
   int tm, tn;
   tile_coords(blockIdx.x, args.tiles_m, args.tiles_n, tm, tn);
@@ -150,7 +158,8 @@ gemm_f32_kernel(GemmF32Args args) {
 
   auto compute = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < BK / 8; ++j) {
+    for (int jj = 0; jj < JP; ++jj) {
+      const int j = wave_k * JP + jj;
       f32x4 a[RB];
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
@@ -185,6 +194,36 @@ gemm_f32_kernel(GemmF32Args args) {
       if (more) store_lds(buf ^ 1);
       __syncthreads();
     }
+  }
+
+  // Waves that split K add their partial tiles into wave group 0 through
+  // LDS, in wave order (the K loop ended with a barrier).
+  if constexpr (WAVES_K > 1) {
+    __shared__ f32x4 red[WAVES_K - 1][WMN][RB * CP * 4][64];
+    if (wave_k > 0) {
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int c = 0; c < CP; ++c)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            red[wave_k - 1][wave % WMN][(i * CP + c) * 4 + q][lane] =
+                f32x4{acc[i][c][4 * q], acc[i][c][4 * q + 1], acc[i][c][4 * q + 2], acc[i][c][4 * q + 3]};
+    }
+    __syncthreads();
+    if (wave_k > 0) return;
+#pragma unroll
+    for (int w = 0; w < WAVES_K - 1; ++w)
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int c = 0; c < CP; ++c)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4 t = red[w][wave % WMN][(i * CP + c) * 4 + q][lane];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][c][4 * q + e] += t[e];
+          }
   }
 
   // Epilogue: lane holds rows rbase + 8*(r/4) + 4*half + r%4 of each 32-row
@@ -240,6 +279,11 @@ gemm_f32_kernel(GemmF32Args args) {
 //  4:  64x64x16,  2x2 waves, guarded (any shape / alignment)
 //  5: 256x256x32, 4x2 waves
 //  6: 128x256x16, 2x2 waves (wave tile 64x128)
+//  7-11: 64x64x{32,64}, 128x64x32, 64x128x32, 128x128x32 with 2x2 waves
+//  12-13: 32x32x{32,64}, one wave
+//  14-18: _kN = N waves per output block splitting each K step, partial tiles
+//         summed through LDS: 64x64x64 and 64x64x32 (k2), 32x32x64 (k2, k4),
+//         128x128x32 (k2)
 const GemmF32Config kConfigs[] = {
     {256, 256, 16, 2, 2, false, "f32_256x256x16_w2x2"},
     {256, 256, 16, 4, 2, false, "f32_256x256x16_w4x2"},
@@ -248,17 +292,29 @@ const GemmF32Config kConfigs[] = {
     {64, 64, 16, 2, 2, true, "f32_64x64x16_w2x2_guard"},
     {256, 256, 32, 4, 2, false, "f32_256x256x32_w4x2"},
     {128, 256, 16, 2, 2, false, "f32_128x256x16_w2x2"},
+    {64, 64, 32, 2, 2, false, "f32_64x64x32_w2x2"},
+    {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2"},
+    {128, 64, 32, 2, 2, false, "f32_128x64x32_w2x2"},
+    {64, 128, 32, 2, 2, false, "f32_64x128x32_w2x2"},
+    {128, 128, 32, 2, 2, false, "f32_128x128x32_w2x2"},
+    {32, 32, 32, 1, 1, false, "f32_32x32x32_w1x1"},
+    {32, 32, 64, 1, 1, false, "f32_32x32x64_w1x1"},
+    {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2_k2"},
+    {64, 64, 32, 2, 2, false, "f32_64x64x32_w2x2_k2"},
+    {32, 32, 64, 1, 1, false, "f32_32x32x64_w1x1_k2"},
+    {32, 32, 64, 1, 1, false, "f32_32x32x64_w1x1_k4"},
+    {128, 128, 32, 2, 2, false, "f32_128x128x32_w2x2_k2"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
-template <int BM, int BN, int BK, int WMW, int WNW, bool GUARD>
+template <int BM, int BN, int BK, int WMW, int WNW, int WKW, bool GUARD>
 hipError_t launch_cfg(int epi, const GemmF32Args& a, hipStream_t stream) {
   const dim3 grid(a.tiles_m * a.tiles_n);
-  const dim3 block(WMW * WNW * 64);
-#define EDSL_F32_CASE(E)                                                                      \
-  case E:                                                                                     \
-    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WMW, WNW, E, GUARD>), grid, block, 0, \
-                       stream, a);                                                            \
+  const dim3 block(WMW * WNW * WKW * 64);
+#define EDSL_F32_CASE(E)                                                                           \
+  case E:                                                                                          \
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WMW, WNW, WKW, E, GUARD>), grid, block, 0, \
+                       stream, a);                                                                 \
     break;
   switch (epi) {
     EDSL_F32_CASE(epi_code(false, ACT_NONE))
@@ -281,13 +337,25 @@ const GemmF32Config& gemm_f32_config(int cfg) { return kConfigs[cfg]; }
 
 hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) {
   switch (cfg) {
-    case 0: return launch_cfg<256, 256, 16, 2, 2, false>(epi, a, stream);
-    case 1: return launch_cfg<256, 256, 16, 4, 2, false>(epi, a, stream);
-    case 2: return launch_cfg<128, 128, 16, 2, 2, false>(epi, a, stream);
-    case 3: return launch_cfg<64, 64, 16, 2, 2, false>(epi, a, stream);
-    case 4: return launch_cfg<64, 64, 16, 2, 2, true>(epi, a, stream);
-    case 5: return launch_cfg<256, 256, 32, 4, 2, false>(epi, a, stream);
-    case 6: return launch_cfg<128, 256, 16, 2, 2, false>(epi, a, stream);
+    case 0: return launch_cfg<256, 256, 16, 2, 2, 1, false>(epi, a, stream);
+    case 1: return launch_cfg<256, 256, 16, 4, 2, 1, false>(epi, a, stream);
+    case 2: return launch_cfg<128, 128, 16, 2, 2, 1, false>(epi, a, stream);
+    case 3: return launch_cfg<64, 64, 16, 2, 2, 1, false>(epi, a, stream);
+    case 4: return launch_cfg<64, 64, 16, 2, 2, 1, true>(epi, a, stream);
+    case 5: return launch_cfg<256, 256, 32, 4, 2, 1, false>(epi, a, stream);
+    case 6: return launch_cfg<128, 256, 16, 2, 2, 1, false>(epi, a, stream);
+    case 7: return launch_cfg<64, 64, 32, 2, 2, 1, false>(epi, a, stream);
+    case 8: return launch_cfg<64, 64, 64, 2, 2, 1, false>(epi, a, stream);
+    case 9: return launch_cfg<128, 64, 32, 2, 2, 1, false>(epi, a, stream);
+    case 10: return launch_cfg<64, 128, 32, 2, 2, 1, false>(epi, a, stream);
+    case 11: return launch_cfg<128, 128, 32, 2, 2, 1, false>(epi, a, stream);
+    case 12: return launch_cfg<32, 32, 32, 1, 1, 1, false>(epi, a, stream);
+    case 13: return launch_cfg<32, 32, 64, 1, 1, 1, false>(epi, a, stream);
+    case 14: return launch_cfg<64, 64, 64, 2, 2, 2, false>(epi, a, stream);
+    case 15: return launch_cfg<64, 64, 32, 2, 2, 2, false>(epi, a, stream);
+    case 16: return launch_cfg<32, 32, 64, 1, 1, 2, false>(epi, a, stream);
+    case 17: return launch_cfg<32, 32, 64, 1, 1, 4, false>(epi, a, stream);
+    case 18: return launch_cfg<128, 128, 32, 2, 2, 2, false>(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }
