@@ -672,9 +672,9 @@ int edsl_hip_dense_f32_launch(const float* X, int64_t ldx, const float* W, int64
   return guarded([&] {
     if (epi_has_bias(epilogue) && !bias && N > 0) fail(kErrArgument, "epilogue adds a bias but bias is null");
     if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) fail(kErrArgument, "null operand");
-    if (ldx < std::max<int64_t>(K, 1) && M > 1) fail(kErrStride, "ldx < K");
-    if (ldw < std::max<int64_t>(N, 1) && K > 1) fail(kErrStride, "ldw < N");
-    if (ldy < std::max<int64_t>(N, 1) && M > 1) fail(kErrStride, "ldy < N");
+    if (K > 0 && M > 1 && ldx < K) fail(kErrStride, "ldx < K");
+    if (N > 0 && K > 1 && ldw < N) fail(kErrStride, "ldw < N");
+    if (N > 0 && M > 1 && ldy < N) fail(kErrStride, "ldy < N");
     std::lock_guard<std::mutex> lock(g_mu);
     read_env_overrides();
     DeviceState& ds = device_state(nullptr);
@@ -689,9 +689,9 @@ int edsl_hip_dense_i32_launch(const int32_t* X, int64_t ldx, const int32_t* W, i
   return guarded([&] {
     if (epi_has_bias(epilogue) && !bias && N > 0) fail(kErrArgument, "epilogue adds a bias but bias is null");
     if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) fail(kErrArgument, "null operand");
-    if (ldx < std::max<int64_t>(K, 1) && M > 1) fail(kErrStride, "ldx < K");
-    if (ldw < std::max<int64_t>(N, 1) && K > 1) fail(kErrStride, "ldw < N");
-    if (ldy < std::max<int64_t>(N, 1) && M > 1) fail(kErrStride, "ldy < N");
+    if (K > 0 && M > 1 && ldx < K) fail(kErrStride, "ldx < K");
+    if (N > 0 && K > 1 && ldw < N) fail(kErrStride, "ldw < N");
+    if (N > 0 && M > 1 && ldy < N) fail(kErrStride, "ldy < N");
     std::lock_guard<std::mutex> lock(g_mu);
     read_env_overrides();
     DeviceState& ds = device_state(nullptr);

@@ -1,0 +1,106 @@
+"""Seeded random parity cases for the dense path through the C ABI.
+
+Each case draws a shape (including K = 0 and sizes that are no multiple of
+any tile), a dtype, a pattern, host or device operands, and for device
+operands a padded row stride and an element offset, then compares the HIP
+result with the oracle: i32 bit-exact (int8-range values take the int8 MFMA
+path, wider ones the exact i32 fallback), f32 within relative Frobenius 1e-5
+and max|delta| <= 1e-4*sqrt(K).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_f32_parity
+from mlir_edsl_hip import _native
+from mlir_edsl_hip.device import dense_launch
+
+pytestmark = pytest.mark.gpu
+
+_PATTERNS = {"matmul": (False, "none"), "matmul_relu": (False, "relu"), "matmul_bias": (True, "none"),
+             "dense_relu": (True, "relu"), "dense_leaky": (True, "leaky")}
+_EPI = {"none": 0, "relu": 1, "leaky": 2}
+
+
+def _case(seed):
+    rng = np.random.default_rng(seed)
+    dims = [1, 2, 3, 7, 16, 17, 31, 32, 33, 63, 64, 65, 96, 127, 128, 129, 200, 256, 300]
+    M, N = (int(rng.choice(dims)) for _ in range(2))
+    K = int(rng.choice(dims + [0]))
+    dtype = "i32" if rng.random() < 0.4 else "f32"
+    pats = [p for p in _PATTERNS if not (dtype == "i32" and p == "dense_leaky")]
+    pattern = pats[int(rng.integers(len(pats)))]
+    device = bool(rng.random() < 0.6)
+    pad = int(rng.choice([0, 0, 1, 3, 4, 9])) if device else 0
+    off = int(rng.choice([0, 0, 1, 2, 4])) if device else 0
+    wide = dtype == "i32" and rng.random() < 0.3
+    return rng, M, K, N, dtype, pattern, device, pad, off, wide
+
+
+def _draw(rng, shape, dtype, wide):
+    if dtype == "f32":
+        return rng.standard_normal(shape, dtype=np.float32)
+    lim = 2**31 if wide else 128
+    return rng.integers(-lim, lim, size=shape, dtype=np.int64).astype(np.int32)
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    assert torch.cuda.is_available()
+    return torch
+
+
+def _device_view(torch, a, pad, off):
+    """a copied to the device as a view with row stride cols + pad and an
+    element offset off."""
+    if a.ndim == 1:
+        buf = torch.empty(a.shape[0] + off, dtype=torch.float32 if a.dtype == np.float32 else torch.int32,
+                          device="cuda")
+        v = buf[off:off + a.shape[0]]
+        v.copy_(torch.from_numpy(a))
+        return v
+    rows, cols = a.shape
+    buf = torch.empty(rows * (cols + pad) + off + 1, dtype=torch.float32 if a.dtype == np.float32 else torch.int32,
+                      device="cuda")
+    v = buf[off:off + rows * (cols + pad)].view(rows, cols + pad)[:, :cols]
+    v.copy_(torch.from_numpy(a))
+    return v
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_random_case(seed, torch_cuda):
+    torch = torch_cuda
+    rng, M, K, N, dtype, pattern, device, pad, off, wide = _case(seed)
+    bias, act = _PATTERNS[pattern]
+    X = _draw(rng, (M, K), dtype, wide)
+    W = _draw(rng, (K, N), dtype, wide)
+    b = _draw(rng, (N,), dtype, wide) if bias else None
+    alpha = float(np.float32(rng.uniform(0.01, 0.5)))
+    if dtype == "f32":
+        ref = oracle.dense_f32(X, W, b, act, alpha)
+    else:
+        ref = oracle.dense_i32(X, W, b, act)
+    epi = (1 if bias else 0) | (_EPI[act] << 1)
+    if device:
+        tX, tW = _device_view(torch, X, pad, off), _device_view(torch, W, pad, off)
+        tb = _device_view(torch, b, 0, off) if bias else None
+        tY = _device_view(torch, np.zeros((M, N), X.dtype), pad, off)
+        dense_launch(tX, tW, tb, tY, epi, alpha)
+        torch.cuda.synchronize()
+        got = tY.cpu().numpy()
+    else:
+        from mlir_edsl_hip import backend
+        args = [X, W] + ([b] if bias else [])
+        got = backend.run(pattern, *args, alpha=alpha)
+    what = f"seed={seed} {dtype} {pattern} M={M} K={K} N={N} device={device} pad={pad} off={off} " \
+           f"wide={wide} [{_native.last_plan()}]"
+    if dtype == "i32":
+        assert np.array_equal(got, ref), what
+    else:
+        try:
+            assert_f32_parity(got, ref, K)
+        except AssertionError as e:
+            raise AssertionError(f"{what}: {e}") from None
