@@ -9,8 +9,10 @@ layer 2048^3 (c5), 1024^3 (c2) and the 256^3 matmul (c1).
 
 A step is one call of the dense layer on device-resident inputs (the
 C-ABI launch entry point, enqueued on torch's current stream). W warmup
-steps, then K timed steps between two device synchronisations; per-launch
-HIP events on the same stream give the kernel time used for the roofline.
+steps, then K timed steps between two device synchronisations. Two HIP
+events on the same stream bracket the K steps; their device time / K is the
+average launch duration used for the roofline. A second pass with one event
+pair per launch reports the spread.
 The CPU baseline times the oracle (a C restatement of the reference CPU-JIT
 schedule) on a row sample of the same workload, on this host's cores.
 
@@ -68,22 +70,36 @@ def measure(wname: str, steps: int, warmup: int, rotate: int = 1) -> dict:
         launch(i)
     torch.cuda.synchronize()
     plan = _native.last_plan()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    # Timed region: K steps back to back between one pair of events. Its
+    # device time / K is the average launch duration (the two events' own
+    # latency, ~4 us on this stack, is spread over K steps instead of being
+    # added to every step).
+    region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    region[0].record()
+    for i in range(steps):
+        launch(i)
+    region[1].record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    device_ms = region[0].elapsed_time(region[1]) / steps
+    # Spread: one event pair around each launch (each pair carries the event
+    # latency, so these read high for short launches).
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     for i in range(steps):
         starts[i].record()
         launch(i)
         ends[i].record()
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
     kms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     res = {
         "workload": wname,
         "ms_per_step": (t1 - t0) * 1e3 / steps,
-        "kernel_ms_mean": statistics.fmean(kms),
-        "kernel_ms_median": statistics.median(kms),
+        "kernel_ms_mean": device_ms,
+        "event_pair_ms_median": statistics.median(kms),
+        "event_pair_ms_min": min(kms),
         "plan": plan,
         "rotate_w": rotate,
     }

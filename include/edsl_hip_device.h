@@ -59,8 +59,9 @@ void edsl_hip_set_gemv_ksplit(int ksplit);
 /* Small-M column block: columns per workgroup, one of 32, 64, 128, 256;
  * 0 = automatic. */
 void edsl_hip_set_gemv_cols(int cols);
-/* int8 GEMM pipeline variant (waves per workgroup x stages in flight), index
- * < edsl_hip_i8_variant_count(); -1 = automatic. */
+/* int8 GEMM variant = operand prefetch depth in 32-k steps (0: 4, 1: 2,
+ * 2: 8 when K % 256 == 0, else 4), index < edsl_hip_i8_variant_count();
+ * -1 = automatic. */
 void edsl_hip_set_i8_variant(int variant);
 int edsl_hip_i8_variant_count(void);
 int edsl_hip_f32_config_count(void);

@@ -11,11 +11,12 @@
 // the product can run on v_mfma_i32_32x32x32_i8 exactly: each product fits in
 // 15 bits and the i32 accumulator cannot overflow for K < 2^17, so the sum
 // equals the exact integer sum -- identical to the wrapping i32 sum in any
-// order. A pre-pass narrows X to int8 [M][K] and W to int8 [N][K] (transposed,
-// so both MFMA operands are K-contiguous) and flags any out-of-range value.
-// The GEMM kernel reads the flag: if set, the whole grid takes the exact
-// wrapping-i32 vector-ALU path on the original i32 tensors instead. The flag
-// is compared against a per-call epoch, so it never needs clearing.
+// order. A pre-pass narrows X and W to int8 and writes them fragment-packed
+// (each 32x32 block stored as the 64 lanes x 16 bytes the MFMA consumes, W
+// transposed on the way), and flags any out-of-range value. The GEMM reads the
+// flag: if set, the whole grid takes the exact wrapping-i32 vector-ALU path on
+// the original i32 tensors instead. The flag is compared against a per-call
+// epoch, so it never needs clearing.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -23,11 +24,10 @@ namespace edsl {
 namespace {
 
 // ------------------------------------------------------------------ pre-pass
-// Only used on the int8 path, where M, N and K are multiples of kI8Tile, so
-// X8 rows (K bytes) and W8t rows start 16-byte aligned. The i32 sources may
-// have any alignment / row stride: `vec_ok` selects 16-byte source loads.
+// Only used on the int8 path, where M, N and K are multiples of kI8Tile. The
+// i32 sources may have any alignment / row stride: `vec_ok` selects 16-byte
+// source loads.
 constexpr int kNarrowTile = 64;
-constexpr int kNarrowLdp = kNarrowTile + 4;  // LDS row pitch (bytes) of the transposed tile
 
 __device__ __forceinline__ uint32_t pack_i8x4(i32x4 v, bool& bad) {
   uint32_t out = 0;
@@ -44,46 +44,61 @@ __device__ __forceinline__ i32x4 load4(const int32_t* p, bool vec_ok) {
   return i32x4{p[0], p[1], p[2], p[3]};
 }
 
-// Grid: 64x64 tiles of X (no transpose) followed by 64x64 tiles of W
-// (transposed through LDS).
+// Byte offset of element (r, k) inside a 64x64 tile held as its four packed
+// fragments (2 row blocks x 2 k steps, 1 KB each, in [rb][kt] order).
+__device__ __forceinline__ int tile_packed_offset(int r, int k) {
+  return ((((r >> 5) * 2 + (k >> 5)) * 64 + (r & 31) + 32 * ((k >> 4) & 1)) << 4) + (k & 15);
+}
+
+// Grid: 64x64 tiles of X, then 64x64 tiles of W. Thread t owns a 4x4 block of
+// the tile (4 row loads of 16 bytes), narrows it, and writes it into LDS in
+// packed order: for X each 16-byte row piece is already 4 consecutive k of one
+// row (one packed word); for W the 4x4 block is transposed in registers so each
+// word holds 4 consecutive k of one column. The packed tile then leaves with
+// one 16-byte store per thread (four 1 KB fragments).
 __global__ void __launch_bounds__(256) narrow_i8_kernel(NarrowI8Args a, int vec_ok_x, int vec_ok_w) {
+  __shared__ uint32_t pk[kNarrowTile * kNarrowTile / 4];
   const int tid = threadIdx.x;
+  const int bi = tid >> 4;        // 4-row block along the source's rows
+  const int bj = 4 * (tid & 15);  // 4-column block along the source's columns
   const int x_tiles_k = a.K / kNarrowTile;
   const int x_tiles = (a.M / kNarrowTile) * x_tiles_k;
   bool bad = false;
+  int r0, k0;  // tile origin in the packed matrix's (row, k) coordinates
+  int8_t* dst;
   if ((int)blockIdx.x < x_tiles) {
-    const int tm = blockIdx.x / x_tiles_k, tk = blockIdx.x % x_tiles_k;
+    r0 = (blockIdx.x / x_tiles_k) * kNarrowTile;
+    k0 = (blockIdx.x % x_tiles_k) * kNarrowTile;
+    dst = a.X8p;
+    i32x4 v[4];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int idx = tid + p * 256;
-      const int m = tm * kNarrowTile + idx / 16;
-      const int k = tk * kNarrowTile + 4 * (idx % 16);
-      const i32x4 v = load4(a.X + (int64_t)m * a.ldx + k, vec_ok_x);
-      *reinterpret_cast<uint32_t*>(a.X8 + (int64_t)m * a.K + k) = pack_i8x4(v, bad);
-    }
+    for (int i = 0; i < 4; ++i) v[i] = load4(a.X + (int64_t)(r0 + 4 * bi + i) * a.ldx + k0 + bj, vec_ok_x);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pk[tile_packed_offset(4 * bi + i, bj) >> 2] = pack_i8x4(v[i], bad);
   } else {
-    __shared__ uint8_t t[kNarrowTile * kNarrowLdp];  // [n][k]
     const int b = blockIdx.x - x_tiles;
     const int w_tiles_n = a.N / kNarrowTile;
-    const int tk = b / w_tiles_n, tn = b % w_tiles_n;
+    k0 = (b / w_tiles_n) * kNarrowTile;
+    r0 = (b % w_tiles_n) * kNarrowTile;  // packed rows are W's columns
+    dst = a.W8p;
+    uint32_t q[4];  // q[i] = W row k0 + 4bi + i, columns r0 + bj .. + 3 (byte e = column e)
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int idx = tid + p * 256;
-      const int r = idx / 16;        // k within tile
-      const int c = 4 * (idx % 16);  // n within tile
-      const i32x4 v = load4(a.W + (int64_t)(tk * kNarrowTile + r) * a.ldw + tn * kNarrowTile + c, vec_ok_w);
-      const uint32_t q = pack_i8x4(v, bad);
+    for (int i = 0; i < 4; ++i)
+      q[i] = pack_i8x4(load4(a.W + (int64_t)(k0 + 4 * bi + i) * a.ldw + r0 + bj, vec_ok_w), bad);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) t[(c + e) * kNarrowLdp + r] = (uint8_t)(q >> (8 * e));
+    for (int e = 0; e < 4; ++e) {
+      // column r0 + bj + e, rows k0 + 4bi .. + 3 as one word (byte i = row i)
+      uint32_t w = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w |= ((q[i] >> (8 * e)) & 0xffu) << (8 * i);
+      pk[tile_packed_offset(bj + e, 4 * bi) >> 2] = w;
     }
-    __syncthreads();
-    // Thread writes 16 consecutive k of one n row as one 16-byte store.
-    const int n = tid / 4;
-    const int c = 16 * (tid % 4);
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(t + n * kNarrowLdp + c);
-    const i32x4 out = {(int)src[0], (int)src[1], (int)src[2], (int)src[3]};
-    *reinterpret_cast<i32x4*>(a.W8t + (int64_t)(tn * kNarrowTile + n) * a.K + tk * kNarrowTile + c) = out;
   }
+  __syncthreads();
+  const int frag = tid >> 6, lane = tid & 63;
+  const int rb = (r0 >> 5) + (frag >> 1), kt = (k0 >> 5) + (frag & 1);
+  const i32x4 out = reinterpret_cast<const i32x4*>(pk)[tid];
+  *reinterpret_cast<i32x4*>(dst + ((((int64_t)rb * (a.K >> 5) + kt) * 64 + lane) << 4)) = out;
   if (__any(bad) && (tid & 63) == 0) *a.flag = a.epoch;
 }
 
@@ -159,129 +174,97 @@ __global__ void __launch_bounds__(256) gemm_i32_valu_kernel(GemmI32Args a) {
 }
 
 // -------------------------------------------------------- int8 MFMA kernel
-// 128x128 output tile per workgroup of WAVES waves (4: 2x2 waves of 64x64;
-// 8: 4x2 waves of 32x64), K staged BKB bytes at a time through two LDS
-// buffers (the next stage's global loads are issued before the current
-// stage's MFMAs and written to the other buffer after them). LDS rows are BKB
-// bytes = BKB/16 chunks of 16 B with the chunk index XOR-ed by (row % 8), so
-// the 16-byte fragment reads of 16 consecutive rows spread over the banks.
-// Inside a stage the fragments of 32-k step t+1 are read from LDS while the
-// MFMAs of step t run, so the matrix cores do not wait on LDS latency.
-// v_mfma_i32_32x32x32_i8: lane l supplies 16 int8 of A row l%32 and 16 int8
-// of B^T row (= output column) l%32, both from chunk (2t + l/32) of the
-// 32-k step t, so A and B always pair the same k.
-template <int BKB>
-struct I8Smem {
-  i32x4 a[2][kI8Tile * (BKB / 16)];
-  i32x4 b[2][kI8Tile * (BKB / 16)];
-};
-
-template <int EPI, int WAVES, int BKB>
-__global__ void __launch_bounds__(WAVES * 64) gemm_i8_kernel(GemmI32Args a) {
-  constexpr int NT = WAVES * 64;
-  constexpr int CH = BKB / 16;                 // 16-byte chunks per row per stage
-  constexpr int TS = BKB / 32;                 // 32-k MFMA steps per stage
-  constexpr int WAVES_N = 2;
-  constexpr int WAVES_M = WAVES / WAVES_N;
-  constexpr int RBM = kI8Tile / WAVES_M / 32;  // 32-row blocks per wave
-  constexpr int RBN = kI8Tile / WAVES_N / 32;  // 32-col blocks per wave
-  constexpr int LD = kI8Tile * CH / NT;        // chunks per thread per operand per stage
-  __shared__ union {
-    I8Smem<BKB> mf;
-    ValuSmem valu;
-  } sm;
+// 128x128 output tile per workgroup of 4 waves, each wave a 64x64 quadrant
+// (2x2 blocks of 32x32). Operands come straight from the fragment-packed
+// copies: each fragment is one fully coalesced 16-byte load per lane in the
+// exact MFMA operand layout, so nothing is staged through LDS and no lane
+// shuffles are needed. Fragments of step s + D are loaded while the MFMAs of
+// step s run (D steps in flight; past the last step the last step is loaded
+// again, which keeps the loop free of branches so the wait counts stay exact).
+// v_mfma_i32_32x32x32_i8: lane l supplies 16 int8 of A row l%32 and of B^T row
+// (= output column) l%32 from k-chunk l/32 of the step, so A and B always
+// pair the same k.
+template <int EPI, int D>
+__global__ void __launch_bounds__(256) gemm_i8_kernel(GemmI32Args a) {
+  __shared__ ValuSmem valu;
   int tm, tn;
   tile_coords(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
   const int m0 = tm * kI8Tile, n0 = tn * kI8Tile;
 
   if (*a.flag == a.epoch) {  // some value outside int8: exact i32 path
-    valu_tile_i32<EPI, NT>(a, m0, n0, sm.valu);
+    valu_tile_i32<EPI, 256>(a, m0, n0, valu);
     return;
   }
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = (wave / WAVES_N) * (32 * RBM);
-  const int wn = (wave % WAVES_N) * (32 * RBN);
-  const int half = lane >> 5;
-  const int l32 = lane & 31;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int KT = a.K >> 5;  // 32-k steps; a multiple of D
+  const i32x4* ap[2];
+  const i32x4* bp[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    ap[i] = reinterpret_cast<const i32x4*>(a.A8p) + (int64_t)((m0 >> 5) + 2 * wm + i) * KT * 64 + lane;
+    bp[i] = reinterpret_cast<const i32x4*>(a.B8p) + (int64_t)((n0 >> 5) + 2 * wn + i) * KT * 64 + lane;
+  }
 
-  i32x4 ra[LD], rb[LD];
-  auto load_global = [&](int k0) {
+  i32x16 acc[2][2];
 #pragma unroll
-    for (int i = 0; i < LD; ++i) {
-      const int idx = tid + i * NT;
-      const int r = idx / CH, q = idx % CH;
-      ra[i] = *reinterpret_cast<const i32x4*>(a.A8 + (int64_t)(m0 + r) * a.K + k0 + 16 * q);
-      rb[i] = *reinterpret_cast<const i32x4*>(a.B8t + (int64_t)(n0 + r) * a.K + k0 + 16 * q);
-    }
-  };
-  // chunk q of row `row` lives at slot q ^ (row % min(CH, 8)): stays below CH
-  auto swz = [](int row, int q) { return row * CH + (q ^ (row % (CH < 8 ? CH : 8))); };
-  auto store_lds = [&](int buf) {
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int i = 0; i < LD; ++i) {
-      const int idx = tid + i * NT;
-      const int r = idx / CH, q = idx % CH;
-      sm.mf.a[buf][swz(r, q)] = ra[i];
-      sm.mf.b[buf][swz(r, q)] = rb[i];
-    }
-  };
-
-  i32x16 acc[RBM][RBN];
-#pragma unroll
-  for (int i = 0; i < RBM; ++i)
-#pragma unroll
-    for (int j = 0; j < RBN; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  auto read_frags = [&](int buf, int t, i32x4 (&av)[RBM], i32x4 (&bv)[RBN]) {
-    const int q = 2 * t + half;
+  // Prologue loads in the loop's order (slot by slot): the wait counts at the
+  // loop head are exact only if the two orders agree.
+  i32x4 fa[D][2], fb[D][2];
 #pragma unroll
-    for (int i = 0; i < RBM; ++i) av[i] = sm.mf.a[buf][swz(wm + 32 * i + l32, q)];
+  for (int d = 0; d < D; ++d) {
+    const int s = min(d, KT - 1);
 #pragma unroll
-    for (int j = 0; j < RBN; ++j) bv[j] = sm.mf.b[buf][swz(wn + 32 * j + l32, q)];
-  };
-  auto compute = [&](int buf) {
-    i32x4 av[2][RBM], bv[2][RBN];
-    read_frags(buf, 0, av[0], bv[0]);
-#pragma unroll
-    for (int t = 0; t < TS; ++t) {
-      if (t + 1 < TS) read_frags(buf, t + 1, av[(t + 1) & 1], bv[(t + 1) & 1]);
-#pragma unroll
-      for (int i = 0; i < RBM; ++i)
-#pragma unroll
-        for (int j = 0; j < RBN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[t & 1][i], bv[t & 1][j], acc[i][j], 0, 0, 0);
+    for (int i = 0; i < 2; ++i) {
+      fa[d][i] = ap[i][(int64_t)s * 64];
+      fb[d][i] = bp[i][(int64_t)s * 64];
     }
-  };
-
-  const int nk = a.K / BKB;
-  load_global(0);
-  store_lds(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) load_global((kt + 1) * BKB);
-    compute(buf);
-    if (more) store_lds(buf ^ 1);
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll 1
+  for (int s0 = 0; s0 < KT; s0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[d][i], fb[d][j], acc[i][j], 0, 0, 0);
+      // Keep the refill of this slot after its MFMAs and before the next
+      // slot's, so each slot's loads stay D steps ahead of their use.
+      __builtin_amdgcn_sched_barrier(0);
+      const int sn = min(s0 + d + D, KT - 1);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        fa[d][i] = ap[i][(int64_t)sn * 64];
+        fb[d][i] = bp[i][(int64_t)sn * 64];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
-  // Epilogue: lane holds rows 8*(r/4) + 4*half + r%4 and column l32 of each block.
+  // Epilogue: lane holds rows 8*(r/4) + 4*half + r%4 and column l32 of each
+  // block; each store instruction writes two full 128-byte row segments.
+  // Non-temporal: the result is not re-read by this kernel.
+  const int half = lane >> 5, l32 = lane & 31;
 #pragma unroll
-  for (int j = 0; j < RBN; ++j) {
-    const int n = n0 + wn + 32 * j + l32;
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + 64 * wn + 32 * j + l32;
     const int32_t b = epi_has_bias(EPI) ? a.bias[n] : 0;
 #pragma unroll
-    for (int i = 0; i < RBM; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * half + (r & 3);
-        a.C[(int64_t)m * a.ldc + n] = apply_epilogue_i32<EPI>(acc[i][j][r], b);
+        const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * half + (r & 3);
+        __builtin_nontemporal_store(apply_epilogue_i32<EPI>(acc[i][j][r], b), a.C + (int64_t)m * a.ldc + n);
       }
   }
 }
@@ -304,24 +287,12 @@ __global__ void __launch_bounds__(WAVES * 64) gemm_i8_kernel(GemmI32Args a) {
       return hipErrorInvalidValue;                                                     \
   }
 
-}  // namespace
-
-hipError_t launch_narrow_i8(NarrowI8Args a, hipStream_t stream) {
-  if (a.M % kNarrowTile || a.N % kNarrowTile || a.K % kNarrowTile) return hipErrorInvalidValue;
-  const int x_tiles = (a.M / kNarrowTile) * (a.K / kNarrowTile);
-  const int w_tiles = (a.K / kNarrowTile) * (a.N / kNarrowTile);
-  const int vec_x = ((reinterpret_cast<uintptr_t>(a.X) & 15) == 0) && (a.ldx % 4 == 0);
-  const int vec_w = ((reinterpret_cast<uintptr_t>(a.W) & 15) == 0) && (a.ldw % 4 == 0);
-  hipLaunchKernelGGL(narrow_i8_kernel, dim3(x_tiles + w_tiles), dim3(256), 0, stream, a, vec_x, vec_w);
-  return hipGetLastError();
-}
-
-template <int WAVES, int BKB>
-hipError_t launch_i8_variant(int epi, const GemmI32Args& a, hipStream_t stream) {
-  const dim3 grid(a.tiles_m * a.tiles_n), block(WAVES * 64);
-#define EDSL_I8_CASE(E)                                                                             \
-  case E:                                                                                           \
-    hipLaunchKernelGGL((gemm_i8_kernel<E, WAVES, BKB>), grid, block, 0, stream, a);                \
+template <int D>
+hipError_t launch_i8_depth(int epi, const GemmI32Args& a, hipStream_t stream) {
+  const dim3 grid(a.tiles_m * a.tiles_n), block(256);
+#define EDSL_I8_CASE(E)                                                              \
+  case E:                                                                            \
+    hipLaunchKernelGGL((gemm_i8_kernel<E, D>), grid, block, 0, stream, a);           \
     break;
   switch (epi) {
     EDSL_I8_CASE(epi_code(false, ACT_NONE))
@@ -335,17 +306,33 @@ hipError_t launch_i8_variant(int epi, const GemmI32Args& a, hipStream_t stream) 
   return hipGetLastError();
 }
 
+}  // namespace
+
+hipError_t launch_narrow_i8(NarrowI8Args a, hipStream_t stream) {
+  if (a.M % kNarrowTile || a.N % kNarrowTile || a.K % kNarrowTile) return hipErrorInvalidValue;
+  const int x_tiles = (a.M / kNarrowTile) * (a.K / kNarrowTile);
+  const int w_tiles = (a.K / kNarrowTile) * (a.N / kNarrowTile);
+  const int vec_x = ((reinterpret_cast<uintptr_t>(a.X) & 15) == 0) && (a.ldx % 4 == 0);
+  const int vec_w = ((reinterpret_cast<uintptr_t>(a.W) & 15) == 0) && (a.ldw % 4 == 0);
+  hipLaunchKernelGGL(narrow_i8_kernel, dim3(x_tiles + w_tiles), dim3(256), 0, stream, a, vec_x, vec_w);
+  return hipGetLastError();
+}
+
+int gemm_i8_depth(int variant, int K) {
+  if (variant < 0 || variant >= kI8Variants) variant = kI8DefaultVariant;
+  static const int kDepth[kI8Variants] = {4, 2, 8};
+  const int d = kDepth[variant];
+  return (K / 32) % d == 0 ? d : 4;  // K % 128 == 0 on this path, so 4 always divides
+}
+
 hipError_t launch_gemm_i8(int epi, GemmI32Args a, hipStream_t stream, int variant) {
+  if (a.M % kI8Tile || a.N % kI8Tile || a.K % kI8Tile || a.K <= 0) return hipErrorInvalidValue;
   a.tiles_m = a.M / kI8Tile;
   a.tiles_n = a.N / kI8Tile;
-  if (variant < 0) variant = kI8DefaultVariant;
-  if (a.K % 256 != 0 && (variant == 1 || variant == 3)) variant = (variant == 1) ? 0 : 2;
-  switch (variant) {
-    case 0: return launch_i8_variant<4, 128>(epi, a, stream);
-    case 1: return launch_i8_variant<4, 256>(epi, a, stream);
-    case 2: return launch_i8_variant<8, 128>(epi, a, stream);
-    case 3: return launch_i8_variant<8, 256>(epi, a, stream);
-    case 4: return launch_i8_variant<4, 64>(epi, a, stream);
+  switch (gemm_i8_depth(variant, a.K)) {
+    case 2: return launch_i8_depth<2>(epi, a, stream);
+    case 4: return launch_i8_depth<4>(epi, a, stream);
+    case 8: return launch_i8_depth<8>(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

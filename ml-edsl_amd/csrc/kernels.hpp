@@ -53,11 +53,16 @@ int gemv_f32_max_ksplit();
 constexpr int kGemvMaxM = 64;
 
 // ------------------------------------------------------------- integer path
+// Fragment-packed int8 operand. A row-major int8 [R][K] matrix (R = the M rows
+// of X, or the N columns of W) is stored as 32x32 fragments, ordered
+// [R/32][K/32]; fragment (rb, kt) holds rows 32rb.. and k 32kt.. as 64 lanes x
+// 16 bytes with lane = r % 32 + 32 * ((k % 32) / 16) and byte = k % 16 -- the
+// v_mfma_i32_32x32x32_i8 operand of that block, one 16-byte load per lane.
 struct NarrowI8Args {
   const int32_t* X;   // [M][K], ldx
   const int32_t* W;   // [K][N], ldw
-  int8_t* X8;         // [M][K] dense
-  int8_t* W8t;        // [N][K] dense (transposed)
+  int8_t* X8p;        // X narrowed, fragment-packed over (M, K)
+  int8_t* W8p;        // W narrowed, fragment-packed over (N, K) (W transposed)
   int64_t ldx, ldw;
   int M, N, K;
   unsigned* flag;     // set to `epoch` when a value lies outside [-128, 127]
@@ -65,8 +70,8 @@ struct NarrowI8Args {
 };
 
 struct GemmI32Args {
-  const int8_t* A8;   // [M][K] dense  (int8 fast path)
-  const int8_t* B8t;  // [N][K] dense  (int8 fast path)
+  const int8_t* A8p;  // fragment-packed X (int8 fast path)
+  const int8_t* B8p;  // fragment-packed W^T (int8 fast path)
   const int32_t* X;   // [M][K], ldx   (exact i32 fallback)
   const int32_t* W;   // [K][N], ldw   (exact i32 fallback)
   const int32_t* bias;
@@ -80,10 +85,11 @@ struct GemmI32Args {
 
 constexpr int kI8Tile = 128;   // M, N, K multiples of this for the int8 MFMA path
 hipError_t launch_narrow_i8(NarrowI8Args args, hipStream_t stream);
-// variant (waves x K bytes per stage): 0 = 4x128, 1 = 4x256, 2 = 8x128, 3 = 8x256, 4 = 4x64;
-// -1 = default. Variants with 256-byte stages need K % 256 == 0.
-constexpr int kI8Variants = 5;
-constexpr int kI8DefaultVariant = 3;
+// variant = fragment prefetch depth in 32-k steps: 0 = 4, 1 = 2, 2 = 8 (needs
+// K % 256 == 0, else 4); -1 = default.
+constexpr int kI8Variants = 3;
+constexpr int kI8DefaultVariant = 0;
+int gemm_i8_depth(int variant, int K);
 hipError_t launch_gemm_i8(int epi, GemmI32Args args, hipStream_t stream, int variant = -1);
 // Exact wrapping i32 GEMM on the vector ALUs: any shape, any alignment.
 hipError_t launch_gemm_i32_valu(int epi, GemmI32Args args, hipStream_t stream);

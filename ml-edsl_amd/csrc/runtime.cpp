@@ -358,8 +358,8 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     NarrowI8Args n{};
     n.X = a.X;
     n.W = a.W;
-    n.X8 = x8;
-    n.W8t = w8;
+    n.X8p = x8;
+    n.W8p = w8;
     n.ldx = a.ldx;
     n.ldw = a.ldw;
     n.M = a.M;
@@ -368,14 +368,14 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     n.flag = flag;
     n.epoch = ds.epoch;
     check_hip(launch_narrow_i8(n, stream), "narrow_i8 launch");
-    a.A8 = x8;
-    a.B8t = w8;
+    a.A8p = x8;
+    a.B8p = w8;
     a.flag = flag;
     a.epoch = ds.epoch;
-    int variant = (g_force_i8 >= 0 && g_force_i8 < kI8Variants) ? g_force_i8 : kI8DefaultVariant;
-    if (a.K % 256 != 0 && (variant == 1 || variant == 3)) variant = (variant == 1) ? 0 : 2;
+    const int variant = (g_force_i8 >= 0 && g_force_i8 < kI8Variants) ? g_force_i8 : kI8DefaultVariant;
     check_hip(launch_gemm_i8(L.epi, a, stream, variant), "gemm_i8 launch");
-    set_plan("narrow_i8+gemm_i8 variant=%d grid=%d", variant, (a.M / kI8Tile) * (a.N / kI8Tile));
+    set_plan("narrow_i8+gemm_i8 variant=%d depth=%d grid=%d", variant, gemm_i8_depth(variant, a.K),
+             (a.M / kI8Tile) * (a.N / kI8Tile));
   } else {
     check_hip(launch_gemm_i32_valu(L.epi, a, stream), "gemm_i32_valu launch");
     set_plan("gemm_i32_valu grid=%d", ((a.M + 127) / 128) * ((a.N + 127) / 128));
