@@ -86,9 +86,9 @@ struct GemmI32Args {
 constexpr int kI8Tile = 128;   // M, N, K multiples of this for the int8 MFMA path
 hipError_t launch_narrow_i8(NarrowI8Args args, hipStream_t stream);
 // variant = fragment prefetch depth in 32-k steps: 0 = 4, 1 = 2, 2 = 8 (needs
-// K % 256 == 0, else 4); -1 = default.
+// K % 256 == 0, else 4); -1 = default (8: measured fastest at 2048^3).
 constexpr int kI8Variants = 3;
-constexpr int kI8DefaultVariant = 0;
+constexpr int kI8DefaultVariant = 2;
 int gemm_i8_depth(int variant, int K);
 hipError_t launch_gemm_i8(int epi, GemmI32Args args, hipStream_t stream, int variant = -1);
 // Exact wrapping i32 GEMM on the vector ALUs: any shape, any alignment.
