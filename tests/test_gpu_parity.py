@@ -224,6 +224,44 @@ def test_every_int8_variant(torch_cuda):
         set_i8_variant(-1)
 
 
+@pytest.mark.parametrize("K", [128, 384, 1152])
+def test_int8_depth_fallback_and_strided_sources(K, torch_cuda):
+    """K/32 = 4, 12, 36 steps: prefetch depth 8 does not divide them, so every
+    variant runs at depth 4 or 2 (the plan names the depth). The sources are
+    device views with an odd row pitch and an element offset, so the
+    narrowing pass takes its unaligned 4-byte loads."""
+    import torch
+    from mlir_edsl_hip.device import dense_launch, set_i8_variant
+    rng = np.random.default_rng(K)
+    M, N = 256, 128
+    X = rng.integers(-128, 128, size=(M, K), dtype=np.int32)
+    W = rng.integers(-128, 128, size=(K, N), dtype=np.int32)
+    b = rng.integers(-2**20, 2**20, size=(N,), dtype=np.int32)
+    exp = oracle.dense_i32(X, W, b, "relu")
+
+    def view(a, pad, off):
+        rows, cols = a.shape
+        buf = torch.zeros(rows * (cols + pad) + off, dtype=torch.int32, device="cuda")
+        v = buf[off:].view(rows, cols + pad)[:, :cols]
+        v.copy_(torch.from_numpy(a))
+        return v
+
+    tX, tW = view(X, 3, 1), view(W, 5, 2)
+    tb = torch.from_numpy(b).cuda()
+    n = _native.lib().edsl_hip_i8_variant_count()
+    try:
+        for v in range(n):
+            set_i8_variant(v)
+            tY = torch.full((M, N), -7, dtype=torch.int32, device="cuda")
+            dense_launch(tX, tW, tb, tY, _native.EPI_BIAS_RELU)
+            torch.cuda.synchronize()
+            plan = _native.last_plan()
+            assert f"variant={v}" in plan and "depth=8" not in plan, plan
+            assert np.array_equal(tY.cpu().numpy(), exp), plan
+    finally:
+        set_i8_variant(-1)
+
+
 @pytest.mark.parametrize("shape", [(1, 1, 1), (3, 5, 7), (65, 33, 17), (130, 128, 128), (128, 256, 384)])
 def test_int_shapes(shape, torch_cuda):
     M, K, N = shape
