@@ -29,6 +29,7 @@
 #include "../../include/edsl_hip_device.h"
 #include "common.hpp"
 #include "kernels.hpp"
+#include "host_stage.hpp"
 #include "runtime_internal.hpp"
 
 namespace edsl {
@@ -400,25 +401,13 @@ void launch_dense(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
 // ------------------------------------------------- synchronous host entry
 // Shapes: X [M,K], W [K,N], bias [N] (when the epilogue adds one), Y [M,N].
 // Copies a host matrix into a device buffer with rows padded to a multiple
-// of 4 elements; one contiguous copy when neither side is padded.
+// of 4 elements (and back), staged through the pinned ring.
 void copy_h2d(void* d, int64_t dld, const Mat& m, size_t es, hipStream_t stream) {
-  if (m.ld == m.cols && dld == m.cols)
-    check_hip(hipMemcpyAsync(d, m.base, (size_t)m.rows * m.cols * es, hipMemcpyHostToDevice, stream),
-              "hipMemcpyAsync H2D");
-  else
-    check_hip(hipMemcpy2DAsync(d, dld * es, m.base, m.ld * es, m.cols * es, m.rows, hipMemcpyHostToDevice,
-                               stream),
-              "hipMemcpy2DAsync H2D");
+  stage_h2d(d, dld, m.base, m.ld, m.rows, m.cols, es, stream);
 }
 
 void copy_d2h(const Mat& m, const void* d, int64_t dld, size_t es, hipStream_t stream) {
-  if (m.ld == m.cols && dld == m.cols)
-    check_hip(hipMemcpyAsync(m.base, d, (size_t)m.rows * m.cols * es, hipMemcpyDeviceToHost, stream),
-              "hipMemcpyAsync D2H");
-  else
-    check_hip(hipMemcpy2DAsync(m.base, m.ld * es, d, dld * es, m.cols * es, m.rows, hipMemcpyDeviceToHost,
-                               stream),
-              "hipMemcpy2DAsync D2H");
+  stage_d2h(m.base, m.ld, d, dld, m.rows, m.cols, es, stream);
 }
 
 void sync_dense_chain(int dtype, const LayerOp* layers, int n, const Mat& Y) {
