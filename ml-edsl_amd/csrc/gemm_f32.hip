@@ -64,7 +64,7 @@ gemm_f32_kernel(GemmF32Args args) {
   constexpr int KCH = BK / 4;
   static_assert(WM % 32 == 0, "wave tile rows must be a multiple of 32");
   static_assert(WN == 32 * CP && (CP == 1 || CP == 2 || CP == 4), "wave tile cols");
-  static_assert(BK % 8 == 0 && KCH <= 16, "BK");
+  static_assert(BK % 8 == 0 && KCH <= 32 && (KCH & (KCH - 1)) == 0, "BK");
   static_assert((BK / 8) % WAVES_K == 0, "waves splitting K need equal shares of a K step");
   constexpr int JP = BK / 8 / WAVES_K;  // 8-k groups of a K step per wave
   constexpr int A_F4 = BM * KCH;
@@ -197,9 +197,18 @@ gemm_f32_kernel(GemmF32Args args) {
   }
 
   // Waves that split K add their partial tiles into wave group 0 through
-  // LDS, in wave order (the K loop ended with a barrier).
+  // LDS, in wave order. The K loop ended with a barrier, so the A tile's LDS
+  // is free and holds the partials when it is large enough.
   if constexpr (WAVES_K > 1) {
-    __shared__ f32x4 red[WAVES_K - 1][WMN][RB * CP * 4][64];
+    using Red = f32x4[WAVES_K - 1][WMN][RB * CP * 4][64];
+    Red* red_p;
+    if constexpr (sizeof(Red) <= sizeof(sA)) {
+      red_p = reinterpret_cast<Red*>(&sA[0][0]);
+    } else {
+      __shared__ Red red_own;
+      red_p = &red_own;
+    }
+    Red& red = *red_p;
     if (wave_k > 0) {
 #pragma unroll
       for (int i = 0; i < RB; ++i)
@@ -284,6 +293,8 @@ gemm_f32_kernel(GemmF32Args args) {
 //  14-18: _kN = N waves per output block splitting each K step, partial tiles
 //         summed through LDS: 64x64x64 and 64x64x32 (k2), 32x32x64 (k2, k4),
 //         128x128x32 (k2)
+//  19-21: 64x64x128 (k2, k4) and 64x64x64 (k4): deeper K steps / more waves
+//         per CU for latency-bound mid-size shapes
 const GemmF32Config kConfigs[] = {
     {256, 256, 16, 2, 2, false, "f32_256x256x16_w2x2"},
     {256, 256, 16, 4, 2, false, "f32_256x256x16_w4x2"},
@@ -304,6 +315,9 @@ const GemmF32Config kConfigs[] = {
     {32, 32, 64, 1, 1, false, "f32_32x32x64_w1x1_k2"},
     {32, 32, 64, 1, 1, false, "f32_32x32x64_w1x1_k4"},
     {128, 128, 32, 2, 2, false, "f32_128x128x32_w2x2_k2"},
+    {64, 64, 128, 2, 2, false, "f32_64x64x128_w2x2_k2"},
+    {64, 64, 128, 2, 2, false, "f32_64x64x128_w2x2_k4"},
+    {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2_k4"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -356,6 +370,9 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case 16: return launch_cfg<32, 32, 64, 1, 1, 2, false>(epi, a, stream);
     case 17: return launch_cfg<32, 32, 64, 1, 1, 4, false>(epi, a, stream);
     case 18: return launch_cfg<128, 128, 32, 2, 2, 2, false>(epi, a, stream);
+    case 19: return launch_cfg<64, 64, 128, 2, 2, 2, false>(epi, a, stream);
+    case 20: return launch_cfg<64, 64, 128, 2, 2, 4, false>(epi, a, stream);
+    case 21: return launch_cfg<64, 64, 64, 2, 2, 4, false>(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -294,9 +294,10 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     if (g_force_cfg >= 0 && g_force_cfg < gemm_f32_num_configs() && fits(g_force_cfg)) {
       cfg = g_force_cfg;
     } else {
-      // Measured on MI355X: 256x256x32 (8 waves) at 4096^3; at 1024^3 the 64x64x64 tile with two
-      // waves per output block splitting K (26 us) beats the plain 64x64x16 one (31 us).
-      static const int kOrder[] = {5, 0, 6, 2, 14, 15, 3};
+      // Measured on MI355X: 256x256x32 (8 waves) at 4096^3; at 1024^3 the 64x64x64 tile with four
+      // waves per output block splitting K (22.8 us) beats two (23.6 us) and the plain 64x64x16
+      // tile (29.6 us).
+      static const int kOrder[] = {5, 0, 6, 2, 21, 14, 15, 3};
       int best = -1;
       int64_t best_tiles = 0;
       for (int c : kOrder) {
