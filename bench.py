@@ -9,10 +9,12 @@ layer 2048^3 (c5), 1024^3 (c2) and the 256^3 matmul (c1).
 
 A step is one call of the dense layer on device-resident inputs (the
 C-ABI launch entry point, enqueued on torch's current stream). W warmup
-steps, then K timed steps between two device synchronisations. Two HIP
-events on the same stream bracket the K steps; their device time / K is the
-average launch duration used for the roofline. A second pass with one event
-pair per launch reports the spread.
+steps, then K timed steps between two device synchronisations (the wall
+clock gives `value`). A second pass enqueues K more steps behind a short
+spin kernel, so the GPU never waits on the host, between two HIP events on
+the same stream: their device time / K is the average launch duration used
+for the roofline. A third pass with one event pair per launch reports the
+spread.
 The CPU baseline times the oracle (a C restatement of the reference CPU-JIT
 schedule) on a row sample of the same workload, on this host's cores.
 
@@ -46,6 +48,25 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+_SLEEP_RATE = None
+
+
+def sleep_cycles_per_s() -> float:
+    """Rate of torch.cuda._sleep's cycle argument on this device (measured once)."""
+    global _SLEEP_RATE
+    if _SLEEP_RATE is None:
+        import torch
+        n = 1_000_000
+        torch.cuda._sleep(n)  # first call compiles / warms up
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        torch.cuda._sleep(n)
+        b.record()
+        torch.cuda.synchronize()
+        _SLEEP_RATE = n / max(a.elapsed_time(b) * 1e-3, 1e-6)
+    return _SLEEP_RATE
+
+
 def measure(wname: str, steps: int, warmup: int, rotate: int = 1) -> dict:
     import torch
 
@@ -70,20 +91,34 @@ def measure(wname: str, steps: int, warmup: int, rotate: int = 1) -> dict:
         launch(i)
     torch.cuda.synchronize()
     plan = _native.last_plan()
-    # Timed region: K steps back to back between one pair of events. Its
-    # device time / K is the average launch duration (the two events' own
-    # latency, ~4 us on this stack, is spread over K steps instead of being
-    # added to every step).
+    # Timed region (the contract's): K steps between two synchronisations;
+    # the wall clock gives `value`. Two events on the stream record its device
+    # span as well (reported as region_ms_per_step).
     region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     region[0].record()
     for i in range(steps):
         launch(i)
+    t_enq = time.perf_counter()
     region[1].record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    device_ms = region[0].elapsed_time(region[1]) / steps
+    wall_region_ms = region[0].elapsed_time(region[1]) / steps
+    # Device time per launch with the GPU never waiting on the host: a short
+    # spin kernel holds the stream while the K launches are enqueued behind
+    # it, and the events bracket only the K launches. (When the host issues
+    # slower than the GPU runs -- small shapes -- the timed region above is
+    # host-bound.)
+    enqueue_s = t_enq - t0  # host time to enqueue the K launches
+    torch.cuda._sleep(int(sleep_cycles_per_s() * (enqueue_s * 1.5 + 2e-4)))
+    backlog = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    backlog[0].record()
+    for i in range(steps):
+        launch(i)
+    backlog[1].record()
+    torch.cuda.synchronize()
+    device_ms = backlog[0].elapsed_time(backlog[1]) / steps
     # Spread: one event pair around each launch (each pair carries the event
     # latency, so these read high for short launches).
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
@@ -98,6 +133,7 @@ def measure(wname: str, steps: int, warmup: int, rotate: int = 1) -> dict:
         "workload": wname,
         "ms_per_step": (t1 - t0) * 1e3 / steps,
         "kernel_ms_mean": device_ms,
+        "region_ms_per_step": wall_region_ms,
         "event_pair_ms_median": statistics.median(kms),
         "event_pair_ms_min": min(kms),
         "plan": plan,
