@@ -15,8 +15,8 @@
 //
 // The device side uses row pitch `dld` (elements), the host side `hld`; chunks
 // are whole rows, so padded and strided layouts go through the same path.
-// Copies smaller than kMinStaged bytes, or with rows longer than a slot, use
-// the plain async copy. Callers hold the runtime's global lock, so the ring and
+// Copies smaller than kMinStaged bytes, with rows longer than a slot, or on a
+// host where pinned memory cannot be allocated use the plain async copy. Callers hold the runtime's global lock, so the ring and
 // the pool serve one copy at a time.
 #include "host_stage.hpp"
 
@@ -29,6 +29,8 @@
 #include <mutex>
 #include <thread>
 #include <vector>
+
+#include <unistd.h>
 
 #include "runtime_internal.hpp"
 
@@ -54,8 +56,10 @@ class CopyPool {
 
   void run(const std::function<void(int, int)>& fn) {
     const int n = parts();
-    if (n == 1) {
-      fn(0, 1);
+    if (n == 1 || getpid() != owner_) {
+      // No workers (or a forked child, which has none of the parent's
+      // threads): every part on the calling thread.
+      for (int p = 0; p < n; ++p) fn(p, n);
       return;
     }
     {
@@ -72,6 +76,11 @@ class CopyPool {
   }
 
   ~CopyPool() {
+    if (getpid() != owner_) {
+      // A forked child: the worker threads are the parent's.
+      for (auto& t : threads_) t.detach();
+      return;
+    }
     {
       std::lock_guard<std::mutex> lk(mu_);
       stop_ = true;
@@ -87,7 +96,7 @@ class CopyPool {
     return (int)std::min(8u, std::max(2u, hw / 2)) - 1;
   }
 
-  explicit CopyPool(int workers) {
+  explicit CopyPool(int workers) : owner_(getpid()) {
     for (int i = 0; i < workers; ++i) threads_.emplace_back([this, i] { loop(i); });
   }
 
@@ -108,6 +117,7 @@ class CopyPool {
     }
   }
 
+  const pid_t owner_;
   std::mutex mu_;
   std::condition_variable go_, done_;
   const std::function<void(int, int)>* fn_ = nullptr;
@@ -124,23 +134,34 @@ struct Ring {
   hipEvent_t ev[kSlots] = {};
   bool busy[kSlots] = {};
   bool ready = false;
+  bool unavailable = false;  // pinned memory could not be allocated: direct copies
 };
 Ring g_ring[kMaxStageDevices];
 
-Ring& ring_for_current_device() {
+// The current device's ring, or nullptr when pinned memory is unavailable.
+Ring* ring_for_current_device() {
   int dev = 0;
   check_hip(hipGetDevice(&dev), "hipGetDevice");
   if (dev < 0 || dev >= kMaxStageDevices) fail(kErrLimit, "device index %d out of range", dev);
   Ring& r = g_ring[dev];
-  if (!r.ready) {
-    for (int i = 0; i < kSlots; ++i) {
-      check_hip(hipHostMalloc(reinterpret_cast<void**>(&r.slot[i]), kSlotBytes, hipHostMallocDefault),
-                "hipHostMalloc");
+  if (!r.ready && !r.unavailable) {
+    for (int i = 0; i < kSlots && !r.unavailable; ++i) {
+      if (hipHostMalloc(reinterpret_cast<void**>(&r.slot[i]), kSlotBytes, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();  // not an error of the call: fall back to direct copies
+        for (int j = 0; j < i; ++j) {  // nothing has used these yet
+          (void)hipHostFree(r.slot[j]);
+          (void)hipEventDestroy(r.ev[j]);
+          r.slot[j] = nullptr;
+        }
+        r.slot[i] = nullptr;
+        r.unavailable = true;
+        break;
+      }
       check_hip(hipEventCreateWithFlags(&r.ev[i], hipEventDisableTiming), "hipEventCreate");
     }
-    r.ready = true;
+    r.ready = !r.unavailable;
   }
-  return r;
+  return r.ready ? &r : nullptr;
 }
 
 // Copies `rows` rows of `row_bytes` bytes from src (pitch src_pitch) to dst
@@ -174,7 +195,8 @@ bool direct(int64_t rows, int64_t dld, size_t es) {
 void stage_h2d(void* dev, int64_t dld, const void* host, int64_t hld, int64_t rows, int64_t cols, size_t es,
                hipStream_t stream) {
   if (rows <= 0 || cols <= 0) return;
-  if (direct(rows, dld, es)) {
+  Ring* rp = direct(rows, dld, es) ? nullptr : ring_for_current_device();
+  if (!rp) {
     if (hld == cols && dld == cols)
       check_hip(hipMemcpyAsync(dev, host, (size_t)rows * cols * es, hipMemcpyHostToDevice, stream),
                 "hipMemcpyAsync H2D");
@@ -183,7 +205,7 @@ void stage_h2d(void* dev, int64_t dld, const void* host, int64_t hld, int64_t ro
                 "hipMemcpy2DAsync H2D");
     return;
   }
-  Ring& r = ring_for_current_device();
+  Ring& r = *rp;
   const size_t dpitch = (size_t)dld * es, hpitch = (size_t)hld * es, row_bytes = (size_t)cols * es;
   const int64_t chunk_rows = std::max<int64_t>(1, (int64_t)(kSlotBytes / dpitch));
   int s = 0;
@@ -204,7 +226,8 @@ void stage_h2d(void* dev, int64_t dld, const void* host, int64_t hld, int64_t ro
 void stage_d2h(void* host, int64_t hld, const void* dev, int64_t dld, int64_t rows, int64_t cols, size_t es,
                hipStream_t stream) {
   if (rows <= 0 || cols <= 0) return;
-  if (direct(rows, dld, es)) {
+  Ring* rp = direct(rows, dld, es) ? nullptr : ring_for_current_device();
+  if (!rp) {
     if (hld == cols && dld == cols)
       check_hip(hipMemcpyAsync(host, dev, (size_t)rows * cols * es, hipMemcpyDeviceToHost, stream),
                 "hipMemcpyAsync D2H");
@@ -213,7 +236,7 @@ void stage_d2h(void* host, int64_t hld, const void* dev, int64_t dld, int64_t ro
                 "hipMemcpy2DAsync D2H");
     return;
   }
-  Ring& r = ring_for_current_device();
+  Ring& r = *rp;
   const size_t dpitch = (size_t)dld * es, hpitch = (size_t)hld * es, row_bytes = (size_t)cols * es;
   const int64_t chunk_rows = std::max<int64_t>(1, (int64_t)(kSlotBytes / dpitch));
   const int64_t chunks = (rows + chunk_rows - 1) / chunk_rows;
