@@ -262,6 +262,28 @@ def test_int8_depth_fallback_and_strided_sources(K, torch_cuda):
         set_i8_variant(-1)
 
 
+@pytest.mark.parametrize("K, path", [(2**17 - 128, "narrow_i8+gemm_i8"), (2**17, "gemm_i32_valu")])
+def test_int8_exactness_boundary(K, path, torch_cuda):
+    """Every product is (-128)(-128) = 16384, so every output is 16384*K,
+    exact in i32 up to K = 2^17 - 128 (the int8 path runs) and 2^31 at
+    K = 2^17, which wraps to -2^31 (arith.addi semantics; the exact i32 path
+    runs, as it does for every K >= 2^17). ReLU of the wrapped value is 0."""
+    import torch
+    from mlir_edsl_hip.device import dense_launch
+    M = N = 128
+    X = torch.full((M, K), -128, dtype=torch.int32, device="cuda")
+    W = torch.full((K, N), -128, dtype=torch.int32, device="cuda")
+    exp = (16384 * K + 2**31) % 2**32 - 2**31
+    for epi, want in ((_native.EPI_NONE, exp), (_native.EPI_RELU, max(exp, 0))):
+        Y = torch.full((M, N), 7, dtype=torch.int32, device="cuda")
+        dense_launch(X, W, None, Y, epi)
+        torch.cuda.synchronize()
+        plan = _native.last_plan()
+        assert plan.startswith(path), plan
+        got = Y.cpu().numpy()
+        assert (got == want).all(), (plan, int(got.min()), int(got.max()), want)
+
+
 @pytest.mark.parametrize("shape", [(1, 1, 1), (3, 5, 7), (65, 33, 17), (130, 128, 128), (128, 256, 384)])
 def test_int_shapes(shape, torch_cuda):
     M, K, N = shape
