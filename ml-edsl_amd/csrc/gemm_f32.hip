@@ -26,6 +26,8 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <type_traits>
+
 namespace edsl {
 namespace {
 
@@ -52,7 +54,10 @@ __device__ __forceinline__ void load_b_frag(const float* p, float (&v)[CP]) {
   }
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int WAVES_K, int EPI, bool GUARD>
+template <int N>
+using Ic = std::integral_constant<int, N>;
+
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int WAVES_K, int PF, int EPI, bool GUARD>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64)
 gemm_f32_kernel(GemmF32Args args) {
   constexpr int NT = WAVES_M * WAVES_N * WAVES_K * 64;
@@ -88,10 +93,13 @@ gemm_f32_kernel(GemmF32Args args) {
   const int n0 = tn * BN;
   const int M = args.M, N = args.N, K = args.K;
 
-  f32x4 ra[A_LD];
-  f32x4 rb[B_LD];
+  static_assert(PF == 1 || PF == 2, "global prefetch depth");
+  f32x4 ra[PF][A_LD];
+  f32x4 rb[PF][B_LD];
 
-  auto load_global = [&](int k0) {
+  // Register set S receives the global tile loads of one K step.
+  auto load_global = [&](auto set, int k0) {
+    constexpr int S = decltype(set)::value;
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
       const int idx = tid + i * NT;
@@ -100,13 +108,13 @@ gemm_f32_kernel(GemmF32Args args) {
       const int gm = m0 + r;
       const int gk = k0 + 4 * q;
       if constexpr (!GUARD) {
-        ra[i] = *reinterpret_cast<const f32x4*>(args.A + (int64_t)gm * args.lda + gk);
+        ra[S][i] = *reinterpret_cast<const f32x4*>(args.A + (int64_t)gm * args.lda + gk);
       } else {
         f32x4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           v[e] = (gm < M && gk + e < K) ? args.A[(int64_t)gm * args.lda + gk + e] : 0.0f;
-        ra[i] = v;
+        ra[S][i] = v;
       }
     }
 #pragma unroll
@@ -117,31 +125,32 @@ gemm_f32_kernel(GemmF32Args args) {
       const int gk = k0 + r;
       const int gn = n0 + c;
       if constexpr (!GUARD) {
-        rb[i] = *reinterpret_cast<const f32x4*>(args.B + (int64_t)gk * args.ldb + gn);
+        rb[S][i] = *reinterpret_cast<const f32x4*>(args.B + (int64_t)gk * args.ldb + gn);
       } else {
         f32x4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           v[e] = (gk < K && gn + e < N) ? args.B[(int64_t)gk * args.ldb + gn + e] : 0.0f;
-        rb[i] = v;
+        rb[S][i] = v;
       }
     }
   };
 
-  auto store_lds = [&](int buf) {
+  auto store_lds = [&](auto set, int buf) {
+    constexpr int S = decltype(set)::value;
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
       const int idx = tid + i * NT;
       const int r = idx / KCH;
       const int q = idx % KCH;
-      sA[buf][r * KCH + (q ^ a_swizzle<KCH>(r))] = ra[i];
+      sA[buf][r * KCH + (q ^ a_swizzle<KCH>(r))] = ra[S][i];
     }
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
       const int idx = tid + i * NT;
       const int r = idx / (BN / 4);
       const int c = 4 * (idx % (BN / 4));
-      *reinterpret_cast<f32x4*>(&sB[buf][r * BN + c]) = rb[i];
+      *reinterpret_cast<f32x4*>(&sB[buf][r * BN + c]) = rb[S][i];
     }
   };
 
@@ -182,18 +191,47 @@ gemm_f32_kernel(GemmF32Args args) {
   };
 
   const int nk = (K + BK - 1) / BK;
-  if (nk > 0) {
-    load_global(0);
-    store_lds(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const int buf = kt & 1;
-      const bool more = kt + 1 < nk;
-      if (more) load_global((kt + 1) * BK);
-      compute(buf);
-      if (more) store_lds(buf ^ 1);
+  if constexpr (PF == 1) {
+    if (nk > 0) {
+      load_global(Ic<0>{}, 0);
+      store_lds(Ic<0>{}, 0);
       __syncthreads();
+      for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) load_global(Ic<0>{}, (kt + 1) * BK);
+        compute(buf);
+        if (more) store_lds(Ic<0>{}, buf ^ 1);
+        __syncthreads();
+      }
     }
+  } else if (nk > 0) {
+    // Two K steps of global loads in flight: while step kt is computed from
+    // LDS buffer kt&1, step kt+1 (register set (kt+1)&1, loaded one iteration
+    // earlier) goes to the other LDS buffer and step kt+2 is loaded into set
+    // kt&1. Past the last step the loads repeat the last step (in bounds,
+    // never used), so the body has no branch and its wait counts stay exact.
+    load_global(Ic<0>{}, 0);
+    load_global(Ic<1>{}, (nk > 1 ? 1 : 0) * BK);
+    store_lds(Ic<0>{}, 0);
+    __syncthreads();
+    auto step = [&](auto cur, int kt) {
+      constexpr int C = decltype(cur)::value;
+      load_global(Ic<C>{}, min(kt + 2, nk - 1) * BK);
+      // Keep the loads ahead of this step's MFMAs (the scheduler would
+      // otherwise sink them and shorten their lead to one step).
+      __builtin_amdgcn_sched_barrier(0);
+      compute(kt & 1);
+      __builtin_amdgcn_sched_barrier(0);
+      store_lds(Ic<1 - C>{}, (kt + 1) & 1);
+      __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+      step(Ic<0>{}, kt);
+      step(Ic<1>{}, kt + 1);
+    }
+    if (kt < nk) step(Ic<0>{}, kt);
   }
 
   // Waves that split K add their partial tiles into wave group 0 through
@@ -295,6 +333,8 @@ gemm_f32_kernel(GemmF32Args args) {
 //         128x128x32 (k2)
 //  19-21: 64x64x128 (k2, k4) and 64x64x64 (k4): deeper K steps / more waves
 //         per CU for latency-bound mid-size shapes
+//  22: 64x64x64 (k2) with global loads two K steps ahead (_pf2); the same
+//      lead measured slower for the k4 and 256x256 tiles
 const GemmF32Config kConfigs[] = {
     {256, 256, 16, 2, 2, false, "f32_256x256x16_w2x2"},
     {256, 256, 16, 4, 2, false, "f32_256x256x16_w4x2"},
@@ -318,16 +358,17 @@ const GemmF32Config kConfigs[] = {
     {64, 64, 128, 2, 2, false, "f32_64x64x128_w2x2_k2"},
     {64, 64, 128, 2, 2, false, "f32_64x64x128_w2x2_k4"},
     {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2_k4"},
+    {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2_k2_pf2"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
-template <int BM, int BN, int BK, int WMW, int WNW, int WKW, bool GUARD>
+template <int BM, int BN, int BK, int WMW, int WNW, int WKW, bool GUARD, int PF = 1>
 hipError_t launch_cfg(int epi, const GemmF32Args& a, hipStream_t stream) {
   const dim3 grid(a.tiles_m * a.tiles_n);
   const dim3 block(WMW * WNW * WKW * 64);
 #define EDSL_F32_CASE(E)                                                                           \
   case E:                                                                                          \
-    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WMW, WNW, WKW, E, GUARD>), grid, block, 0, \
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WMW, WNW, WKW, PF, E, GUARD>), grid, block, 0, \
                        stream, a);                                                                 \
     break;
   switch (epi) {
@@ -373,6 +414,7 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case 19: return launch_cfg<64, 64, 128, 2, 2, 2, false>(epi, a, stream);
     case 20: return launch_cfg<64, 64, 128, 2, 2, 4, false>(epi, a, stream);
     case 21: return launch_cfg<64, 64, 64, 2, 2, 4, false>(epi, a, stream);
+    case 22: return launch_cfg<64, 64, 64, 2, 2, 2, false, 2>(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }
