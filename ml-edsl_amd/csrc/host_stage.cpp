@@ -243,8 +243,9 @@ void stage_d2h(void* host, int64_t hld, const void* dev, int64_t dld, int64_t ro
   auto issue = [&](int64_t c) {
     const int s = (int)(c % kSlots);
     const int64_t r0 = c * chunk_rows, n = std::min(chunk_rows, rows - r0);
-    // A slot's previous contents were copied out synchronously before it is
-    // reissued, so only the device-side order matters here.
+    // A slot still being read by an upload (possibly on another stream) is
+    // overwritten only after that DMA; one this call already copied out is free.
+    if (r.busy[s]) check_hip(hipStreamWaitEvent(stream, r.ev[s], 0), "hipStreamWaitEvent");
     check_hip(hipMemcpyAsync(r.slot[s], static_cast<const char*>(dev) + r0 * dpitch, (size_t)n * dpitch,
                              hipMemcpyDeviceToHost, stream),
               "hipMemcpyAsync D2H");

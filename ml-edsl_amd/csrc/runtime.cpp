@@ -97,6 +97,8 @@ struct DevBuf {
   }
 };
 
+constexpr int kPipeBlocks = 4;  // row blocks of a pipelined host-buffer layer
+
 struct DeviceState {
   bool ready = false;
   int cus = 256;
@@ -105,6 +107,11 @@ struct DeviceState {
   DevBuf gemv_partials;
   DevBuf i8_x, i8_w, i8_flag;
   unsigned epoch = 0;
+  // Pipelined host-buffer layers: uploads, kernels and downloads on three
+  // non-blocking streams (default priority), ordered by events.
+  bool pipe_ready = false;
+  hipStream_t pipe_up = nullptr, pipe_run = nullptr, pipe_down = nullptr;
+  hipEvent_t ev_w = nullptr, ev_x[kPipeBlocks] = {}, ev_g[kPipeBlocks] = {};
 };
 
 constexpr int kMaxDevices = 64;
@@ -114,6 +121,7 @@ int g_force_cfg = -1;
 int g_force_ksplit = 0;
 int g_force_cols = 0;
 int g_force_i8 = -1;
+bool g_no_pipeline = false;  // EDSL_HIP_HOST_PIPELINE=0: plain staged sequence for host buffers
 
 void read_env_overrides() {
   static bool done = false;
@@ -123,6 +131,7 @@ void read_env_overrides() {
   if (const char* s = getenv("EDSL_HIP_GEMV_KSPLIT")) g_force_ksplit = atoi(s);
   if (const char* s = getenv("EDSL_HIP_GEMV_COLS")) g_force_cols = atoi(s);
   if (const char* s = getenv("EDSL_HIP_I8_VARIANT")) g_force_i8 = atoi(s);
+  if (const char* s = getenv("EDSL_HIP_HOST_PIPELINE")) g_no_pipeline = atoi(s) == 0;
 }
 
 DeviceState& device_state(int* dev_out) {
@@ -413,6 +422,102 @@ void copy_d2h(const Mat& m, const void* d, int64_t dld, size_t es, hipStream_t s
   stage_d2h(m.base, m.ld, d, dld, m.rows, m.cols, es, stream);
 }
 
+// One f32 layer with host X and Y, large enough to overlap PCIe copies with
+// the kernels: W (and b) go up first; then X is uploaded in kPipeBlocks row
+// blocks on one stream, each block's kernel runs on a second stream as soon
+// as its rows have landed, and its Y rows come down on a third while the next
+// block computes. Returns false when the call does not qualify (the caller
+// then runs the plain staged sequence).
+constexpr int64_t kPipeMinRows = 1024;
+constexpr int64_t kPipeRowAlign = 256;
+
+bool pipelined_host_layer(DeviceState& ds, int dev, int dtype, const LayerOp& op, const Mat& Y) {
+  const Mat& X = *op.X;
+  const Mat& W = *op.W;
+  const int64_t M = X.rows, K = X.cols, N = W.cols;
+  if (dtype != EDSL_DTYPE_F32 || M < kPipeMinRows || K == 0 || N == 0) return false;
+  if (is_device_pointer(X.base, dev) || is_device_pointer(Y.base, dev)) return false;
+  const size_t es = 4;
+  if ((size_t)M * (size_t)(K + N) * es < (size_t)(16u << 20)) return false;
+  if (!ds.pipe_ready) {
+    check_hip(hipStreamCreateWithFlags(&ds.pipe_up, hipStreamNonBlocking), "hipStreamCreate");
+    check_hip(hipStreamCreateWithFlags(&ds.pipe_run, hipStreamNonBlocking), "hipStreamCreate");
+    check_hip(hipStreamCreateWithFlags(&ds.pipe_down, hipStreamNonBlocking), "hipStreamCreate");
+    check_hip(hipEventCreateWithFlags(&ds.ev_w, hipEventDisableTiming), "hipEventCreate");
+    for (int i = 0; i < kPipeBlocks; ++i) {
+      check_hip(hipEventCreateWithFlags(&ds.ev_x[i], hipEventDisableTiming), "hipEventCreate");
+      check_hip(hipEventCreateWithFlags(&ds.ev_g[i], hipEventDisableTiming), "hipEventCreate");
+    }
+    ds.pipe_ready = true;
+  }
+  // Every host-buffer call is synchronous, so no earlier work on these or the
+  // legacy stream can still touch the staging buffers.
+  const int64_t dldx = (K + 3) & ~int64_t(3), dldy = (N + 3) & ~int64_t(3);
+  char* dx = static_cast<char*>(ds.stage[0].ensure((size_t)M * dldx * es, false));
+  char* dy = static_cast<char*>(ds.stage[3].ensure((size_t)M * dldy * es, false));
+  DenseLaunch L{};
+  L.dtype = dtype;
+  L.epi = op.epi;
+  L.alpha = op.alpha;
+  L.K = K;
+  L.N = N;
+  if (is_device_pointer(W.base, dev)) {
+    L.w = W.base;
+    L.ldw = W.ld;
+  } else {
+    const int64_t dldw = (N + 3) & ~int64_t(3);
+    void* dw = ds.stage[1].ensure((size_t)K * dldw * es, false);
+    stage_h2d(dw, dldw, W.base, W.ld, K, N, es, ds.pipe_up);
+    L.w = dw;
+    L.ldw = dldw;
+  }
+  if (epi_has_bias(op.epi)) {
+    if (is_device_pointer(op.b->base, dev)) {
+      L.bias = op.b->base;
+    } else {
+      void* d = ds.stage[2].ensure((size_t)N * es, false);
+      check_hip(hipMemcpyAsync(d, op.b->base, (size_t)N * es, hipMemcpyHostToDevice, ds.pipe_up),
+                "hipMemcpyAsync H2D");
+      L.bias = d;
+    }
+  }
+  check_hip(hipEventRecord(ds.ev_w, ds.pipe_up), "hipEventRecord");
+  check_hip(hipStreamWaitEvent(ds.pipe_run, ds.ev_w, 0), "hipStreamWaitEvent");
+
+  const int64_t mb = ((M + kPipeBlocks - 1) / kPipeBlocks + kPipeRowAlign - 1) / kPipeRowAlign * kPipeRowAlign;
+  const int nb = (int)((M + mb - 1) / mb);
+  std::string plan0;
+  auto download = [&](int i) {
+    const int64_t r0 = i * mb, rows = std::min(mb, M - r0);
+    check_hip(hipStreamWaitEvent(ds.pipe_down, ds.ev_g[i], 0), "hipStreamWaitEvent");
+    stage_d2h(Y.base + r0 * Y.ld * (int64_t)es, Y.ld, dy + r0 * dldy * (int64_t)es, dldy, rows, N, es,
+              ds.pipe_down);
+  };
+  for (int i = 0; i < nb; ++i) {
+    const int64_t r0 = i * mb, rows = std::min(mb, M - r0);
+    stage_h2d(dx + r0 * dldx * (int64_t)es, dldx, X.base + r0 * X.ld * (int64_t)es, X.ld, rows, K, es,
+              ds.pipe_up);
+    check_hip(hipEventRecord(ds.ev_x[i], ds.pipe_up), "hipEventRecord");
+    check_hip(hipStreamWaitEvent(ds.pipe_run, ds.ev_x[i], 0), "hipStreamWaitEvent");
+    L.M = rows;
+    L.x = dx + r0 * dldx * (int64_t)es;
+    L.ldx = dldx;
+    L.y = dy + r0 * dldy * (int64_t)es;
+    L.ldy = dldy;
+    launch_dense(ds, L, ds.pipe_run);
+    if (i == 0) plan0 = t_plan;
+    check_hip(hipEventRecord(ds.ev_g[i], ds.pipe_run), "hipEventRecord");
+    if (i > 0) download(i - 1);  // overlaps block i's kernel
+  }
+  download(nb - 1);
+  check_hip(hipStreamSynchronize(ds.pipe_up), "hipStreamSynchronize");
+  check_hip(hipStreamSynchronize(ds.pipe_run), "hipStreamSynchronize");
+  check_hip(hipStreamSynchronize(ds.pipe_down), "hipStreamSynchronize");
+  check_hip(hipGetLastError(), "kernel execution");
+  set_plan("host pipeline %d x %lld rows: %s", nb, (long long)mb, plan0.c_str());
+  return true;
+}
+
 void sync_dense_chain(int dtype, const LayerOp* layers, int n, const Mat& Y) {
   if (n < 1 || !layers || !layers[0].X) fail(kErrArgument, "a chain needs at least one layer and an input");
   const int64_t M = layers[0].X->rows;
@@ -442,6 +547,19 @@ void sync_dense_chain(int dtype, const LayerOp* layers, int n, const Mat& Y) {
   read_env_overrides();
   int dev = 0;
   DeviceState& ds = device_state(&dev);
+  if (n == 1 && !g_no_pipeline) {
+    bool done = false;
+    try {
+      done = pipelined_host_layer(ds, dev, dtype, layers[0], Y);
+    } catch (...) {
+      // Drain the pipeline's streams before anything else touches the
+      // staging buffers (the legacy stream does not order against them).
+      if (ds.pipe_ready)
+        for (hipStream_t st : {ds.pipe_up, ds.pipe_run, ds.pipe_down}) (void)hipStreamSynchronize(st);
+      throw;
+    }
+    if (done) return;
+  }
   hipStream_t stream = nullptr;
   const size_t es = 4;
 

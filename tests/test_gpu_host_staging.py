@@ -2,8 +2,11 @@
 ring (2 MiB and up): several chunks wrapping the 4-slot ring in both
 directions, padded device rows (column counts not a multiple of 4), and host
 operands that are strided views with an element offset, passed straight
-through the memref ABI (the reference's JIT calling convention). Results are
-checked against the oracle: i32 bit-exact, f32 to the usual bar."""
+through the memref ABI (the reference's JIT calling convention). The large
+f32 cases take the pipelined path (row blocks uploaded, computed and
+downloaded on three streams), the i32 and small ones the plain sequence.
+Results are checked against the oracle: i32 bit-exact, f32 to the usual
+bar."""
 from __future__ import annotations
 
 import ctypes
@@ -89,7 +92,12 @@ def test_host_staging(dt, M, K, N, xpo, wpo, ypo, lib):
     _slice(outside, M, N, *ypo)[...] = False
     Yb_before = Yb.copy()
     _call_dense_relu(lib, dtype, Xb, X, Wb, W, b, Yb, Y)
-    what = f"{dt} M={M} K={K} N={N} X pad/off={xpo} W={wpo} Y={ypo} [{_native.last_plan()}]"
+    plan = _native.last_plan()
+    what = f"{dt} M={M} K={K} N={N} X pad/off={xpo} W={wpo} Y={ypo} [{plan}]"
+    # f32 layers with M >= 1024 rows and >= 16 MiB of X and Y overlap their
+    # copies with the kernels (row blocks on three streams)
+    pipelined = dt == "f32" and M >= 1024 and M * (K + N) * 4 >= 16 << 20
+    assert plan.startswith("host pipeline") == pipelined, what
     if dt == "i32":
         ref = oracle.dense_i32(np.ascontiguousarray(X), np.ascontiguousarray(W), b, "relu")
         assert np.array_equal(Y, ref), what
