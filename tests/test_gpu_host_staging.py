@@ -106,3 +106,29 @@ def test_host_staging(dt, M, K, N, xpo, wpo, ypo, lib):
         assert_f32_parity(np.ascontiguousarray(Y), ref, K)
     # nothing outside the output view was written
     assert np.array_equal(Yb[outside], Yb_before[outside]), what
+
+
+def test_pipeline_with_device_weights(lib):
+    """Host X and Y with W and b already on the device (zero-copy): the
+    pipeline uploads only X's row blocks."""
+    import torch
+    rng = np.random.default_rng(7)
+    M, K, N = 3000, 1024, 1536
+    Xb, X = _view(rng, M, K, 0, 0, np.float32)
+    W = rng.standard_normal((K, N), dtype=np.float32) / np.float32(np.sqrt(K))
+    b = rng.standard_normal(N, dtype=np.float32)
+    tW, tb = torch.from_numpy(W).cuda(), torch.from_numpy(b).cuda()
+    Yb, Y = _view(rng, M, N, 0, 0, np.float32)
+    Y[...] = np.nan
+    args = (_desc2(Xb, X) + [tW.data_ptr(), tW.data_ptr(), 0, K, N, N, 1] +
+            [tb.data_ptr(), tb.data_ptr(), 0, N, 1] + _desc2(Yb, Y))
+    fn = ctypes.CFUNCTYPE(None, *([ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 5) * 2 +
+                          [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64] +
+                          [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 5)(
+        ctypes.cast(lib.edsl_hip_dense_relu_f32, ctypes.c_void_p).value)
+    lib.edsl_hip_clear_error()
+    fn(*args)
+    _native.raise_on_error("edsl_hip_dense_relu_f32")
+    plan = _native.last_plan()
+    assert plan.startswith("host pipeline"), plan
+    assert_f32_parity(Y, oracle.dense_f32(X, W, b, "relu"), K)
