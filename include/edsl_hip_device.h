@@ -14,8 +14,11 @@
  * and the call returns without waiting. Returns 0 on success, otherwise an
  * error code with the message in edsl_hip_last_error(). Library-owned
  * workspaces (small-M split-K partials, int8 operand copies) are shared by all
- * calls on a device: launches that overlap in time on different streams of
- * one device must not be issued.
+ * calls on a device. While one stream uses them nothing is added; the first
+ * call from a second stream waits for the device once (hipDeviceSynchronize,
+ * so it must not be issued during stream capture), and from then on calls
+ * that use a workspace record an event that the next such call from another
+ * stream waits for: those calls run one after another on the device.
  */
 #ifndef EDSL_HIP_DEVICE_H
 #define EDSL_HIP_DEVICE_H

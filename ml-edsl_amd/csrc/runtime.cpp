@@ -107,6 +107,12 @@ struct DeviceState {
   DevBuf gemv_partials;
   DevBuf i8_x, i8_w, i8_flag;
   unsigned epoch = 0;
+  // Ordering of the launches that use the library scratch above (split-K
+  // partials, packed int8 operands and flag) across streams.
+  hipStream_t ws_stream = nullptr;  // stream of the last such launch
+  bool ws_seen = false;             // any such launch yet
+  bool ws_multi = false;            // a second stream has used the scratch: ws_ev orders every use
+  hipEvent_t ws_ev = nullptr;
   // Pipelined host-buffer layers: uploads, kernels and downloads on three
   // non-blocking streams (default priority), ordered by events.
   bool pipe_ready = false;
@@ -147,6 +153,31 @@ DeviceState& device_state(int* dev_out) {
   }
   if (dev_out) *dev_out = dev;
   return s;
+}
+
+// ------------------------------------------------ scratch stream ordering
+// Launches on one stream run in order, so while a single stream uses the
+// library scratch nothing is added. The first launch from a second stream
+// waits for the whole device once (the earlier stream may since have been
+// destroyed, so no event can be recorded on it after the fact); from then on
+// every scratch launch records ws_ev after its kernels, and a launch from a
+// stream other than the last one waits for that event first. Overlapping
+// calls on different streams are thereby serialised on the device.
+void scratch_begin(DeviceState& ds, hipStream_t stream) {
+  if (!ds.ws_multi) {
+    if (!ds.ws_seen || stream == ds.ws_stream) return;
+    check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    if (!ds.ws_ev) check_hip(hipEventCreateWithFlags(&ds.ws_ev, hipEventDisableTiming), "hipEventCreate");
+    ds.ws_multi = true;
+    return;
+  }
+  if (stream != ds.ws_stream) check_hip(hipStreamWaitEvent(stream, ds.ws_ev, 0), "hipStreamWaitEvent");
+}
+
+void scratch_end(DeviceState& ds, hipStream_t stream) {
+  ds.ws_seen = true;
+  ds.ws_stream = stream;
+  if (ds.ws_multi) check_hip(hipEventRecord(ds.ws_ev, stream), "hipEventRecord");
 }
 
 // ---------------------------------------------------------- operand views
@@ -285,10 +316,13 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     a.alpha = L.alpha;
     a.ksplit = gemv_ks;
     const int mb = (M + 15) / 16;
-    if (a.ksplit > 1)
+    if (a.ksplit > 1) {
       a.partials = static_cast<float*>(
           ds.gemv_partials.ensure((size_t)a.ksplit * 16 * mb * N * sizeof(float), false));
+      scratch_begin(ds, stream);
+    }
     check_hip(launch_gemv_f32(L.epi, gemv_cols, a, stream), "gemv_f32 launch");
+    if (a.ksplit > 1) scratch_end(ds, stream);
     set_plan("gemv_f32 mb=%d ksplit=%d cols=%d grid=%d%s", mb, a.ksplit, gemv_cols,
              (N / gemv_cols) * a.ksplit, a.ksplit > 1 ? " +reduce" : "");
     return;
@@ -380,6 +414,7 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     n.K = a.K;
     n.flag = flag;
     n.epoch = ds.epoch;
+    scratch_begin(ds, stream);
     check_hip(launch_narrow_i8(n, stream), "narrow_i8 launch");
     a.A8p = x8;
     a.B8p = w8;
@@ -387,6 +422,7 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     a.epoch = ds.epoch;
     const int variant = (g_force_i8 >= 0 && g_force_i8 < kI8Variants) ? g_force_i8 : kI8DefaultVariant;
     check_hip(launch_gemm_i8(L.epi, a, stream, variant), "gemm_i8 launch");
+    scratch_end(ds, stream);
     set_plan("narrow_i8+gemm_i8 variant=%d depth=%d grid=%d", variant, gemm_i8_depth(variant, a.K),
              (a.M / kI8Tile) * (a.N / kI8Tile));
   } else {

@@ -1,0 +1,66 @@
+"""Device entry points called from several streams at once. The small-M
+split-K partials and the packed int8 operands are library scratch shared by
+every call on a device; calls from different streams that would overlap on
+the device must still give each caller its own result. Each launch is queued
+behind a spin kernel on its stream, so the launches of the two streams
+would start together if nothing ordered them."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_f32_parity
+from mlir_edsl_hip import _native
+from mlir_edsl_hip.device import dense_launch
+
+pytestmark = pytest.mark.gpu
+
+SPIN_CYCLES = 200_000  # ~0.1 ms
+
+
+def _problem(torch, rng, dtype, M, K, N):
+    if dtype == "f32":
+        X = rng.standard_normal((M, K), dtype=np.float32)
+        W = rng.standard_normal((K, N), dtype=np.float32)
+        b = rng.standard_normal(N, dtype=np.float32)
+        ref = oracle.dense_f32(X, W, b, "relu")
+    else:
+        X = rng.integers(-128, 128, size=(M, K), dtype=np.int32)
+        W = rng.integers(-128, 128, size=(K, N), dtype=np.int32)
+        b = rng.integers(-2**20, 2**20, size=N, dtype=np.int32)
+        ref = oracle.dense_i32(X, W, b, "relu")
+    t = [torch.from_numpy(a).cuda() for a in (X, W, b)]
+    Y = torch.full((M, N), -7, dtype=t[0].dtype, device="cuda")
+    return t, Y, ref, K
+
+
+@pytest.mark.parametrize("kinds", [("f32", "f32"), ("i32", "i32"), ("f32", "i32")])
+def test_scratch_users_on_two_streams(kinds):
+    import torch
+    assert torch.cuda.is_available()
+    rng = np.random.default_rng(11)
+    shapes = {"f32": (16, 2048, 2048), "i32": (256, 384, 256)}
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    # four rounds, each stream gets its own problem every round
+    probs = [[_problem(torch, rng, kinds[j], *shapes[kinds[j]]) for j in range(2)] for _ in range(4)]
+    torch.cuda.synchronize()
+    plans = set()
+    for rnd in probs:
+        for s, ((X, W, b), Y, _, _) in zip(streams, rnd):
+            with torch.cuda.stream(s):
+                torch.cuda._sleep(SPIN_CYCLES)
+                dense_launch(X, W, b, Y, _native.EPI_BIAS_RELU, stream=s)
+                plans.add(_native.last_plan())
+    torch.cuda.synchronize()
+    # both scratch users are exercised
+    for k in set(kinds):
+        want = "ksplit=" if k == "f32" else "narrow_i8+gemm_i8"
+        assert any(want in p and ("ksplit=1 " not in p) for p in plans), plans
+    for r, rnd in enumerate(probs):
+        for j, (_, Y, ref, K) in enumerate(rnd):
+            got = Y.cpu().numpy()
+            if got.dtype == np.int32:
+                assert np.array_equal(got, ref), f"round {r} stream {j}"
+            else:
+                assert_f32_parity(got, ref, K)
