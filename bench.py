@@ -5,7 +5,9 @@ Headline (BASELINE.json metric): fused fp32 matmul+bias+ReLU at M=N=K=4096
 (workload c3), in TFLOP/s and as a fraction of the dense fp32 MFMA peak.
 Secondary lines (same run): the M=16, K=N=8192 layer in GB/s (c4, W rotated
 over 3 buffers so the 256 MB Infinity Cache cannot serve it), the integer
-layer 2048^3 (c5), 1024^3 (c2) and the 256^3 matmul (c1).
+layer 2048^3 (c5), 1024^3 (c2), the 256^3 matmul (c1), and one GPU's share
+of c4 and c3 column-sharded over 8 GPUs (c4s8: N=1024, W rotated over 12
+buffers; c3s8: N=512).
 
 A step is one call of the dense layer on device-resident inputs (the
 C-ABI launch entry point, enqueued on torch's current stream). W warmup
@@ -41,7 +43,8 @@ PEAK = {  # MI355X published dense peaks
     "hbm_gbs": 8000.0,
 }
 KERNEL_NAMES = {"c1": "gemm_f32_kernel", "c2": "gemm_f32_kernel", "c3": "gemm_f32_kernel",
-                "c4": "gemv_f32_kernel + gemv_reduce_kernel", "c5": "narrow_i8_kernel + gemm_i8_kernel"}
+                "c4": "gemv_f32_kernel + gemv_reduce_kernel", "c5": "narrow_i8_kernel + gemm_i8_kernel",
+                "c3s8": "gemm_f32_kernel", "c4s8": "gemv_f32_kernel + gemv_reduce_kernel"}
 
 
 def log(msg: str) -> None:
@@ -177,7 +180,7 @@ def roofline_for(wname: str, r: dict, traffic: dict) -> dict:
     w = WORKLOADS[wname]
     t = r["kernel_ms_mean"] * 1e-3
     tr = traffic.get(wname, {}).get("hbm_bytes_per_launch")
-    if wname == "c4":
+    if wname in ("c4", "c4s8"):
         achieved = w.compulsory_bytes / t / 1e9
         return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK["hbm_gbs"],
                 "unit": "GB/s", "frac": round(achieved / PEAK["hbm_gbs"], 4), "traffic": tr,
@@ -258,10 +261,13 @@ def cpu_baseline(wname: str, budget_s: float) -> dict:
             "host_cpu": cpu_model()}
 
 
-UNITS = {"c1": "TFLOP/s", "c2": "TFLOP/s", "c3": "TFLOP/s", "c4": "GB/s", "c5": "TOP/s"}
-# (steps, warmup, W buffers rotated) of each workload when it is not the headline
+UNITS = {"c1": "TFLOP/s", "c2": "TFLOP/s", "c3": "TFLOP/s", "c4": "GB/s", "c5": "TOP/s",
+         "c3s8": "TFLOP/s", "c4s8": "GB/s"}
+# (steps, warmup, W buffers rotated) of each workload when it is not the headline.
+# W is rotated over enough copies to exceed the 256 MB Infinity Cache where it
+# would otherwise be served from there: c4 3 x 256 MiB, c4s8 12 x 32 MiB.
 SECONDARY_PLAN = {"c4": (200, 20, 3), "c5": (100, 20, 1), "c2": (100, 20, 1), "c1": (200, 20, 1),
-                  "c3": (50, 10, 1)}
+                  "c3": (50, 10, 1), "c3s8": (100, 10, 1), "c4s8": (300, 30, 12)}
 
 
 def step_value(wname: str, step_s: float) -> float:
@@ -281,7 +287,7 @@ def main() -> int:
     ap.add_argument("--workload", default="c3", choices=sorted(UNITS),
                     help="workload of the headline line (default c3, the BASELINE metric's config)")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--secondary", default="c4,c5,c2,c1",
+    ap.add_argument("--secondary", default="c4,c5,c2,c1,c4s8,c3s8",
                     help="comma-separated workloads measured after the headline one")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)

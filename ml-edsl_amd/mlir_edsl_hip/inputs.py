@@ -11,6 +11,8 @@ uniform[0,1) with seed 42, reference benchmarks/bench_matmul.py:97,109-111):
   c3  fp32 dense 4096^3, same distributions, seed 2
   c4  fp32 dense M=16, K=N=8192 (W is 256 MiB), seed 3
   c5  integer dense 2048^3, X and W uniform ints in [-8, 7], b in [-512, 511], seed 4
+  c3s8, c4s8  one GPU's share of c3 / c4 column-sharded over 8 GPUs (N / 8
+      columns), seeds 5 and 6, c3's distributions
 """
 from __future__ import annotations
 
@@ -55,6 +57,12 @@ WORKLOADS = {
                    "fp32 dense relu(X@W+b) M=16 K=N=8192, seed 3"),
     "c5": Workload("c5", "dense_relu", "i32", 2048, 2048, 2048, 4,
                    "int dense relu(X@W+b) 2048^3, values in [-8,7], b in [-512,511], seed 4"),
+    # One GPU's share of c3 and c4 when the layer is column-sharded 8 ways
+    # (each GPU owns N/8 columns of W, b and Y; X is replicated).
+    "c3s8": Workload("c3s8", "dense_relu", "f32", 4096, 4096, 512, 5,
+                     "fp32 dense relu(X@W+b), c3's 8-way column shard: M=K=4096, N=512, seed 5"),
+    "c4s8": Workload("c4s8", "dense_relu", "f32", 16, 8192, 1024, 6,
+                     "fp32 dense relu(X@W+b), c4's 8-way column shard: M=16, K=8192, N=1024, seed 6"),
 }
 
 

@@ -167,6 +167,44 @@ def test_c4_dense_small_m(torch_cuda):
         check(got, ref, w.K)
 
 
+def test_c4_column_shard(torch_cuda):
+    """One GPU's share of c4 column-sharded 8 ways, full output."""
+    w = WORKLOADS["c4s8"]
+    X, W, b = make_inputs(w)
+    got = gpu_run("dense_relu", [X, W, b], device=True)
+    assert _native.last_plan().startswith("gemv_f32")
+    check(got, oracle.dense_f32(X, W, b, "relu"), w.K)
+
+
+def test_c3_column_shard_sampled_rows(torch_cuda):
+    """One GPU's share of c3 column-sharded 8 ways, 256 sampled rows."""
+    w = WORKLOADS["c3s8"]
+    X, W, b = make_inputs(w)
+    got = gpu_run("dense_relu", [X, W, b], device=True)
+    assert _native.last_plan().startswith("gemm_f32")
+    rows = np.sort(np.random.default_rng(1).choice(w.M, 256, replace=False))
+    check(got[rows], oracle.dense_f32(X[rows], W, b, "relu"), w.K)
+
+
+def test_column_shards_reassemble_the_layer(torch_cuda):
+    """Column sharding needs no exchange: the 8 shards of c4, each run on a
+    strided column slice of W (row stride 8192) and of b, written into the
+    matching columns of one Y, give the layer's output."""
+    import torch
+    from mlir_edsl_hip.device import dense_launch
+    w = WORKLOADS["c4"]
+    X, W, b = make_inputs(w)
+    tX, tW, tb = to_dev(torch, [X, W, b])
+    Y = torch.full((w.M, w.N), float("nan"), device="cuda")
+    n = w.N // 8
+    for g in range(8):
+        cols = slice(g * n, (g + 1) * n)
+        dense_launch(tX, tW[:, cols], tb[cols], Y[:, cols], _native.EPI_BIAS_RELU)
+        assert _native.last_plan().startswith("gemv_f32")
+    torch.cuda.synchronize()
+    check(Y.cpu().numpy(), oracle.dense_f32(X, W, b, "relu"), w.K)
+
+
 def test_c5_int_dense_bit_exact(torch_cuda):
     w = WORKLOADS["c5"]
     X, W, b = make_inputs(w)
