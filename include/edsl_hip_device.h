@@ -19,6 +19,12 @@
  * so it must not be issued during stream capture), and from then on calls
  * that use a workspace record an event that the next such call from another
  * stream waits for: those calls run one after another on the device.
+ *
+ * The launches may be captured into a HIP graph (stream capture) once the
+ * same shapes have run eagerly, which sizes the workspaces: nothing is then
+ * allocated or synchronised during capture, and workspaces that later grow
+ * keep their old buffers, so a replay still finds the ones it was captured
+ * with. Replays are ordered only by the stream the graph is launched on.
  */
 #ifndef EDSL_HIP_DEVICE_H
 #define EDSL_HIP_DEVICE_H

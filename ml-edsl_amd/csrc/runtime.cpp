@@ -24,6 +24,7 @@
 #include <exception>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/edsl_hip.h"
 #include "../../include/edsl_hip_device.h"
@@ -75,17 +76,33 @@ int copy_out(const std::string& s, char* buf, size_t len) {
 struct DevBuf {
   void* p = nullptr;
   size_t cap = 0;
-  // Grow-only. The old buffer may still be in use by queued work, so the
-  // device is drained before it is released.
+  // Workspaces of the device entry points may be baked into HIP graphs that
+  // callers capture, so an outgrown one is kept (retired) rather than freed:
+  // a replay still finds the buffer it was captured with. Growth is then at
+  // least twofold, which bounds the retired total by the final capacity.
+  bool keep_old = false;
+  std::vector<void*> retired;
+
+  DevBuf() = default;
+  explicit DevBuf(bool keep) : keep_old(keep) {}
+
+  // Grow-only. A buffer that is released may still be in use by queued work,
+  // so the device is drained first.
   void* ensure(size_t bytes, bool zero_fill) {
     if (bytes <= cap && p) return p;
-    if (p) {
+    size_t grow = 0;
+    if (p && keep_old) {
+      retired.push_back(p);
+      grow = 2 * cap;
+      p = nullptr;
+      cap = 0;
+    } else if (p) {
       check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
       check_hip(hipFree(p), "hipFree");
       p = nullptr;
       cap = 0;
     }
-    const size_t want = std::max<size_t>((bytes + 255) & ~size_t(255), 256);
+    const size_t want = std::max<size_t>({(bytes + 255) & ~size_t(255), size_t(256), grow});
     check_hip(hipMalloc(&p, want), "hipMalloc");
     if (zero_fill) {
       // Finished before any stream (blocking or not) can use the buffer.
@@ -104,8 +121,8 @@ struct DeviceState {
   int cus = 256;
   DevBuf stage[4];  // host-operand staging: X/A, W/B, bias, Y/C
   DevBuf chain[2];  // intermediate activations of multi-layer programs (ping-pong)
-  DevBuf gemv_partials;
-  DevBuf i8_x, i8_w, i8_flag;
+  DevBuf gemv_partials{true};
+  DevBuf i8_x{true}, i8_w{true}, i8_flag{true};
   unsigned epoch = 0;
   // Ordering of the launches that use the library scratch above (split-K
   // partials, packed int8 operands and flag) across streams.
@@ -163,7 +180,20 @@ DeviceState& device_state(int* dev_out) {
 // every scratch launch records ws_ev after its kernels, and a launch from a
 // stream other than the last one waits for that event first. Overlapping
 // calls on different streams are thereby serialised on the device.
+// While `stream` is being captured into a graph nothing is added: a captured
+// launch cannot wait for work outside the capture, and replays are ordered
+// by the stream the graph is launched on.
+bool capturing(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return st != hipStreamCaptureStatusNone;
+}
+
 void scratch_begin(DeviceState& ds, hipStream_t stream) {
+  if (capturing(stream)) return;
   if (!ds.ws_multi) {
     if (!ds.ws_seen || stream == ds.ws_stream) return;
     check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
@@ -175,6 +205,7 @@ void scratch_begin(DeviceState& ds, hipStream_t stream) {
 }
 
 void scratch_end(DeviceState& ds, hipStream_t stream) {
+  if (capturing(stream)) return;
   ds.ws_seen = true;
   ds.ws_stream = stream;
   if (ds.ws_multi) check_hip(hipEventRecord(ds.ws_ev, stream), "hipEventRecord");
