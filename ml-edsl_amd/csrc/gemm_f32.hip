@@ -335,6 +335,9 @@ gemm_f32_kernel(GemmF32Args args) {
 //         per CU for latency-bound mid-size shapes
 //  22: 64x64x64 (k2) with global loads two K steps ahead (_pf2); the same
 //      lead measured slower for the k4 and 256x256 tiles
+//  23: 256x256x16 with 16 waves (4x4, wave tile 64x64): at 4096^3 ~2 % faster
+//      than 8 waves (992 vs 1012 us); 8x2 waves measure the same, 2x8 and
+//      BK = 32 with 16 waves slower, two K steps of prefetch slower
 const GemmF32Config kConfigs[] = {
     {256, 256, 16, 2, 2, false, "f32_256x256x16_w2x2"},
     {256, 256, 16, 4, 2, false, "f32_256x256x16_w4x2"},
@@ -359,6 +362,7 @@ const GemmF32Config kConfigs[] = {
     {64, 64, 128, 2, 2, false, "f32_64x64x128_w2x2_k4"},
     {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2_k4"},
     {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2_k2_pf2"},
+    {256, 256, 16, 4, 4, false, "f32_256x256x16_w4x4"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -415,6 +419,7 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case 20: return launch_cfg<64, 64, 128, 2, 2, 4, false>(epi, a, stream);
     case 21: return launch_cfg<64, 64, 64, 2, 2, 4, false>(epi, a, stream);
     case 22: return launch_cfg<64, 64, 64, 2, 2, 2, false, 2>(epi, a, stream);
+    case 23: return launch_cfg<256, 256, 16, 4, 4, 1, false>(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -368,12 +368,13 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     if (g_force_cfg >= 0 && g_force_cfg < gemm_f32_num_configs() && fits(g_force_cfg)) {
       cfg = g_force_cfg;
     } else {
-      // Measured on MI355X: 256x256x32 (8 waves) at 4096^3; at 1024^3 the 64x64x64 tile with two
+      // Measured on MI355X: 256x256x16 with 16 waves at 4096^3 (992 us; 256x256x32 with 8 waves
+      // 1012 us, the next in line); at 1024^3 the 64x64x64 tile with two
       // waves per output block splitting K and global loads two K steps ahead (24.9 us) beats
       // four K waves (25.6 us), two with one step ahead (26.1 us) and the plain 64x64x16 tile
       // (29.6 us); at 256^3 the 32x32x64 tile with four K waves (64 workgroups, 3.5 us inside
       // the kernel) beats every 64x64 tile (16 workgroups, 7 us).
-      static const int kOrder[] = {5, 0, 6, 2, 22, 21, 14, 15, 3, 17};
+      static const int kOrder[] = {23, 5, 0, 6, 2, 22, 21, 14, 15, 3, 17};
       int best = -1;
       int64_t best_tiles = 0;
       for (int c : kOrder) {
