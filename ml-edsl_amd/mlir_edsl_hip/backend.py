@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import ctypes
 import enum
+import threading
 from dataclasses import dataclass, field
 from typing import Any, Sequence
 
@@ -201,6 +202,24 @@ def make_output_descriptor(tensor_type: TensorType, like=None):
     return c_types, c_vals, buf
 
 
+def _data_ptr(a: np.ndarray) -> int:
+    return a.__array_interface__["data"][0]
+
+
+class _GpuArgs:
+    """Argument arrays of edsl_hip_execute_gpu_function for n inputs of rank
+    <= 2: pointers, per-input shape arrays (and the array of pointers to
+    them), ranks and the output shape."""
+
+    def __init__(self, n: int):
+        self.ptrs = (ctypes.c_void_p * n)()
+        self.ranks = (ctypes.c_int * n)()
+        self.dims = [(ctypes.c_int64 * 2)() for _ in range(n)]
+        self.shapes = (ctypes.POINTER(ctypes.c_int64) * n)(
+            *[ctypes.cast(d, ctypes.POINTER(ctypes.c_int64)) for d in self.dims])
+        self.oshape = (ctypes.c_int64 * 2)()
+
+
 class HipBackend:
     """Function registry + execution for the HIP dense path (one per process,
     see :func:`get_backend`)."""
@@ -210,6 +229,7 @@ class HipBackend:
         self._functions: dict[str, DenseFunction] = {}
         self._target = "gpu"
         self._opt_level = 2
+        self._tls = threading.local()  # per-thread argument arrays of execute_gpu_function
 
     # ---------------------------------------------------------- compilation
     def compile_dense(self, name: str, pattern: str, param_types: Sequence[TensorType],
@@ -218,6 +238,12 @@ class HipBackend:
         fn = DenseFunction(name, pattern, list(param_types), ret, alpha)
         self._functions[name] = fn
         return fn
+
+    def _gpu_args(self, n: int) -> "_GpuArgs":
+        cache = self._tls.__dict__.setdefault("gpu_args", {})
+        if n not in cache:
+            cache[n] = _GpuArgs(n)
+        return cache[n]
 
     def has_function(self, name: str) -> bool:
         return name in self._functions
@@ -280,17 +306,23 @@ class HipBackend:
             if a.dtype != pt.element_type.numpy_dtype:
                 raise TypeError(f"ndarray dtype {a.dtype} does not match expected "
                                 f"{np.dtype(pt.element_type.numpy_dtype)}")
+            if a.ndim > 2:
+                raise TypeError(f"rank {a.ndim} operand: the dense path takes 1-D and 2-D arrays")
             arrays.append(np.ascontiguousarray(a))
-        ptrs = (ctypes.c_void_p * n)(*[a.ctypes.data for a in arrays])
-        shape_bufs = [(ctypes.c_int64 * a.ndim)(*a.shape) for a in arrays]
-        shapes = (ctypes.POINTER(ctypes.c_int64) * n)(
-            *[ctypes.cast(s, ctypes.POINTER(ctypes.c_int64)) for s in shape_bufs])
-        ranks = (ctypes.c_int * n)(*[a.ndim for a in arrays])
+        # The argument arrays are reused per thread and filled in place: building
+        # them per call (ctypes.cast in particular) leaves reference cycles that
+        # pile up until a full garbage collection, tens of ms with torch loaded.
+        a_ = self._gpu_args(n)
+        for i, a in enumerate(arrays):
+            a_.ptrs[i] = _data_ptr(a)
+            a_.ranks[i] = a.ndim
+            for d, extent in enumerate(a.shape):
+                a_.dims[i][d] = extent
         out = np.empty(fn.return_type.shape, dtype=fn.return_type.element_type.numpy_dtype)
-        oshape = (ctypes.c_int64 * 2)(*out.shape)
+        a_.oshape[0], a_.oshape[1] = out.shape
         rc = self._lib.edsl_hip_execute_gpu_function(
-            _PATTERN_CODES[fn.pattern], fn.return_type.element_type.code, n, ptrs, shapes, ranks,
-            out.ctypes.data, oshape, 2, 4, fn.alpha)
+            _PATTERN_CODES[fn.pattern], fn.return_type.element_type.code, n, a_.ptrs, a_.shapes, a_.ranks,
+            _data_ptr(out), a_.oshape, 2, 4, fn.alpha)
         if rc != 0:
             _native.raise_on_error(name)
         return out

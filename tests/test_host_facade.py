@@ -106,3 +106,33 @@ def test_workload_inputs_are_deterministic_and_in_range():
     assert A.dtype == np.float32 and A.min() >= -1 and A.max() < 1
     X, W, b = make_inputs(WORKLOADS["c2"], M=32, K=1024, N=16)
     assert abs(float(W.std()) - 1 / 32) < 0.005 and np.abs(b).max() <= 0.1
+
+
+def test_execute_gpu_function_builds_no_reference_cycles():
+    """The host-array entry reuses per-thread argument arrays: building them
+    per call (ctypes.cast) left ~5 cyclic objects per call, which with torch
+    loaded made every few hundred calls pay a full garbage collection of tens
+    of ms. Here the call fails (no device in this container) after the
+    marshalling; on a GPU box it succeeds; neither may leave cyclic garbage
+    that grows with the number of calls."""
+    import gc
+    be = HipBackend()
+    A = np.ones((4, 4), np.float32)
+    be.compile_dense("cyc", "matmul", [TensorType((4, 4), f32)] * 2)
+
+    def call():
+        try:
+            be.execute_gpu_function("cyc", A, A)
+        except RuntimeError:
+            pass
+
+    call()  # creates this thread's argument arrays (once)
+    gc.collect()
+    gc.disable()
+    try:
+        for _ in range(200):
+            call()
+        unreachable = gc.collect()
+    finally:
+        gc.enable()
+    assert unreachable < 20, unreachable  # the per-call arrays left ~1000 here
