@@ -331,10 +331,16 @@ class HipBackend:
 _global_backend: HipBackend | None = None
 
 
+_backend_lock = threading.Lock()
+
+
 def get_backend() -> HipBackend:
+    """The process-wide backend, created on first use (by one thread only)."""
     global _global_backend
     if _global_backend is None:
-        _global_backend = HipBackend()
+        with _backend_lock:
+            if _global_backend is None:
+                _global_backend = HipBackend()
     return _global_backend
 
 
