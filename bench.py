@@ -302,7 +302,8 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures the dense path on one GPU only: this build has no multi-GPU "
-              "path (the column-sharding design is described in DESIGN.md); run with --gpus 1.",
+              "path. One GPU's share of an 8-way column-sharded layer is measured as the "
+              "c4s8 and c3s8 workloads; run with --gpus 1.",
               file=sys.stderr)
         return 2
 
