@@ -27,6 +27,7 @@
 #include "kernels.hpp"
 
 #include <type_traits>
+#include <utility>
 
 namespace edsl {
 namespace {
@@ -59,6 +60,16 @@ __device__ __forceinline__ void load_b_frag(const float* p, float (&v)[CP]) {
 
 template <int N>
 using Ic = std::integral_constant<int, N>;
+
+// f(Ic<0>{}), f(Ic<1>{}), ..., f(Ic<N-1>{}) in order.
+template <typename F, int... S>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, S...>) {
+  (f(Ic<S>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int WAVES_K, int PF, int EPI, bool GUARD>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64)
@@ -96,7 +107,7 @@ gemm_f32_kernel(GemmF32Args args) {
   const int n0 = tn * BN;
   const int M = args.M, N = args.N, K = args.K;
 
-  static_assert(PF == 1 || PF == 2, "global prefetch depth");
+  static_assert(PF >= 1 && PF <= 4, "global prefetch depth");
   f32x4 ra[PF][A_LD];
   f32x4 rb[PF][B_LD];
 
@@ -209,32 +220,38 @@ gemm_f32_kernel(GemmF32Args args) {
       }
     }
   } else if (nk > 0) {
-    // Two K steps of global loads in flight: while step kt is computed from
-    // LDS buffer kt&1, step kt+1 (register set (kt+1)&1, loaded one iteration
-    // earlier) goes to the other LDS buffer and step kt+2 is loaded into set
-    // kt&1. Past the last step the loads repeat the last step (in bounds,
-    // never used), so the body has no branch and its wait counts stay exact.
-    load_global(Ic<0>{}, 0);
-    load_global(Ic<1>{}, (nk > 1 ? 1 : 0) * BK);
+    // PF K steps of global loads in flight, in a ring of PF register sets
+    // (step s lives in set s % PF): while step kt is computed from LDS buffer
+    // kt&1, step kt+1 (loaded PF-1 iterations earlier) goes to the other LDS
+    // buffer and step kt+PF is loaded into set kt % PF, whose step went to the
+    // LDS one iteration earlier. Past the last step the loads repeat the last
+    // step (in bounds, never used), so the body has no branch and its wait
+    // counts stay exact.
+    auto prologue = [&](auto set) {
+      constexpr int S = decltype(set)::value;
+      load_global(Ic<S>{}, min(S, nk - 1) * BK);
+    };
+    static_for<PF>(prologue);
     store_lds(Ic<0>{}, 0);
     __syncthreads();
     auto step = [&](auto cur, int kt) {
       constexpr int C = decltype(cur)::value;
-      load_global(Ic<C>{}, min(kt + 2, nk - 1) * BK);
+      load_global(Ic<C>{}, min(kt + PF, nk - 1) * BK);
       // Keep the loads ahead of this step's MFMAs (the scheduler would
-      // otherwise sink them and shorten their lead to one step).
+      // otherwise sink them and shorten their lead).
       __builtin_amdgcn_sched_barrier(0);
       compute(kt & 1);
       __builtin_amdgcn_sched_barrier(0);
-      store_lds(Ic<1 - C>{}, (kt + 1) & 1);
+      store_lds(Ic<(C + 1) % PF>{}, (kt + 1) & 1);
       __syncthreads();
     };
     int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-      step(Ic<0>{}, kt);
-      step(Ic<1>{}, kt + 1);
+    for (; kt + PF <= nk; kt += PF) {
+      static_for<PF>([&](auto s) { step(s, kt + decltype(s)::value); });
     }
-    if (kt < nk) step(Ic<0>{}, kt);
+    static_for<PF>([&](auto s) {
+      if (kt + decltype(s)::value < nk) step(s, kt + decltype(s)::value);
+    });
   }
 
   // Waves that split K add their partial tiles into wave group 0 through
@@ -341,6 +358,11 @@ gemm_f32_kernel(GemmF32Args args) {
 //  23: 256x256x16 with 16 waves (4x4, wave tile 64x64): at 4096^3 ~2 % faster
 //      than 8 waves (992 vs 1012 us); 8x2 waves measure the same, 2x8 and
 //      BK = 32 with 16 waves slower, two K steps of prefetch slower
+//  24: 64x64x32 (k2) with global loads four K steps ahead: at 1024^3 (one
+//      workgroup per CU, nothing else on the CU to hide a step's loads)
+//      24.1-24.4 vs 24.6-25.0 us for 22; at 4096x512x4096 (two per CU) 171
+//      vs 163 us. Three steps ahead, and 64-deep steps four ahead, measured
+//      no better than 22.
 const GemmF32Config kConfigs[] = {
     {256, 256, 16, 2, 2, false, "f32_256x256x16_w2x2"},
     {256, 256, 16, 4, 2, false, "f32_256x256x16_w4x2"},
@@ -366,6 +388,7 @@ const GemmF32Config kConfigs[] = {
     {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2_k4"},
     {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2_k2_pf2"},
     {256, 256, 16, 4, 4, false, "f32_256x256x16_w4x4"},
+    {64, 64, 32, 2, 2, false, "f32_64x64x32_w2x2_k2_pf4"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -423,6 +446,7 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case 21: return launch_cfg<64, 64, 64, 2, 2, 4, false>(epi, a, stream);
     case 22: return launch_cfg<64, 64, 64, 2, 2, 2, false, 2>(epi, a, stream);
     case 23: return launch_cfg<256, 256, 16, 4, 4, 1, false>(epi, a, stream);
+    case 24: return launch_cfg<64, 64, 32, 2, 2, 2, false, 4>(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

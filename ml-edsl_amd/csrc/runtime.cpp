@@ -374,13 +374,18 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
       // four K waves (25.6 us), two with one step ahead (26.1 us) and the plain 64x64x16 tile
       // (29.6 us); at 256^3 the 32x32x64 tile with four K waves (64 workgroups, 3.5 us inside
       // the kernel) beats every 64x64 tile (16 workgroups, 7 us).
-      static const int kOrder[] = {23, 5, 0, 6, 2, 22, 21, 14, 15, 3, 17};
+      // The 64x64 tile with four 32-deep K steps of loads ahead (24) only
+      // pays when there is one workgroup per CU at most (1024^3: 24.1-24.4 us
+      // against 24.6-25.0 for 22); with two per CU the other workgroup hides
+      // the loads and the deeper steps of 22 win (4096x512x4096: 163 vs 171 us).
+      static const int kOrder[] = {23, 5, 0, 6, 2, 24, 22, 21, 14, 15, 3, 17};
       int best = -1;
       int64_t best_tiles = 0;
       for (int c : kOrder) {
         if (!fits(c)) continue;
         const GemmF32Config& g = gemm_f32_config(c);
         const int64_t tiles = (int64_t)(M / g.bm) * (N / g.bn);
+        if (c == 24 && tiles > ds.cus) continue;
         if (tiles >= ds.cus) {
           cfg = c;
           break;
