@@ -269,6 +269,119 @@ __global__ void __launch_bounds__(256) gemm_i8_kernel(GemmI32Args a) {
   }
 }
 
+// K-split waves: every wave computes the whole 128x128 tile (4x4 blocks of
+// 32x32, 256 accumulator registers) over every fourth 32-k step (wave w takes
+// steps w, w + 4, ...). Each A and B fragment is then fetched by exactly one
+// wave -- half the vector-cache requests of the quadrant layout above, where
+// every fragment is fetched by the two waves sharing its row or column block
+// -- and each wave runs 16 MFMAs per 8 fragment loads instead of 4 per 4.
+// Afterwards the four partial tiles are summed through LDS in two rounds of
+// two row blocks; integer addition wraps associatively, so the order of the
+// sum does not change the result. One workgroup per CU (all 512 registers per
+// lane are available to its waves).
+constexpr int kI8KsRedBytes = 4 * 2 * 4 * 16 * 64 * 4;  // [wave][ii][j][reg][lane] i32, 128 KB
+
+template <int EPI, int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_i8_ksplit_kernel(GemmI32Args a) {
+  __shared__ i32x4 red[kI8KsRedBytes / 16];
+  static_assert(sizeof(ValuSmem) <= sizeof(red), "exact-path staging must fit the reduce buffer");
+  int tm, tn;
+  tile_coords(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  const int m0 = tm * kI8Tile, n0 = tn * kI8Tile;
+
+  if (*a.flag == a.epoch) {  // some value outside int8: exact i32 path
+    valu_tile_i32<EPI, 256>(a, m0, n0, *reinterpret_cast<ValuSmem*>(red));
+    return;
+  }
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int KT = a.K >> 5;  // 32-k steps, a multiple of 4
+  const int NS = KT >> 2;   // steps per wave, a multiple of D
+  const i32x4* ap = reinterpret_cast<const i32x4*>(a.A8p) + (int64_t)(m0 >> 5) * KT * 64 + lane;
+  const i32x4* bp = reinterpret_cast<const i32x4*>(a.B8p) + (int64_t)(n0 >> 5) * KT * 64 + lane;
+  const int64_t block_stride = (int64_t)KT * 64;  // next 32-row (or 32-column) block
+
+  i32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  // Loads of this wave's t-th step; past the last one the last is loaded again
+  // (never used), which keeps the loop free of branches.
+  i32x4 fa[D][4], fb[D][4];
+  auto load = [&](i32x4(&xa)[4], i32x4(&xb)[4], int t) {
+    const int64_t s = (int64_t)(min(t, NS - 1) * 4 + wave) * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xa[i] = ap[i * block_stride + s];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xb[j] = bp[j * block_stride + s];
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    load(fa[d], fb[d], d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll 1
+  for (int t0 = 0; t0 < NS; t0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[d][i], fb[d][j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      load(fa[d], fb[d], t0 + d + D);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // Round h: every wave writes its partial blocks (2h + ii, j) for ii < 2,
+  // j < 4; then wave w sums row block 2h + w/2, column blocks 2(w%2) + jj over
+  // the four waves and stores them with the epilogue. A lane holds rows
+  // 8*(r/4) + 4*half + r%4 and column l32 of each block, so each store
+  // instruction writes two full 128-byte row segments.
+  const int half = lane >> 5, l32 = lane & 31;
+  auto slot = [&](int p, int ii, int j, int q) { return (((p * 2 + ii) * 4 + j) * 4 + q) * 64 + lane; };
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (h == 1) __syncthreads();  // round 0's reads are done before round 1 overwrites
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const i32x16& v = acc[2 * h + ii][j];
+          red[slot(wave, ii, j, q)] = i32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+        }
+    __syncthreads();
+    const int ii = wave >> 1;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * (wave & 1) + jj;
+      const int n = n0 + 32 * j + l32;
+      const int32_t b = epi_has_bias(EPI) ? a.bias[n] : 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        i32x4 sum = red[slot(0, ii, j, q)];
+#pragma unroll
+        for (int p = 1; p < 4; ++p) sum += red[slot(p, ii, j, q)];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = m0 + 32 * (2 * h + ii) + 8 * q + 4 * half + e;
+          __builtin_nontemporal_store(apply_epilogue_i32<EPI>(sum[e], b), a.C + (int64_t)m * a.ldc + n);
+        }
+      }
+    }
+  }
+}
+
 #define EDSL_I32_EPI_SWITCH(KERNEL, GRID, ARGS)                                        \
   switch (epi) {                                                                       \
     case epi_code(false, ACT_NONE):                                                    \
@@ -287,12 +400,15 @@ __global__ void __launch_bounds__(256) gemm_i8_kernel(GemmI32Args a) {
       return hipErrorInvalidValue;                                                     \
   }
 
-template <int D>
+template <bool KSPLIT, int D>
 hipError_t launch_i8_depth(int epi, const GemmI32Args& a, hipStream_t stream) {
   const dim3 grid(a.tiles_m * a.tiles_n), block(256);
-#define EDSL_I8_CASE(E)                                                              \
-  case E:                                                                            \
-    hipLaunchKernelGGL((gemm_i8_kernel<E, D>), grid, block, 0, stream, a);           \
+#define EDSL_I8_CASE(E)                                                                      \
+  case E:                                                                                    \
+    if constexpr (KSPLIT)                                                                    \
+      hipLaunchKernelGGL((gemm_i8_ksplit_kernel<E, D>), grid, block, 0, stream, a);          \
+    else                                                                                     \
+      hipLaunchKernelGGL((gemm_i8_kernel<E, D>), grid, block, 0, stream, a);                 \
     break;
   switch (epi) {
     EDSL_I8_CASE(epi_code(false, ACT_NONE))
@@ -305,6 +421,18 @@ hipError_t launch_i8_depth(int epi, const GemmI32Args& a, hipStream_t stream) {
 #undef EDSL_I8_CASE
   return hipGetLastError();
 }
+
+// Variant table: wave layout and prefetch depth (32-k steps in flight per
+// wave). The quadrant layout needs K/32 % depth == 0, the K-split one
+// K/128 % depth == 0; a depth that does not divide falls to the next entry of
+// its fallback list.
+struct I8Variant {
+  bool ksplit;
+  int depth[3];  // preferred first; the last is always 1 or a divisor of 4
+};
+constexpr I8Variant kI8Table[kI8Variants] = {
+    {false, {4, 4, 4}}, {false, {2, 2, 2}}, {false, {8, 4, 4}}, {true, {2, 1, 1}}, {true, {4, 2, 1}},
+};
 
 }  // namespace
 
@@ -320,19 +448,35 @@ hipError_t launch_narrow_i8(NarrowI8Args a, hipStream_t stream) {
 
 int gemm_i8_depth(int variant, int K) {
   if (variant < 0 || variant >= kI8Variants) variant = kI8DefaultVariant;
-  static const int kDepth[kI8Variants] = {4, 2, 8};
-  const int d = kDepth[variant];
-  return (K / 32) % d == 0 ? d : 4;  // K % 128 == 0 on this path, so 4 always divides
+  const I8Variant& v = kI8Table[variant];
+  const int steps = v.ksplit ? K / 128 : K / 32;  // K % 128 == 0 on this path
+  for (int d : v.depth)
+    if (steps % d == 0) return d;
+  return 1;
+}
+
+bool gemm_i8_ksplit(int variant) {
+  if (variant < 0 || variant >= kI8Variants) variant = kI8DefaultVariant;
+  return kI8Table[variant].ksplit;
 }
 
 hipError_t launch_gemm_i8(int epi, GemmI32Args a, hipStream_t stream, int variant) {
   if (a.M % kI8Tile || a.N % kI8Tile || a.K % kI8Tile || a.K <= 0) return hipErrorInvalidValue;
   a.tiles_m = a.M / kI8Tile;
   a.tiles_n = a.N / kI8Tile;
-  switch (gemm_i8_depth(variant, a.K)) {
-    case 2: return launch_i8_depth<2>(epi, a, stream);
-    case 4: return launch_i8_depth<4>(epi, a, stream);
-    case 8: return launch_i8_depth<8>(epi, a, stream);
+  const int d = gemm_i8_depth(variant, a.K);
+  if (gemm_i8_ksplit(variant)) {
+    switch (d) {
+      case 1: return launch_i8_depth<true, 1>(epi, a, stream);
+      case 2: return launch_i8_depth<true, 2>(epi, a, stream);
+      case 4: return launch_i8_depth<true, 4>(epi, a, stream);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  switch (d) {
+    case 2: return launch_i8_depth<false, 2>(epi, a, stream);
+    case 4: return launch_i8_depth<false, 4>(epi, a, stream);
+    case 8: return launch_i8_depth<false, 8>(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -85,11 +85,16 @@ struct GemmI32Args {
 
 constexpr int kI8Tile = 128;   // M, N, K multiples of this for the int8 MFMA path
 hipError_t launch_narrow_i8(NarrowI8Args args, hipStream_t stream);
-// variant = fragment prefetch depth in 32-k steps: 0 = 4, 1 = 2, 2 = 8 (needs
-// K % 256 == 0, else 4); -1 = default (8: measured fastest at 2048^3).
-constexpr int kI8Variants = 3;
-constexpr int kI8DefaultVariant = 2;
+// variant = wave layout + fragment prefetch depth in 32-k steps:
+//   0..2: 2x2 waves of 64x64 quadrants, depth 4, 2, 8 (8 needs K % 256 == 0,
+//         else 4);
+//   3..4: K-split waves (each wave the whole tile on every fourth k step),
+//         depth 2 and 4 (when K/128 is not a multiple, 2 then 1);
+// -1 = default.
+constexpr int kI8Variants = 5;
+constexpr int kI8DefaultVariant = 3;
 int gemm_i8_depth(int variant, int K);
+bool gemm_i8_ksplit(int variant);
 hipError_t launch_gemm_i8(int epi, GemmI32Args args, hipStream_t stream, int variant = -1);
 // Exact wrapping i32 GEMM on the vector ALUs: any shape, any alignment.
 hipError_t launch_gemm_i32_valu(int epi, GemmI32Args args, hipStream_t stream);

@@ -460,7 +460,8 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     const int variant = (g_force_i8 >= 0 && g_force_i8 < kI8Variants) ? g_force_i8 : kI8DefaultVariant;
     check_hip(launch_gemm_i8(L.epi, a, stream, variant), "gemm_i8 launch");
     scratch_end(ds, stream);
-    set_plan("narrow_i8+gemm_i8 variant=%d depth=%d grid=%d", variant, gemm_i8_depth(variant, a.K),
+    set_plan("narrow_i8+gemm_i8 variant=%d waves=%s depth=%d grid=%d", variant,
+             gemm_i8_ksplit(variant) ? "ksplit" : "quadrant", gemm_i8_depth(variant, a.K),
              (a.M / kI8Tile) * (a.N / kI8Tile));
   } else {
     check_hip(launch_gemm_i32_valu(L.epi, a, stream), "gemm_i32_valu launch");
