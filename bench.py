@@ -43,7 +43,7 @@ PEAK = {  # MI355X published dense peaks
     "hbm_gbs": 8000.0,
 }
 KERNEL_NAMES = {"c1": "gemm_f32_kernel", "c2": "gemm_f32_kernel", "c3": "gemm_f32_kernel",
-                "c4": "gemv_f32_kernel + gemv_reduce_kernel", "c5": "narrow_i8_kernel + gemm_i8_kernel",
+                "c4": "gemv_f32_kernel + gemv_reduce_kernel", "c5": "narrow_i8_kernel + gemm_i8_ksplit_kernel",
                 "c3s8": "gemm_f32_kernel", "c4s8": "gemv_f32_kernel + gemv_reduce_kernel"}
 
 
