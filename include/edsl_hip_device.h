@@ -70,9 +70,9 @@ void edsl_hip_set_gemv_ksplit(int ksplit);
 void edsl_hip_set_gemv_cols(int cols);
 /* int8 GEMM variant = wave layout and operand prefetch depth in 32-k steps:
  * 0..2 give each of 4 waves a 64x64 quadrant of the 128x128 tile, depth
- * 0: 4, 1: 2, 2: 8 when K % 256 == 0, else 4; 3..4 give each wave the whole
- * tile on every fourth 32-k step (partials summed in LDS), depth 3: 2,
- * 4: 4 when K/128 is a multiple of it, else 2, then 1.
+ * 0: 4, 1: 2, 2: 8 when K % 256 == 0, else 4; 3 gives each wave the whole
+ * tile on every fourth 32-k step (partials summed in LDS), depth 2 when
+ * K/128 is even, else 1.
  * index < edsl_hip_i8_variant_count(); -1 = automatic. */
 void edsl_hip_set_i8_variant(int variant);
 int edsl_hip_i8_variant_count(void);

@@ -224,9 +224,10 @@ gemm_f32_kernel(GemmF32Args args) {
     // (step s lives in set s % PF): while step kt is computed from LDS buffer
     // kt&1, step kt+1 (loaded PF-1 iterations earlier) goes to the other LDS
     // buffer and step kt+PF is loaded into set kt % PF, whose step went to the
-    // LDS one iteration earlier. Past the last step the loads repeat the last
-    // step (in bounds, never used), so the body has no branch and its wait
-    // counts stay exact.
+    // LDS one iteration earlier. At depth 4, when PF divides the step count,
+    // the last PF steps, already loaded, run without loads. Otherwise the
+    // loads past the last step repeat the last step (in bounds, never used),
+    // so the body has no branch and its wait counts stay exact.
     auto prologue = [&](auto set) {
       constexpr int S = decltype(set)::value;
       load_global(Ic<S>{}, min(S, nk - 1) * BK);
@@ -246,12 +247,35 @@ gemm_f32_kernel(GemmF32Args args) {
       __syncthreads();
     };
     int kt = 0;
-    for (; kt + PF <= nk; kt += PF) {
-      static_for<PF>([&](auto s) { step(s, kt + decltype(s)::value); });
+    // At depth 4 the repeated loads are 4 of every nk + 4 (1/9 at C2's 32
+    // steps), and a tail without them measured 2% faster there. At depth 2
+    // (2 of 66 at the 8-way C3 column shard, two workgroups per CU) the tail
+    // measured 1-4% slower, so that depth keeps the repeated loads.
+    if (PF >= 4 && nk % PF == 0) {
+      // Every load of the loop is in range, and the last PF steps (already
+      // loaded) run without loads: no step is fetched twice.
+      for (; kt + PF < nk; kt += PF) {
+        static_for<PF>([&](auto s) { step(s, kt + decltype(s)::value); });
+      }
+      static_for<PF>([&](auto s) {
+        constexpr int C = decltype(s)::value;
+        compute((kt + C) & 1);
+        if constexpr (C + 1 < PF) {
+          __builtin_amdgcn_sched_barrier(0);
+          store_lds(Ic<C + 1>{}, (kt + C + 1) & 1);
+        }
+        // Also after the last step: the K-split reduction below reuses the
+        // A tile's LDS.
+        __syncthreads();
+      });
+    } else {
+      for (; kt + PF <= nk; kt += PF) {
+        static_for<PF>([&](auto s) { step(s, kt + decltype(s)::value); });
+      }
+      static_for<PF>([&](auto s) {
+        if (kt + decltype(s)::value < nk) step(s, kt + decltype(s)::value);
+      });
     }
-    static_for<PF>([&](auto s) {
-      if (kt + decltype(s)::value < nk) step(s, kt + decltype(s)::value);
-    });
   }
 
   // Waves that split K add their partial tiles into wave group 0 through

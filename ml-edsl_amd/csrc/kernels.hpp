@@ -88,10 +88,10 @@ hipError_t launch_narrow_i8(NarrowI8Args args, hipStream_t stream);
 // variant = wave layout + fragment prefetch depth in 32-k steps:
 //   0..2: 2x2 waves of 64x64 quadrants, depth 4, 2, 8 (8 needs K % 256 == 0,
 //         else 4);
-//   3..4: K-split waves (each wave the whole tile on every fourth k step),
-//         depth 2 and 4 (when K/128 is not a multiple, 2 then 1);
+//   3:    K-split waves (each wave the whole tile on every fourth k step),
+//         depth 2 (1 when K/128 is odd);
 // -1 = default.
-constexpr int kI8Variants = 5;
+constexpr int kI8Variants = 4;
 constexpr int kI8DefaultVariant = 3;
 int gemm_i8_depth(int variant, int K);
 bool gemm_i8_ksplit(int variant);
