@@ -413,6 +413,7 @@ const GemmF32Config kConfigs[] = {
     {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2_k2_pf2"},
     {256, 256, 16, 4, 4, false, "f32_256x256x16_w4x4"},
     {64, 64, 32, 2, 2, false, "f32_64x64x32_w2x2_k2_pf4"},
+    {32, 32, 64, 1, 1, false, "f32_32x32x64_w1x1_k4_pf4"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -471,6 +472,7 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case 22: return launch_cfg<64, 64, 64, 2, 2, 2, false, 2>(epi, a, stream);
     case 23: return launch_cfg<256, 256, 16, 4, 4, 1, false>(epi, a, stream);
     case 24: return launch_cfg<64, 64, 32, 2, 2, 2, false, 4>(epi, a, stream);
+    case 25: return launch_cfg<32, 32, 64, 1, 1, 4, false, 4>(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -378,7 +378,10 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
       // pays when there is one workgroup per CU at most (1024^3: 24.1-24.4 us
       // against 24.6-25.0 for 22); with two per CU the other workgroup hides
       // the loads and the deeper steps of 22 win (4096x512x4096: 163 vs 171 us).
-      static const int kOrder[] = {23, 5, 0, 6, 2, 24, 22, 21, 14, 15, 3, 17};
+      // At 256^3 the 32x32x64 tile with four K waves loads all four K steps
+      // up front (25: 7.54-7.56 TFLOP/s against 7.31 for 17, one step ahead;
+      // 2 steps ahead, 8 K waves, or 128-deep steps measured lower).
+      static const int kOrder[] = {23, 5, 0, 6, 2, 24, 22, 21, 14, 15, 3, 25};
       int best = -1;
       int64_t best_tiles = 0;
       for (int c : kOrder) {
