@@ -71,7 +71,17 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int WAVES_K, int PF, int EPI, bool GUARD>
+// GUARD selects the bounds handling:
+//  kGuardNone: M, N, K are multiples of the tile, operands 16-byte aligned.
+//  kGuardEdge: partial tiles at the M, N and K edges; operands 16-byte aligned
+//    with row strides, N and K multiples of 4. Loads stay 16-byte vectors at
+//    clamped addresses: A rows past M read row M-1 and B columns past N read
+//    columns N-4.., which only feed outputs that are never stored; k past K
+//    reads k K-4.. (A) or row K-1 (B) and is then zeroed, since it feeds valid
+//    outputs. Stores are masked per vector (N % 4 == 0, so a vector of CP <= 4
+//    columns is all in or all out).
+//  kGuardAll: any shape and alignment; element-wise checked scalar loads/stores.
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int WAVES_K, int PF, int EPI, int GUARD>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64)
 gemm_f32_kernel(GemmF32Args args) {
   constexpr int NT = WAVES_M * WAVES_N * WAVES_K * 64;
@@ -121,8 +131,12 @@ gemm_f32_kernel(GemmF32Args args) {
       const int q = idx % KCH;
       const int gm = m0 + r;
       const int gk = k0 + 4 * q;
-      if constexpr (!GUARD) {
+      if constexpr (GUARD == kGuardNone) {
         ra[S][i] = *reinterpret_cast<const f32x4*>(args.A + (int64_t)gm * args.lda + gk);
+      } else if constexpr (GUARD == kGuardEdge) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(args.A + (int64_t)min(gm, M - 1) * args.lda +
+                                                        min(gk, K - 4));
+        ra[S][i] = gk < K ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       } else {
         f32x4 v;
 #pragma unroll
@@ -138,8 +152,12 @@ gemm_f32_kernel(GemmF32Args args) {
       const int c = 4 * (idx % (BN / 4));
       const int gk = k0 + r;
       const int gn = n0 + c;
-      if constexpr (!GUARD) {
+      if constexpr (GUARD == kGuardNone) {
         rb[S][i] = *reinterpret_cast<const f32x4*>(args.B + (int64_t)gk * args.ldb + gn);
+      } else if constexpr (GUARD == kGuardEdge) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(args.B + (int64_t)min(gk, K - 1) * args.ldb +
+                                                        min(gn, N - 4));
+        rb[S][i] = gk < K ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       } else {
         f32x4 v;
 #pragma unroll
@@ -324,8 +342,10 @@ gemm_f32_kernel(GemmF32Args args) {
 #pragma unroll
   for (int c = 0; c < CP; ++c) bvals[c] = 0.0f;
   if constexpr (epi_has_bias(EPI)) {
-    if constexpr (!GUARD) {
+    if constexpr (GUARD == kGuardNone) {
       load_b_frag<CP>(args.bias + col0, bvals);
+    } else if constexpr (GUARD == kGuardEdge) {
+      if (col0 < N) load_b_frag<CP>(args.bias + col0, bvals);
     } else {
 #pragma unroll
       for (int c = 0; c < CP; ++c) bvals[c] = (col0 + c < N) ? args.bias[col0 + c] : 0.0f;
@@ -341,15 +361,17 @@ gemm_f32_kernel(GemmF32Args args) {
 #pragma unroll
       for (int c = 0; c < CP; ++c) v[c] = apply_epilogue_f32<EPI>(acc[i][c][r], bvals[c], alpha);
       float* dst = args.C + (int64_t)row * args.ldc + col0;
-      if constexpr (!GUARD) {
-        if constexpr (CP == 4) {
-          f32x4 t = {v[0], v[1], v[2], v[3]};
-          *reinterpret_cast<f32x4*>(dst) = t;
-        } else if constexpr (CP == 2) {
-          f32x2 t = {v[0], v[1]};
-          *reinterpret_cast<f32x2*>(dst) = t;
-        } else {
-          *dst = v[0];
+      if constexpr (GUARD != kGuardAll) {
+        if (GUARD == kGuardNone || (row < M && col0 < N)) {
+          if constexpr (CP == 4) {
+            f32x4 t = {v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<f32x4*>(dst) = t;
+          } else if constexpr (CP == 2) {
+            f32x2 t = {v[0], v[1]};
+            *reinterpret_cast<f32x2*>(dst) = t;
+          } else {
+            *dst = v[0];
+          }
         }
       } else {
         if (row < M) {
@@ -387,37 +409,46 @@ gemm_f32_kernel(GemmF32Args args) {
 //      24.1-24.4 vs 24.6-25.0 us for 22; at 4096x512x4096 (two per CU) 171
 //      vs 163 us. Three steps ahead, and 64-deep steps four ahead, measured
 //      no better than 22.
+//  25: 32x32x64 (k4) with all four 64-deep K steps of a 256-deep K loaded
+//      up front (256^3: 7.54 vs 7.31 TFLOP/s for 17)
+//  26-30: edge-tile twins of 23, 2, 24, 22 and 25 (kGuardEdge) for shapes
+//      the tile does not divide
 const GemmF32Config kConfigs[] = {
-    {256, 256, 16, 2, 2, false, "f32_256x256x16_w2x2"},
-    {256, 256, 16, 4, 2, false, "f32_256x256x16_w4x2"},
-    {128, 128, 16, 2, 2, false, "f32_128x128x16_w2x2"},
-    {64, 64, 16, 2, 2, false, "f32_64x64x16_w2x2"},
-    {64, 64, 16, 2, 2, true, "f32_64x64x16_w2x2_guard"},
-    {256, 256, 32, 4, 2, false, "f32_256x256x32_w4x2"},
-    {128, 256, 16, 2, 2, false, "f32_128x256x16_w2x2"},
-    {64, 64, 32, 2, 2, false, "f32_64x64x32_w2x2"},
-    {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2"},
-    {128, 64, 32, 2, 2, false, "f32_128x64x32_w2x2"},
-    {64, 128, 32, 2, 2, false, "f32_64x128x32_w2x2"},
-    {128, 128, 32, 2, 2, false, "f32_128x128x32_w2x2"},
-    {32, 32, 32, 1, 1, false, "f32_32x32x32_w1x1"},
-    {32, 32, 64, 1, 1, false, "f32_32x32x64_w1x1"},
-    {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2_k2"},
-    {64, 64, 32, 2, 2, false, "f32_64x64x32_w2x2_k2"},
-    {32, 32, 64, 1, 1, false, "f32_32x32x64_w1x1_k2"},
-    {32, 32, 64, 1, 1, false, "f32_32x32x64_w1x1_k4"},
-    {128, 128, 32, 2, 2, false, "f32_128x128x32_w2x2_k2"},
-    {64, 64, 128, 2, 2, false, "f32_64x64x128_w2x2_k2"},
-    {64, 64, 128, 2, 2, false, "f32_64x64x128_w2x2_k4"},
-    {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2_k4"},
-    {64, 64, 64, 2, 2, false, "f32_64x64x64_w2x2_k2_pf2"},
-    {256, 256, 16, 4, 4, false, "f32_256x256x16_w4x4"},
-    {64, 64, 32, 2, 2, false, "f32_64x64x32_w2x2_k2_pf4"},
-    {32, 32, 64, 1, 1, false, "f32_32x32x64_w1x1_k4_pf4"},
+    {256, 256, 16, 2, 2, kGuardNone, "f32_256x256x16_w2x2"},
+    {256, 256, 16, 4, 2, kGuardNone, "f32_256x256x16_w4x2"},
+    {128, 128, 16, 2, 2, kGuardNone, "f32_128x128x16_w2x2"},
+    {64, 64, 16, 2, 2, kGuardNone, "f32_64x64x16_w2x2"},
+    {64, 64, 16, 2, 2, kGuardAll, "f32_64x64x16_w2x2_guard"},
+    {256, 256, 32, 4, 2, kGuardNone, "f32_256x256x32_w4x2"},
+    {128, 256, 16, 2, 2, kGuardNone, "f32_128x256x16_w2x2"},
+    {64, 64, 32, 2, 2, kGuardNone, "f32_64x64x32_w2x2"},
+    {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_w2x2"},
+    {128, 64, 32, 2, 2, kGuardNone, "f32_128x64x32_w2x2"},
+    {64, 128, 32, 2, 2, kGuardNone, "f32_64x128x32_w2x2"},
+    {128, 128, 32, 2, 2, kGuardNone, "f32_128x128x32_w2x2"},
+    {32, 32, 32, 1, 1, kGuardNone, "f32_32x32x32_w1x1"},
+    {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1"},
+    {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_w2x2_k2"},
+    {64, 64, 32, 2, 2, kGuardNone, "f32_64x64x32_w2x2_k2"},
+    {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k2"},
+    {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k4"},
+    {128, 128, 32, 2, 2, kGuardNone, "f32_128x128x32_w2x2_k2"},
+    {64, 64, 128, 2, 2, kGuardNone, "f32_64x64x128_w2x2_k2"},
+    {64, 64, 128, 2, 2, kGuardNone, "f32_64x64x128_w2x2_k4"},
+    {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_w2x2_k4"},
+    {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_w2x2_k2_pf2"},
+    {256, 256, 16, 4, 4, kGuardNone, "f32_256x256x16_w4x4"},
+    {64, 64, 32, 2, 2, kGuardNone, "f32_64x64x32_w2x2_k2_pf4"},
+    {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k4_pf4"},
+    {256, 256, 16, 4, 4, kGuardEdge, "f32_256x256x16_w4x4_edge"},
+    {128, 128, 16, 2, 2, kGuardEdge, "f32_128x128x16_w2x2_edge"},
+    {64, 64, 32, 2, 2, kGuardEdge, "f32_64x64x32_w2x2_k2_pf4_edge"},
+    {64, 64, 64, 2, 2, kGuardEdge, "f32_64x64x64_w2x2_k2_pf2_edge"},
+    {32, 32, 64, 1, 1, kGuardEdge, "f32_32x32x64_w1x1_k4_pf4_edge"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
-template <int BM, int BN, int BK, int WMW, int WNW, int WKW, bool GUARD, int PF = 1>
+template <int BM, int BN, int BK, int WMW, int WNW, int WKW, int GUARD, int PF = 1>
 hipError_t launch_cfg(int epi, const GemmF32Args& a, hipStream_t stream) {
   const dim3 grid(a.tiles_m * a.tiles_n);
   const dim3 block(WMW * WNW * WKW * 64);
@@ -447,32 +478,37 @@ const GemmF32Config& gemm_f32_config(int cfg) { return kConfigs[cfg]; }
 
 hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) {
   switch (cfg) {
-    case 0: return launch_cfg<256, 256, 16, 2, 2, 1, false>(epi, a, stream);
-    case 1: return launch_cfg<256, 256, 16, 4, 2, 1, false>(epi, a, stream);
-    case 2: return launch_cfg<128, 128, 16, 2, 2, 1, false>(epi, a, stream);
-    case 3: return launch_cfg<64, 64, 16, 2, 2, 1, false>(epi, a, stream);
-    case 4: return launch_cfg<64, 64, 16, 2, 2, 1, true>(epi, a, stream);
-    case 5: return launch_cfg<256, 256, 32, 4, 2, 1, false>(epi, a, stream);
-    case 6: return launch_cfg<128, 256, 16, 2, 2, 1, false>(epi, a, stream);
-    case 7: return launch_cfg<64, 64, 32, 2, 2, 1, false>(epi, a, stream);
-    case 8: return launch_cfg<64, 64, 64, 2, 2, 1, false>(epi, a, stream);
-    case 9: return launch_cfg<128, 64, 32, 2, 2, 1, false>(epi, a, stream);
-    case 10: return launch_cfg<64, 128, 32, 2, 2, 1, false>(epi, a, stream);
-    case 11: return launch_cfg<128, 128, 32, 2, 2, 1, false>(epi, a, stream);
-    case 12: return launch_cfg<32, 32, 32, 1, 1, 1, false>(epi, a, stream);
-    case 13: return launch_cfg<32, 32, 64, 1, 1, 1, false>(epi, a, stream);
-    case 14: return launch_cfg<64, 64, 64, 2, 2, 2, false>(epi, a, stream);
-    case 15: return launch_cfg<64, 64, 32, 2, 2, 2, false>(epi, a, stream);
-    case 16: return launch_cfg<32, 32, 64, 1, 1, 2, false>(epi, a, stream);
-    case 17: return launch_cfg<32, 32, 64, 1, 1, 4, false>(epi, a, stream);
-    case 18: return launch_cfg<128, 128, 32, 2, 2, 2, false>(epi, a, stream);
-    case 19: return launch_cfg<64, 64, 128, 2, 2, 2, false>(epi, a, stream);
-    case 20: return launch_cfg<64, 64, 128, 2, 2, 4, false>(epi, a, stream);
-    case 21: return launch_cfg<64, 64, 64, 2, 2, 4, false>(epi, a, stream);
-    case 22: return launch_cfg<64, 64, 64, 2, 2, 2, false, 2>(epi, a, stream);
-    case 23: return launch_cfg<256, 256, 16, 4, 4, 1, false>(epi, a, stream);
-    case 24: return launch_cfg<64, 64, 32, 2, 2, 2, false, 4>(epi, a, stream);
-    case 25: return launch_cfg<32, 32, 64, 1, 1, 4, false, 4>(epi, a, stream);
+    case 0: return launch_cfg<256, 256, 16, 2, 2, 1, kGuardNone>(epi, a, stream);
+    case 1: return launch_cfg<256, 256, 16, 4, 2, 1, kGuardNone>(epi, a, stream);
+    case 2: return launch_cfg<128, 128, 16, 2, 2, 1, kGuardNone>(epi, a, stream);
+    case 3: return launch_cfg<64, 64, 16, 2, 2, 1, kGuardNone>(epi, a, stream);
+    case 4: return launch_cfg<64, 64, 16, 2, 2, 1, kGuardAll>(epi, a, stream);
+    case 5: return launch_cfg<256, 256, 32, 4, 2, 1, kGuardNone>(epi, a, stream);
+    case 6: return launch_cfg<128, 256, 16, 2, 2, 1, kGuardNone>(epi, a, stream);
+    case 7: return launch_cfg<64, 64, 32, 2, 2, 1, kGuardNone>(epi, a, stream);
+    case 8: return launch_cfg<64, 64, 64, 2, 2, 1, kGuardNone>(epi, a, stream);
+    case 9: return launch_cfg<128, 64, 32, 2, 2, 1, kGuardNone>(epi, a, stream);
+    case 10: return launch_cfg<64, 128, 32, 2, 2, 1, kGuardNone>(epi, a, stream);
+    case 11: return launch_cfg<128, 128, 32, 2, 2, 1, kGuardNone>(epi, a, stream);
+    case 12: return launch_cfg<32, 32, 32, 1, 1, 1, kGuardNone>(epi, a, stream);
+    case 13: return launch_cfg<32, 32, 64, 1, 1, 1, kGuardNone>(epi, a, stream);
+    case 14: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardNone>(epi, a, stream);
+    case 15: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardNone>(epi, a, stream);
+    case 16: return launch_cfg<32, 32, 64, 1, 1, 2, kGuardNone>(epi, a, stream);
+    case 17: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardNone>(epi, a, stream);
+    case 18: return launch_cfg<128, 128, 32, 2, 2, 2, kGuardNone>(epi, a, stream);
+    case 19: return launch_cfg<64, 64, 128, 2, 2, 2, kGuardNone>(epi, a, stream);
+    case 20: return launch_cfg<64, 64, 128, 2, 2, 4, kGuardNone>(epi, a, stream);
+    case 21: return launch_cfg<64, 64, 64, 2, 2, 4, kGuardNone>(epi, a, stream);
+    case 22: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardNone, 2>(epi, a, stream);
+    case 23: return launch_cfg<256, 256, 16, 4, 4, 1, kGuardNone>(epi, a, stream);
+    case 24: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardNone, 4>(epi, a, stream);
+    case 25: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardNone, 4>(epi, a, stream);
+    case 26: return launch_cfg<256, 256, 16, 4, 4, 1, kGuardEdge>(epi, a, stream);
+    case 27: return launch_cfg<128, 128, 16, 2, 2, 1, kGuardEdge>(epi, a, stream);
+    case 28: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardEdge, 4>(epi, a, stream);
+    case 29: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardEdge, 2>(epi, a, stream);
+    case 30: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardEdge, 4>(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

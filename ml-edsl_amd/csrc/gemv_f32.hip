@@ -74,9 +74,14 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
   const int g = blockIdx.x % groups;
   const int split = blockIdx.x / groups;
   const int n0 = g * kGroupCols + kWaveCols * wn;
-  const int kspan = a.K / a.ksplit;
-  const int kwave = kspan / WK;  // multiple of 16
-  const int kbeg = split * kspan + wk * kwave;
+  // K, in 16-row chunks, is spread as evenly as possible over the ksplit x WK
+  // slices: slice i = split * WK + wk takes chunks [i*C/S, (i+1)*C/S). When S
+  // divides C every slice has the same length.
+  const int chunks = a.K / 16;
+  const int nslices = a.ksplit * WK;
+  const int slice = split * WK + wk;
+  const int kbeg = 16 * (int)((int64_t)slice * chunks / nslices);
+  const int kwave = 16 * (int)((int64_t)(slice + 1) * chunks / nslices) - kbeg;  // multiple of 16
   const int li = lane & 15;
   const int lg = lane >> 4;
 

@@ -19,10 +19,17 @@ struct GemmF32Args {
   float alpha;        // leaky-ReLU slope
 };
 
+// Bounds handling of a tile configuration.
+enum : int {
+  kGuardNone = 0,  // M, N, K multiples of the tile; 16-byte aligned operands and row strides
+  kGuardEdge = 1,  // partial edge tiles; 16-byte aligned operands, strides, N and K multiples of 4
+  kGuardAll = 2,   // any shape and alignment (element-wise checks)
+};
+
 struct GemmF32Config {
   int bm, bn, bk;
   int waves_m, waves_n;
-  bool guarded;       // bounds-checked scalar loads / stores (any shape, any alignment)
+  int guard;          // kGuard*
   const char* name;
 };
 

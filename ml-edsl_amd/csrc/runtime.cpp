@@ -299,17 +299,19 @@ bool plan_gemv(const DeviceState& ds, int64_t N, int64_t K, int* cols_out, int* 
   for (int cols : kCols) {
     if (g_force_cols > 0 && cols != g_force_cols) continue;
     const int64_t wk = gemv_f32_waves_k(cols);
-    if (N % cols != 0 || K % (16 * wk) != 0 || K < 32 * wk) continue;
+    // K is walked in 16-row chunks spread evenly over the ks x wk wave
+    // slices; the automatic plan gives every slice at least two, a forced
+    // split at least one.
+    if (N % cols != 0 || K % 16 != 0) continue;
     const int64_t groups = N / cols;
     int ks = 1;
     if (g_force_ksplit > 0) {
       // A forced split is taken only by widths that can honour it.
-      if (g_force_ksplit > gemv_f32_max_ksplit() || K % (16 * wk * g_force_ksplit) != 0) continue;
+      if (g_force_ksplit > gemv_f32_max_ksplit() || K < 16 * wk * g_force_ksplit) continue;
       ks = g_force_ksplit;
     } else {
-      while (groups * ks < ds.cus && ks * 2 <= gemv_f32_max_ksplit() && K % (16 * wk * ks * 2) == 0 &&
-             K / (ks * 2) >= 32 * wk)
-        ks *= 2;
+      if (K < 32 * wk) continue;
+      while (groups * ks < ds.cus && ks * 2 <= gemv_f32_max_ksplit() && K >= 32 * wk * ks * 2) ks *= 2;
     }
     const int64_t wgs = groups * ks;
     if (wgs > best_wgs) {
@@ -360,46 +362,61 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
   }
 
   int cfg = -1;
+  // Partial edge tiles need 16-byte vectors that are all in or all out of
+  // range: K and N multiples of 4 (true for every contiguous aligned operand).
+  const bool edge_ok = aligned && K >= 4 && N >= 4 && M >= 1 && K % 4 == 0 && N % 4 == 0;
   auto fits = [&](int c) {
     const GemmF32Config& g = gemm_f32_config(c);
-    return !g.guarded && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
+    if (g.guard == kGuardNone) return aligned && K > 0 && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
+    return g.guard == kGuardEdge && edge_ok;
   };
-  if (aligned && K > 0) {
-    if (g_force_cfg >= 0 && g_force_cfg < gemm_f32_num_configs() && fits(g_force_cfg)) {
-      cfg = g_force_cfg;
-    } else {
-      // Measured on MI355X: 256x256x16 with 16 waves at 4096^3 (992 us; 256x256x32 with 8 waves
-      // 1012 us, the next in line); at 1024^3 the 64x64x64 tile with two
-      // waves per output block splitting K and global loads two K steps ahead (24.9 us) beats
-      // four K waves (25.6 us), two with one step ahead (26.1 us) and the plain 64x64x16 tile
-      // (29.6 us); at 256^3 the 32x32x64 tile with four K waves (64 workgroups, 3.5 us inside
-      // the kernel) beats every 64x64 tile (16 workgroups, 7 us).
-      // The 64x64 tile with four 32-deep K steps of loads ahead (24) only
-      // pays when there is one workgroup per CU at most (1024^3: 24.1-24.4 us
-      // against 24.6-25.0 for 22); with two per CU the other workgroup hides
-      // the loads and the deeper steps of 22 win (4096x512x4096: 163 vs 171 us).
-      // At 256^3 the 32x32x64 tile with four K waves loads all four K steps
-      // up front (25: 7.54-7.56 TFLOP/s against 7.31 for 17, one step ahead;
-      // 2 steps ahead, 8 K waves, or 128-deep steps measured lower).
-      static const int kOrder[] = {23, 5, 0, 6, 2, 24, 22, 21, 14, 15, 3, 25};
-      int best = -1;
-      int64_t best_tiles = 0;
-      for (int c : kOrder) {
-        if (!fits(c)) continue;
-        const GemmF32Config& g = gemm_f32_config(c);
-        const int64_t tiles = (int64_t)(M / g.bm) * (N / g.bn);
-        if (c == 24 && tiles > ds.cus) continue;
-        if (tiles >= ds.cus) {
-          cfg = c;
-          break;
+  if (g_force_cfg >= 0 && g_force_cfg < gemm_f32_num_configs() && fits(g_force_cfg)) {
+    cfg = g_force_cfg;
+  } else if (aligned && K > 0) {
+    // Measured on MI355X: 256x256x16 with 16 waves at 4096^3 (992 us; 256x256x32 with 8 waves
+    // 1012 us, the next in line); at 1024^3 the 64x64x64 tile with two
+    // waves per output block splitting K and global loads two K steps ahead (24.9 us) beats
+    // four K waves (25.6 us), two with one step ahead (26.1 us) and the plain 64x64x16 tile
+    // (29.6 us); at 256^3 the 32x32x64 tile with four K waves (64 workgroups, 3.5 us inside
+    // the kernel) beats every 64x64 tile (16 workgroups, 7 us).
+    // The 64x64 tile with four 32-deep K steps of loads ahead (24) only
+    // pays when there is one workgroup per CU at most (1024^3: 24.1-24.4 us
+    // against 24.6-25.0 for 22); with two per CU the other workgroup hides
+    // the loads and the deeper steps of 22 win (4096x512x4096: 163 vs 171 us).
+    // At 256^3 the 32x32x64 tile with four K waves loads all four K steps
+    // up front (25: 7.54-7.56 TFLOP/s against 7.31 for 17, one step ahead;
+    // 2 steps ahead, 8 K waves, or 128-deep steps measured lower).
+    // Each entry: the configuration for shapes the tile divides, and its
+    // edge-tile twin (partial tiles at the M, N, K edges) or -1.
+    static const int kOrder[][2] = {{23, 26}, {5, -1}, {0, -1}, {6, -1}, {2, 27}, {24, 28},
+                                    {22, 29}, {21, -1}, {14, -1}, {15, -1}, {3, -1}, {25, 30}};
+    int best = -1, first_rejected = -1;
+    int64_t best_tiles = 0;
+    for (const auto& e : kOrder) {
+      const int c = fits(e[0]) ? e[0] : (e[1] >= 0 && fits(e[1]) ? e[1] : -1);
+      if (c < 0) continue;
+      const GemmF32Config& g = gemm_f32_config(c);
+      const int64_t tiles = (int64_t)((M + g.bm - 1) / g.bm) * ((N + g.bn - 1) / g.bn);
+      if ((c == 24 || c == 28) && tiles > ds.cus) continue;
+      if (tiles >= ds.cus) {
+        // Tiles larger than 64x64 that need more than one round of
+        // workgroups are taken only when the last round keeps at least
+        // three quarters of the CUs busy (4097x4096: 272 tiles of 256x256
+        // would take two rounds of 4096^3-sized work).
+        const int64_t rounds = (tiles + ds.cus - 1) / ds.cus;
+        if (g.bm * g.bn > 64 * 64 && 4 * tiles < 3 * rounds * ds.cus) {
+          if (first_rejected < 0) first_rejected = c;
+          continue;
         }
-        if (tiles > best_tiles) {
-          best_tiles = tiles;
-          best = c;
-        }
+        cfg = c;
+        break;
       }
-      if (cfg < 0) cfg = best;
+      if (tiles > best_tiles) {
+        best_tiles = tiles;
+        best = c;
+      }
     }
+    if (cfg < 0) cfg = best >= 0 ? best : first_rejected;
   }
   if (cfg < 0) cfg = 4;  // guarded: any shape and alignment
   const GemmF32Config& g = gemm_f32_config(cfg);

@@ -1,0 +1,136 @@
+"""GPU parity for shapes that are not multiples of the tile.
+
+The fp32 tiles have edge variants (partial tiles at the M, N and K edges,
+16-byte vector loads at clamped addresses, masked stores) for 16-byte aligned
+operands whose K, N and row strides are multiples of 4; the small-M kernel
+spreads K over its wave slices in 16-row chunks, so K need only be a multiple
+of 16. Every case is checked against the oracle on the full output.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_f32_parity
+from mlir_edsl_hip import _native
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    assert torch.cuda.is_available()
+    return torch
+
+
+def _inputs(M, K, N, seed):
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.float32(np.sqrt(K))).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, N).astype(np.float32)
+    return X, W, b
+
+
+def _view(torch, a, pad=0, off=0):
+    """Device copy of `a` as a view with row pitch cols + pad, `off` elements in."""
+    rows, cols = a.shape
+    buf = torch.zeros(rows * (cols + pad) + off, dtype=torch.float32, device="cuda")
+    v = buf[off:].view(rows, cols + pad)[:, :cols]
+    v.copy_(torch.from_numpy(a))
+    return v
+
+
+def _run(torch, X, W, b, pad=0, off=0):
+    from mlir_edsl_hip.device import dense_launch
+    M, N = X.shape[0], W.shape[1]
+    tX, tW = _view(torch, X, pad, off), _view(torch, W, pad, off)
+    tb = torch.from_numpy(b).cuda()
+    tY = _view(torch, np.full((M, N), np.nan, dtype=np.float32), pad, off)
+    dense_launch(tX, tW, tb, tY, _native.EPI_BIAS_RELU)
+    torch.cuda.synchronize()
+    return tY.cpu().numpy(), _native.last_plan()
+
+
+EDGE_SHAPES = [(300, 100, 260), (257, 68, 132), (65, 20, 36), (33, 1000, 1028), (1, 4, 4)]
+
+
+def test_every_edge_config_on_odd_shapes(torch_cuda):
+    from mlir_edsl_hip.device import set_f32_config
+    names = _native.f32_config_names()
+    edge = [(c, n) for c, n in enumerate(names) if n.endswith("_edge")]
+    assert len(edge) >= 5
+    try:
+        for cfg, name in edge:
+            set_f32_config(cfg)
+            for i, (M, K, N) in enumerate(EDGE_SHAPES):
+                X, W, b = _inputs(M, K, N, 100 + i)
+                ref = oracle.dense_f32(X, W, b, "relu")
+                # contiguous, then a padded row pitch with an element offset
+                # (both keep 16-byte aligned rows)
+                for pad, off in ((0, 0), (8, 4)):
+                    got, plan = _run(torch_cuda, X, W, b, pad, off)
+                    assert name in plan, (name, plan)
+                    assert_f32_parity(got, ref, K)
+    finally:
+        set_f32_config(-1)
+
+
+@pytest.mark.parametrize("shape, tile", [
+    ((1000, 1000, 1000), "f32_64x64x32_w2x2_k2_pf4_edge"),
+    ((4000, 256, 4000), "f32_256x256x16_w4x4_edge"),
+    # 17 x 16 tiles of 256x256 would need two rounds of workgroups
+    ((4097, 256, 4096), "f32_128x128x16_w2x2_edge"),
+    # K = 1000 leaves a partial last K step on every tile
+    ((512, 1000, 512), "f32_32x32x64_w1x1_k4_pf4_edge"),
+], ids=["1000^3", "4000x256x4000", "4097x256x4096", "512x1000x512"])
+def test_auto_plan_takes_edge_tiles(shape, tile, torch_cuda):
+    M, K, N = shape
+    X, W, b = _inputs(M, K, N, M + K + N)
+    got, plan = _run(torch_cuda, X, W, b)
+    assert f"cfg={tile} " in plan, plan
+    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+
+
+def test_aligned_shapes_keep_their_tiles(torch_cuda):
+    """Shapes the tiles divide still take the unguarded configurations."""
+    for (M, K, N), tile in (((1024, 1024, 1024), "f32_64x64x32_w2x2_k2_pf4"),
+                            ((256, 256, 256), "f32_32x32x64_w1x1_k4_pf4")):
+        X, W, b = _inputs(M, K, N, 7)
+        got, plan = _run(torch_cuda, X, W, b)
+        assert f"cfg={tile} " in plan, plan
+        assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+
+
+def test_unaligned_k_takes_the_checked_tile(torch_cuda):
+    """K not a multiple of 4 leaves rows unaligned: the element-checked tile."""
+    X, W, b = _inputs(70, 37, 50, 9)
+    got, plan = _run(torch_cuda, X, W, b)
+    assert "guard" in plan, plan
+    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), 37)
+
+
+@pytest.mark.parametrize("M, K, N", [(16, 8000, 8192), (16, 8000, 1024), (3, 4112, 2048), (40, 1040, 512)])
+def test_small_m_uneven_k_slices(M, K, N, torch_cuda):
+    X, W, b = _inputs(M, K, N, M * 3 + K)
+    got, plan = _run(torch_cuda, X, W, b)
+    assert plan.startswith("gemv_f32"), plan
+    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+
+
+def test_small_m_forced_splits_on_uneven_k(torch_cuda):
+    from mlir_edsl_hip.device import set_gemv_cols, set_gemv_ksplit
+    M, K, N = 16, 8000, 1024
+    X, W, b = _inputs(M, K, N, 5)
+    ref = oracle.dense_f32(X, W, b, "relu")
+    try:
+        set_gemv_cols(128)
+        for ks in (1, 2, 3, 5, 16):
+            set_gemv_ksplit(ks)
+            got, plan = _run(torch_cuda, X, W, b)
+            assert f"ksplit={ks} cols=128" in plan, plan
+            assert_f32_parity(got, ref, K)
+    finally:
+        set_gemv_ksplit(0)
+        set_gemv_cols(0)
