@@ -13,20 +13,23 @@
 // equals the exact integer sum -- identical to the wrapping i32 sum in any
 // order. A pre-pass narrows X and W to int8 and writes them fragment-packed
 // (each 32x32 block stored as the 64 lanes x 16 bytes the MFMA consumes, W
-// transposed on the way), and flags any out-of-range value. The GEMM reads the
-// flag: if set, the whole grid takes the exact wrapping-i32 vector-ALU path on
-// the original i32 tensors instead. The flag is compared against a per-call
-// epoch, so it never needs clearing.
+// transposed on the way), and flags any out-of-range value. The packed copies
+// are padded with zeros to multiples of the 128-wide tile in M, N and K, so
+// any shape runs on the matrix cores; the GEMM stores only the real M x N.
+// The GEMM reads the flag: if set, the whole grid takes the exact
+// wrapping-i32 vector-ALU path on the original i32 tensors instead. The flag
+// is compared against a per-call epoch, so it never needs clearing.
 #include "common.hpp"
 #include "kernels.hpp"
+
+#include <type_traits>
 
 namespace edsl {
 namespace {
 
 // ------------------------------------------------------------------ pre-pass
-// Only used on the int8 path, where M, N and K are multiples of kI8Tile. The
-// i32 sources may have any alignment / row stride: `vec_ok` selects 16-byte
-// source loads.
+// Only used on the int8 path. The i32 sources may have any alignment / row
+// stride: `vec_ok` selects 16-byte source loads.
 constexpr int kNarrowTile = 64;
 
 __device__ __forceinline__ uint32_t pack_i8x4(i32x4 v, bool& bad) {
@@ -50,41 +53,66 @@ __device__ __forceinline__ int tile_packed_offset(int r, int k) {
   return ((((r >> 5) * 2 + (k >> 5)) * 64 + (r & 31) + 32 * ((k >> 4) & 1)) << 4) + (k & 15);
 }
 
-// Grid: 64x64 tiles of X, then 64x64 tiles of W. Thread t owns a 4x4 block of
-// the tile (4 row loads of 16 bytes), narrows it, and writes it into LDS in
-// packed order: for X each 16-byte row piece is already 4 consecutive k of one
-// row (one packed word); for W the 4x4 block is transposed in registers so each
-// word holds 4 consecutive k of one column. The packed tile then leaves with
-// one 16-byte store per thread (four 1 KB fragments).
+// Grid: 64x64 tiles of the padded X (Mp x Kp), then of the padded W (Kp x Np).
+// Thread t owns a 4x4 block of the tile (4 row loads of 16 bytes), narrows it,
+// and writes it into LDS in packed order: for X each 16-byte row piece is
+// already 4 consecutive k of one row (one packed word); for W the 4x4 block is
+// transposed in registers so each word holds 4 consecutive k of one column.
+// The packed tile then leaves with one 16-byte store per thread (four 1 KB
+// fragments). Tiles that reach past the real M, N or K load element by element
+// and write zeros there.
 __global__ void __launch_bounds__(256) narrow_i8_kernel(NarrowI8Args a, int vec_ok_x, int vec_ok_w) {
   __shared__ uint32_t pk[kNarrowTile * kNarrowTile / 4];
   const int tid = threadIdx.x;
   const int bi = tid >> 4;        // 4-row block along the source's rows
   const int bj = 4 * (tid & 15);  // 4-column block along the source's columns
-  const int x_tiles_k = a.K / kNarrowTile;
-  const int x_tiles = (a.M / kNarrowTile) * x_tiles_k;
+  const int x_tiles_k = a.Kp / kNarrowTile;
+  const int x_tiles = (a.Mp / kNarrowTile) * x_tiles_k;
   bool bad = false;
   int r0, k0;  // tile origin in the packed matrix's (row, k) coordinates
   int8_t* dst;
+  // 4 consecutive elements of row `row` from column `col` of a source with
+  // `rows` x `cols` elements; zeros past either edge.
+  auto load_edge = [](const int32_t* src, int64_t ld, int rows, int cols, int row, int col) {
+    i32x4 v = {0, 0, 0, 0};
+    if (row < rows) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (col + e < cols) v[e] = src[(int64_t)row * ld + col + e];
+    }
+    return v;
+  };
   if ((int)blockIdx.x < x_tiles) {
     r0 = (blockIdx.x / x_tiles_k) * kNarrowTile;
     k0 = (blockIdx.x % x_tiles_k) * kNarrowTile;
     dst = a.X8p;
     i32x4 v[4];
+    if (r0 + kNarrowTile <= a.M && k0 + kNarrowTile <= a.K) {  // uniform per workgroup
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = load4(a.X + (int64_t)(r0 + 4 * bi + i) * a.ldx + k0 + bj, vec_ok_x);
+      for (int i = 0; i < 4; ++i) v[i] = load4(a.X + (int64_t)(r0 + 4 * bi + i) * a.ldx + k0 + bj, vec_ok_x);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = load_edge(a.X, a.ldx, a.M, a.K, r0 + 4 * bi + i, k0 + bj);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) pk[tile_packed_offset(4 * bi + i, bj) >> 2] = pack_i8x4(v[i], bad);
   } else {
     const int b = blockIdx.x - x_tiles;
-    const int w_tiles_n = a.N / kNarrowTile;
+    const int w_tiles_n = a.Np / kNarrowTile;
     k0 = (b / w_tiles_n) * kNarrowTile;
     r0 = (b % w_tiles_n) * kNarrowTile;  // packed rows are W's columns
     dst = a.W8p;
+    i32x4 v[4];
+    if (k0 + kNarrowTile <= a.K && r0 + kNarrowTile <= a.N) {  // uniform per workgroup
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = load4(a.W + (int64_t)(k0 + 4 * bi + i) * a.ldw + r0 + bj, vec_ok_w);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = load_edge(a.W, a.ldw, a.K, a.N, k0 + 4 * bi + i, r0 + bj);
+    }
     uint32_t q[4];  // q[i] = W row k0 + 4bi + i, columns r0 + bj .. + 3 (byte e = column e)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      q[i] = pack_i8x4(load4(a.W + (int64_t)(k0 + 4 * bi + i) * a.ldw + r0 + bj, vec_ok_w), bad);
+    for (int i = 0; i < 4; ++i) q[i] = pack_i8x4(v[i], bad);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       // column r0 + bj + e, rows k0 + 4bi .. + 3 as one word (byte i = row i)
@@ -98,7 +126,7 @@ __global__ void __launch_bounds__(256) narrow_i8_kernel(NarrowI8Args a, int vec_
   const int frag = tid >> 6, lane = tid & 63;
   const int rb = (r0 >> 5) + (frag >> 1), kt = (k0 >> 5) + (frag & 1);
   const i32x4 out = reinterpret_cast<const i32x4*>(pk)[tid];
-  *reinterpret_cast<i32x4*>(dst + ((((int64_t)rb * (a.K >> 5) + kt) * 64 + lane) << 4)) = out;
+  *reinterpret_cast<i32x4*>(dst + ((((int64_t)rb * (a.Kp >> 5) + kt) * 64 + lane) << 4)) = out;
   if (__any(bad) && (tid & 63) == 0) *a.flag = a.epoch;
 }
 
@@ -199,7 +227,7 @@ __global__ void __launch_bounds__(256) gemm_i8_kernel(GemmI32Args a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  const int KT = a.K >> 5;  // 32-k steps; a multiple of D
+  const int KT = a.Kp >> 5;  // 32-k steps of the padded K; a multiple of D
   const i32x4* ap[2];
   const i32x4* bp[2];
 #pragma unroll
@@ -254,19 +282,28 @@ __global__ void __launch_bounds__(256) gemm_i8_kernel(GemmI32Args a) {
   // Epilogue: lane holds rows 8*(r/4) + 4*half + r%4 and column l32 of each
   // block; each store instruction writes two full 128-byte row segments.
   // Non-temporal: the result is not re-read by this kernel.
+  // Rows and columns past the real M and N (padding) are not stored; tiles
+  // that lie inside take the unchecked copy of the loop.
   const int half = lane >> 5, l32 = lane & 31;
+  auto store_tile = [&](auto checked) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + 64 * wn + 32 * j + l32;
-    const int32_t b = epi_has_bias(EPI) ? a.bias[n] : 0;
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + 64 * wn + 32 * j + l32;
+      const int32_t b = epi_has_bias(EPI) && (!checked || n < a.N) ? a.bias[n] : 0;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * half + (r & 3);
-        __builtin_nontemporal_store(apply_epilogue_i32<EPI>(acc[i][j][r], b), a.C + (int64_t)m * a.ldc + n);
-      }
-  }
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * half + (r & 3);
+          if (!checked || (m < a.M && n < a.N))
+            __builtin_nontemporal_store(apply_epilogue_i32<EPI>(acc[i][j][r], b), a.C + (int64_t)m * a.ldc + n);
+        }
+    }
+  };
+  if (m0 + kI8Tile <= a.M && n0 + kI8Tile <= a.N)
+    store_tile(std::false_type{});
+  else
+    store_tile(std::true_type{});
 }
 
 // K-split waves: every wave computes the whole 128x128 tile (4x4 blocks of
@@ -297,7 +334,7 @@ gemm_i8_ksplit_kernel(GemmI32Args a) {
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int KT = a.K >> 5;  // 32-k steps, a multiple of 4
+  const int KT = a.Kp >> 5;  // 32-k steps of the padded K, a multiple of 4
   const int NS = KT >> 2;   // steps per wave, a multiple of D
   const i32x4* ap = reinterpret_cast<const i32x4*>(a.A8p) + (int64_t)(m0 >> 5) * KT * 64 + lane;
   const i32x4* bp = reinterpret_cast<const i32x4*>(a.B8p) + (int64_t)(n0 >> 5) * KT * 64 + lane;
@@ -351,38 +388,47 @@ gemm_i8_ksplit_kernel(GemmI32Args a) {
   // instruction writes two full 128-byte row segments.
   const int half = lane >> 5, l32 = lane & 31;
   auto slot = [&](int p, int ii, int j, int q) { return (((p * 2 + ii) * 4 + j) * 4 + q) * 64 + lane; };
+  // Rows and columns past the real M and N (padding) are not stored; tiles
+  // that lie inside take the unchecked copy of the epilogue.
+  auto epilogue = [&](auto checked) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    if (h == 1) __syncthreads();  // round 0's reads are done before round 1 overwrites
+    for (int h = 0; h < 2; ++h) {
+      if (h == 1) __syncthreads();  // round 0's reads are done before round 1 overwrites
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii)
+      for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const i32x16& v = acc[2 * h + ii][j];
+            red[slot(wave, ii, j, q)] = i32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+          }
+      __syncthreads();
+      const int ii = wave >> 1;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * (wave & 1) + jj;
+        const int n = n0 + 32 * j + l32;
+        const int32_t b = epi_has_bias(EPI) && (!checked || n < a.N) ? a.bias[n] : 0;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const i32x16& v = acc[2 * h + ii][j];
-          red[slot(wave, ii, j, q)] = i32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-        }
-    __syncthreads();
-    const int ii = wave >> 1;
+          i32x4 sum = red[slot(0, ii, j, q)];
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int j = 2 * (wave & 1) + jj;
-      const int n = n0 + 32 * j + l32;
-      const int32_t b = epi_has_bias(EPI) ? a.bias[n] : 0;
+          for (int p = 1; p < 4; ++p) sum += red[slot(p, ii, j, q)];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        i32x4 sum = red[slot(0, ii, j, q)];
-#pragma unroll
-        for (int p = 1; p < 4; ++p) sum += red[slot(p, ii, j, q)];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int m = m0 + 32 * (2 * h + ii) + 8 * q + 4 * half + e;
-          __builtin_nontemporal_store(apply_epilogue_i32<EPI>(sum[e], b), a.C + (int64_t)m * a.ldc + n);
+          for (int e = 0; e < 4; ++e) {
+            const int m = m0 + 32 * (2 * h + ii) + 8 * q + 4 * half + e;
+            if (!checked || (m < a.M && n < a.N))
+              __builtin_nontemporal_store(apply_epilogue_i32<EPI>(sum[e], b), a.C + (int64_t)m * a.ldc + n);
+          }
         }
       }
     }
-  }
+  };
+  if (m0 + kI8Tile <= a.M && n0 + kI8Tile <= a.N)
+    epilogue(std::false_type{});
+  else
+    epilogue(std::true_type{});
 }
 
 #define EDSL_I32_EPI_SWITCH(KERNEL, GRID, ARGS)                                        \
@@ -440,9 +486,10 @@ constexpr I8Variant kI8Table[kI8Variants] = {
 }  // namespace
 
 hipError_t launch_narrow_i8(NarrowI8Args a, hipStream_t stream) {
-  if (a.M % kNarrowTile || a.N % kNarrowTile || a.K % kNarrowTile) return hipErrorInvalidValue;
-  const int x_tiles = (a.M / kNarrowTile) * (a.K / kNarrowTile);
-  const int w_tiles = (a.K / kNarrowTile) * (a.N / kNarrowTile);
+  if (a.Mp % kI8Tile || a.Np % kI8Tile || a.Kp % kI8Tile || a.M > a.Mp || a.N > a.Np || a.K > a.Kp)
+    return hipErrorInvalidValue;
+  const int x_tiles = (a.Mp / kNarrowTile) * (a.Kp / kNarrowTile);
+  const int w_tiles = (a.Kp / kNarrowTile) * (a.Np / kNarrowTile);
   const int vec_x = ((reinterpret_cast<uintptr_t>(a.X) & 15) == 0) && (a.ldx % 4 == 0);
   const int vec_w = ((reinterpret_cast<uintptr_t>(a.W) & 15) == 0) && (a.ldw % 4 == 0);
   hipLaunchKernelGGL(narrow_i8_kernel, dim3(x_tiles + w_tiles), dim3(256), 0, stream, a, vec_x, vec_w);
@@ -452,7 +499,7 @@ hipError_t launch_narrow_i8(NarrowI8Args a, hipStream_t stream) {
 int gemm_i8_depth(int variant, int K) {
   if (variant < 0 || variant >= kI8Variants) variant = kI8DefaultVariant;
   const I8Variant& v = kI8Table[variant];
-  const int steps = v.ksplit ? K / 128 : K / 32;  // K % 128 == 0 on this path
+  const int steps = v.ksplit ? K / 128 : K / 32;  // K: the padded K, a multiple of 128
   for (int d : v.depth)
     if (steps % d == 0) return d;
   return 1;
@@ -464,10 +511,10 @@ bool gemm_i8_ksplit(int variant) {
 }
 
 hipError_t launch_gemm_i8(int epi, GemmI32Args a, hipStream_t stream, int variant) {
-  if (a.M % kI8Tile || a.N % kI8Tile || a.K % kI8Tile || a.K <= 0) return hipErrorInvalidValue;
-  a.tiles_m = a.M / kI8Tile;
-  a.tiles_n = a.N / kI8Tile;
-  const int d = gemm_i8_depth(variant, a.K);
+  if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.Kp % kI8Tile || a.Kp < a.K) return hipErrorInvalidValue;
+  a.tiles_m = (a.M + kI8Tile - 1) / kI8Tile;
+  a.tiles_n = (a.N + kI8Tile - 1) / kI8Tile;
+  const int d = gemm_i8_depth(variant, a.Kp);
   if (gemm_i8_ksplit(variant)) {
     switch (d) {
       case 1: return launch_i8_depth<true, 1>(epi, a, stream);

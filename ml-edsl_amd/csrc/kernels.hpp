@@ -65,13 +65,16 @@ constexpr int kGemvMaxM = 64;
 // [R/32][K/32]; fragment (rb, kt) holds rows 32rb.. and k 32kt.. as 64 lanes x
 // 16 bytes with lane = r % 32 + 32 * ((k % 32) / 16) and byte = k % 16 -- the
 // v_mfma_i32_32x32x32_i8 operand of that block, one 16-byte load per lane.
+// The packed copies cover M, N, K rounded up to multiples of kI8Tile (Mp, Np,
+// Kp); elements past the real M, N or K are zero, so they add nothing.
 struct NarrowI8Args {
   const int32_t* X;   // [M][K], ldx
   const int32_t* W;   // [K][N], ldw
-  int8_t* X8p;        // X narrowed, fragment-packed over (M, K)
-  int8_t* W8p;        // W narrowed, fragment-packed over (N, K) (W transposed)
+  int8_t* X8p;        // X narrowed, fragment-packed over (Mp, Kp)
+  int8_t* W8p;        // W narrowed, fragment-packed over (Np, Kp) (W transposed)
   int64_t ldx, ldw;
-  int M, N, K;
+  int M, N, K;        // real sizes
+  int Mp, Np, Kp;     // padded sizes (multiples of kI8Tile)
   unsigned* flag;     // set to `epoch` when a value lies outside [-128, 127]
   unsigned epoch;
 };
@@ -85,12 +88,13 @@ struct GemmI32Args {
   int32_t* C;         // [M][N], ldc
   int64_t ldx, ldw, ldc;
   int M, N, K;
+  int Kp;             // K of the packed copies (int8 path; a multiple of kI8Tile)
   int tiles_m, tiles_n;
   const unsigned* flag;  // fast path only when *flag != epoch
   unsigned epoch;
 };
 
-constexpr int kI8Tile = 128;   // M, N, K multiples of this for the int8 MFMA path
+constexpr int kI8Tile = 128;   // tile of the int8 MFMA path; packed copies are padded to it
 hipError_t launch_narrow_i8(NarrowI8Args args, hipStream_t stream);
 // variant = wave layout + fragment prefetch depth in 32-k steps:
 //   0..2: 2x2 waves of 64x64 quadrants, depth 4, 2, 8 (8 needs K % 256 == 0,

@@ -451,10 +451,16 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
   a.M = (int)L.M;
   a.N = (int)L.N;
   a.K = (int)L.K;
-  const bool tiled = a.M % kI8Tile == 0 && a.N % kI8Tile == 0 && a.K % kI8Tile == 0 && a.K > 0 &&
-                     a.K < (1 << 17);
+  // The int8 path is exact for K < 2^17 (each product of int8 values has
+  // magnitude <= 2^14, so no i32 partial sum can overflow). Its packed copies
+  // are padded with zeros to multiples of the 128-wide tile, so any M, N and
+  // K run on it; only the stores are limited to the real M x N.
+  const bool tiled = a.M > 0 && a.N > 0 && a.K > 0 && a.K < (1 << 17);
   if (tiled) {
-    const size_t xs = (size_t)a.M * a.K, ws = (size_t)a.N * a.K;
+    auto pad = [](int v) { return (v + kI8Tile - 1) / kI8Tile * kI8Tile; };
+    const int Mp = pad(a.M), Np = pad(a.N), Kp = pad(a.K);
+    a.Kp = Kp;
+    const size_t xs = (size_t)Mp * Kp, ws = (size_t)Np * Kp;
     int8_t* x8 = static_cast<int8_t*>(ds.i8_x.ensure(xs, false));
     int8_t* w8 = static_cast<int8_t*>(ds.i8_w.ensure(ws, false));
     unsigned* flag = static_cast<unsigned*>(ds.i8_flag.ensure(sizeof(unsigned), true));
@@ -469,6 +475,9 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     n.M = a.M;
     n.N = a.N;
     n.K = a.K;
+    n.Mp = Mp;
+    n.Np = Np;
+    n.Kp = Kp;
     n.flag = flag;
     n.epoch = ds.epoch;
     scratch_begin(ds, stream);
@@ -481,8 +490,8 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     check_hip(launch_gemm_i8(L.epi, a, stream, variant), "gemm_i8 launch");
     scratch_end(ds, stream);
     set_plan("narrow_i8+gemm_i8 variant=%d waves=%s depth=%d grid=%d", variant,
-             gemm_i8_ksplit(variant) ? "ksplit" : "quadrant", gemm_i8_depth(variant, a.K),
-             (a.M / kI8Tile) * (a.N / kI8Tile));
+             gemm_i8_ksplit(variant) ? "ksplit" : "quadrant", gemm_i8_depth(variant, Kp),
+             (Mp / kI8Tile) * (Np / kI8Tile));
   } else {
     check_hip(launch_gemm_i32_valu(L.epi, a, stream), "gemm_i32_valu launch");
     set_plan("gemm_i32_valu grid=%d", ((a.M + 127) / 128) * ((a.N + 127) / 128));

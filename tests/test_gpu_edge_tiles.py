@@ -134,3 +134,67 @@ def test_small_m_forced_splits_on_uneven_k(torch_cuda):
     finally:
         set_gemv_ksplit(0)
         set_gemv_cols(0)
+
+
+# ------------------------------------------------------------ integer path
+# The int8 path pads its packed copies with zeros to multiples of 128 in M, N
+# and K, so every shape runs on the matrix cores; results must equal the exact
+# wrapping i32 sums.
+def _exact_i32(X, W, b):
+    y = X.astype(np.int64) @ W.astype(np.int64) + b.astype(np.int64)
+    y = (y + 2**31) % 2**32 - 2**31
+    return np.maximum(y, 0).astype(np.int32)
+
+
+@pytest.mark.parametrize("M, K, N", [(1, 1, 1), (130, 129, 131), (257, 300, 129), (1000, 1000, 1000),
+                                     (2000, 2000, 200)])
+def test_int8_path_on_odd_shapes(M, K, N, torch_cuda):
+    from mlir_edsl_hip.device import dense_launch, set_i8_variant
+    rng = np.random.default_rng(M + 3 * K + 7 * N)
+    X = rng.integers(-128, 128, size=(M, K), dtype=np.int32)
+    W = rng.integers(-128, 128, size=(K, N), dtype=np.int32)
+    b = rng.integers(-2**20, 2**20, size=(N,), dtype=np.int32)
+    exp = _exact_i32(X, W, b)
+    tX, tW, tb = (torch_cuda.from_numpy(a).cuda() for a in (X, W, b))
+    n = _native.lib().edsl_hip_i8_variant_count()
+    try:
+        for v in range(n):
+            set_i8_variant(v)
+            tY = torch_cuda.full((M, N), -7, dtype=torch_cuda.int32, device="cuda")
+            dense_launch(tX, tW, tb, tY, _native.EPI_BIAS_RELU)
+            torch_cuda.cuda.synchronize()
+            plan = _native.last_plan()
+            assert plan.startswith(f"narrow_i8+gemm_i8 variant={v}"), plan
+            assert np.array_equal(tY.cpu().numpy(), exp), plan
+    finally:
+        set_i8_variant(-1)
+    if M * K * N <= 10**7:
+        assert np.array_equal(tY.cpu().numpy(), oracle.dense_i32(X, W, b, "relu"))
+
+
+def test_int8_path_odd_shapes_strided_and_out_of_range(torch_cuda):
+    """Padded, offset device views (the narrowing pass's unaligned loads on
+    edge tiles), then a value outside int8 (the exact i32 fallback on the
+    original tensors), then in range again."""
+    from mlir_edsl_hip.device import dense_launch
+    M, K, N = 300, 250, 190
+    rng = np.random.default_rng(21)
+    X = rng.integers(-128, 128, size=(M, K), dtype=np.int32)
+    W = rng.integers(-128, 128, size=(K, N), dtype=np.int32)
+    b = rng.integers(-1000, 1000, size=(N,), dtype=np.int32)
+
+    def view(a, pad, off):
+        rows, cols = a.shape
+        buf = torch_cuda.zeros(rows * (cols + pad) + off, dtype=torch_cuda.int32, device="cuda")
+        v = buf[off:].view(rows, cols + pad)[:, :cols]
+        v.copy_(torch_cuda.from_numpy(a))
+        return v
+
+    for Xc, path in ((X, "narrow_i8+gemm_i8"), (np.where(np.arange(K) == 17, 5000, X).astype(np.int32),
+                                                 "narrow_i8+gemm_i8"), (X, "narrow_i8+gemm_i8")):
+        tX, tW = view(Xc, 3, 1), view(W, 5, 2)
+        tY = view(np.full((M, N), -7, dtype=np.int32), 2, 3)
+        dense_launch(tX, tW, torch_cuda.from_numpy(b).cuda(), tY, _native.EPI_BIAS_RELU)
+        torch_cuda.cuda.synchronize()
+        assert _native.last_plan().startswith(path)
+        assert np.array_equal(tY.cpu().numpy(), _exact_i32(Xc, W, b))

@@ -300,12 +300,14 @@ def test_int8_depth_fallback_and_strided_sources(K, torch_cuda):
         set_i8_variant(-1)
 
 
-@pytest.mark.parametrize("K, path", [(2**17 - 128, "narrow_i8+gemm_i8"), (2**17, "gemm_i32_valu")])
+@pytest.mark.parametrize("K, path", [(2**17 - 128, "narrow_i8+gemm_i8"), (2**17 - 1, "narrow_i8+gemm_i8"),
+                                     (2**17, "gemm_i32_valu")])
 def test_int8_exactness_boundary(K, path, torch_cuda):
     """Every product is (-128)(-128) = 16384, so every output is 16384*K,
-    exact in i32 up to K = 2^17 - 128 (the int8 path runs) and 2^31 at
-    K = 2^17, which wraps to -2^31 (arith.addi semantics; the exact i32 path
-    runs, as it does for every K >= 2^17). ReLU of the wrapped value is 0."""
+    exact in i32 up to K = 2^17 - 1 (the int8 path runs; K = 2^17 - 1 also
+    pads the packed K to 2^17 with zeros) and 2^31 at K = 2^17, which wraps
+    to -2^31 (arith.addi semantics; the exact i32 path runs, as it does for
+    every K >= 2^17). ReLU of the wrapped value is 0."""
     import torch
     from mlir_edsl_hip.device import dense_launch
     M = N = 128
