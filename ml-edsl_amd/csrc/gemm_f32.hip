@@ -76,10 +76,11 @@ __device__ __forceinline__ void static_for(F&& f) {
 //  kGuardEdge: partial tiles at the M, N and K edges; operands 16-byte aligned
 //    with row strides, N and K multiples of 4. Loads stay 16-byte vectors at
 //    clamped addresses: A rows past M read row M-1 and B columns past N read
-//    columns N-4.., which only feed outputs that are never stored; k past K
-//    reads k K-4.. (A) or row K-1 (B) and is then zeroed, since it feeds valid
-//    outputs. Stores are masked per vector (N % 4 == 0, so a vector of CP <= 4
-//    columns is all in or all out).
+//    columns N-4.., which only feed outputs that are never stored (the clamps
+//    are loop-invariant). The K loop runs the whole BK steps; a partial last
+//    step follows it once, with loads past K skipped and zero. Stores are
+//    masked per vector (N % 4 == 0, so a vector of CP <= 4 columns is all in
+//    or all out).
 //  kGuardAll: any shape and alignment; element-wise checked scalar loads/stores.
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int WAVES_K, int PF, int EPI, int GUARD>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64)
@@ -121,8 +122,10 @@ gemm_f32_kernel(GemmF32Args args) {
   f32x4 ra[PF][A_LD];
   f32x4 rb[PF][B_LD];
 
-  // Register set S receives the global tile loads of one K step.
-  auto load_global = [&](auto set, int k0) {
+  // Register set S receives the global tile loads of one K step. With the
+  // edge guard the K loop runs whole steps only (`tail` false: no check in
+  // k); a partial last step is loaded once, after the loop, with `tail` true.
+  auto load_global = [&](auto set, int k0, auto tail) {
     constexpr int S = decltype(set)::value;
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
@@ -134,9 +137,14 @@ gemm_f32_kernel(GemmF32Args args) {
       if constexpr (GUARD == kGuardNone) {
         ra[S][i] = *reinterpret_cast<const f32x4*>(args.A + (int64_t)gm * args.lda + gk);
       } else if constexpr (GUARD == kGuardEdge) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(args.A + (int64_t)min(gm, M - 1) * args.lda +
-                                                        min(gk, K - 4));
-        ra[S][i] = gk < K ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const float* src = args.A + (int64_t)min(gm, M - 1) * args.lda + gk;
+        if constexpr (decltype(tail)::value) {
+          f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+          if (gk < K) v = *reinterpret_cast<const f32x4*>(src);
+          ra[S][i] = v;
+        } else {
+          ra[S][i] = *reinterpret_cast<const f32x4*>(src);
+        }
       } else {
         f32x4 v;
 #pragma unroll
@@ -155,9 +163,14 @@ gemm_f32_kernel(GemmF32Args args) {
       if constexpr (GUARD == kGuardNone) {
         rb[S][i] = *reinterpret_cast<const f32x4*>(args.B + (int64_t)gk * args.ldb + gn);
       } else if constexpr (GUARD == kGuardEdge) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(args.B + (int64_t)min(gk, K - 1) * args.ldb +
-                                                        min(gn, N - 4));
-        rb[S][i] = gk < K ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const float* src = args.B + (int64_t)gk * args.ldb + min(gn, N - 4);
+        if constexpr (decltype(tail)::value) {
+          f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+          if (gk < K) v = *reinterpret_cast<const f32x4*>(src);
+          rb[S][i] = v;
+        } else {
+          rb[S][i] = *reinterpret_cast<const f32x4*>(src);
+        }
       } else {
         f32x4 v;
 #pragma unroll
@@ -222,16 +235,19 @@ gemm_f32_kernel(GemmF32Args args) {
     }
   };
 
-  const int nk = (K + BK - 1) / BK;
+  // K steps of the main loop: all of them, or with the edge guard the whole
+  // ones only (the partial step follows the loop).
+  const int nk = GUARD == kGuardEdge ? K / BK : (K + BK - 1) / BK;
+  const std::false_type body{};
   if constexpr (PF == 1) {
     if (nk > 0) {
-      load_global(Ic<0>{}, 0);
+      load_global(Ic<0>{}, 0, body);
       store_lds(Ic<0>{}, 0);
       __syncthreads();
       for (int kt = 0; kt < nk; ++kt) {
         const int buf = kt & 1;
         const bool more = kt + 1 < nk;
-        if (more) load_global(Ic<0>{}, (kt + 1) * BK);
+        if (more) load_global(Ic<0>{}, (kt + 1) * BK, body);
         compute(buf);
         if (more) store_lds(Ic<0>{}, buf ^ 1);
         __syncthreads();
@@ -248,14 +264,14 @@ gemm_f32_kernel(GemmF32Args args) {
     // so the body has no branch and its wait counts stay exact.
     auto prologue = [&](auto set) {
       constexpr int S = decltype(set)::value;
-      load_global(Ic<S>{}, min(S, nk - 1) * BK);
+      load_global(Ic<S>{}, min(S, nk - 1) * BK, body);
     };
     static_for<PF>(prologue);
     store_lds(Ic<0>{}, 0);
     __syncthreads();
     auto step = [&](auto cur, int kt) {
       constexpr int C = decltype(cur)::value;
-      load_global(Ic<C>{}, min(kt + PF, nk - 1) * BK);
+      load_global(Ic<C>{}, min(kt + PF, nk - 1) * BK, body);
       // Keep the loads ahead of this step's MFMAs (the scheduler would
       // otherwise sink them and shorten their lead).
       __builtin_amdgcn_sched_barrier(0);
@@ -293,6 +309,17 @@ gemm_f32_kernel(GemmF32Args args) {
       static_for<PF>([&](auto s) {
         if (kt + decltype(s)::value < nk) step(s, kt + decltype(s)::value);
       });
+    }
+  }
+  if constexpr (GUARD == kGuardEdge) {
+    // The partial last K step (K % BK != 0), zero past K. Every path above
+    // ended with a barrier, so LDS buffer nk & 1 is free.
+    if (nk * BK < K) {
+      load_global(Ic<0>{}, nk * BK, std::true_type{});
+      store_lds(Ic<0>{}, nk & 1);
+      __syncthreads();
+      compute(nk & 1);
+      __syncthreads();
     }
   }
 
