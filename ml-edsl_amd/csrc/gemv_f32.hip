@@ -70,7 +70,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
   const int wave = threadIdx.x >> 6;
   const int wn = wave % WN;
   const int wk = wave / WN;
-  const int groups = a.N / kGroupCols;
+  const int groups = (a.N + kGroupCols - 1) / kGroupCols;  // the last may be partial
   const int g = blockIdx.x % groups;
   const int split = blockIdx.x / groups;
   const int n0 = g * kGroupCols + kWaveCols * wn;
@@ -92,7 +92,10 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
     for (int c = 0; c < CPL; ++c) acc[mb][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int64_t ldw = a.ldw;
-  const float* wbase = a.W + (int64_t)(kbeg + 4 * lg) * ldw + n0 + CPL * li;
+  // Lanes whose columns lie past N (a partial last column block) read the
+  // last CPL columns instead; their results are never stored. N % 4 == 0, so
+  // a lane's CPL columns are all in or all out.
+  const float* wbase = a.W + (int64_t)(kbeg + 4 * lg) * ldw + min(n0 + CPL * li, a.N - CPL);
   // Rows of X past M read row 0 instead: MFMA output row i depends only on
   // A row i, and those output rows are never stored.
   const float* xp[MB];
@@ -211,6 +214,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
 
   // Lane holds rows 16*mb + 4*lg + r and columns n0 + CPL*li + c.
   const int col = n0 + CPL * li;
+  if (col >= a.N) return;
   if (a.ksplit == 1) {
     vec bv;
 #pragma unroll
@@ -273,7 +277,7 @@ __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi
 
 template <int MB>
 hipError_t launch_mb(int cols, int epi, const GemvF32Args& a, hipStream_t stream) {
-  const dim3 grid((a.N / cols) * a.ksplit);
+  const dim3 grid(((a.N + cols - 1) / cols) * a.ksplit);
   const dim3 block(kWavesPerWG * 64);
   switch (cols) {
     case 32: hipLaunchKernelGGL((gemv_f32_kernel<MB, 2, 1>), grid, block, 0, stream, a, epi); break;

@@ -299,11 +299,12 @@ bool plan_gemv(const DeviceState& ds, int64_t N, int64_t K, int* cols_out, int* 
   for (int cols : kCols) {
     if (g_force_cols > 0 && cols != g_force_cols) continue;
     const int64_t wk = gemv_f32_waves_k(cols);
-    // K is walked in 16-row chunks spread evenly over the ks x wk wave
-    // slices; the automatic plan gives every slice at least two, a forced
-    // split at least one.
-    if (N % cols != 0 || K % 16 != 0) continue;
-    const int64_t groups = N / cols;
+    // The last column block may be partial (its lanes past N read the last
+    // columns and store nothing), which needs N % 4 == 0. K is walked in
+    // 16-row chunks spread evenly over the ks x wk wave slices; the automatic
+    // plan gives every slice at least two, a forced split at least one.
+    if (N % 4 != 0 || N < 4 || K % 16 != 0) continue;
+    const int64_t groups = (N + cols - 1) / cols;
     int ks = 1;
     if (g_force_ksplit > 0) {
       // A forced split is taken only by widths that can honour it.
@@ -357,7 +358,7 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     check_hip(launch_gemv_f32(L.epi, gemv_cols, a, stream), "gemv_f32 launch");
     if (a.ksplit > 1) scratch_end(ds, stream);
     set_plan("gemv_f32 mb=%d ksplit=%d cols=%d grid=%d%s", mb, a.ksplit, gemv_cols,
-             (N / gemv_cols) * a.ksplit, a.ksplit > 1 ? " +reduce" : "");
+             ((N + gemv_cols - 1) / gemv_cols) * a.ksplit, a.ksplit > 1 ? " +reduce" : "");
     return;
   }
 

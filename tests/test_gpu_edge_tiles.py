@@ -4,7 +4,8 @@ The fp32 tiles have edge variants (partial tiles at the M, N and K edges,
 16-byte vector loads at clamped addresses, masked stores) for 16-byte aligned
 operands whose K, N and row strides are multiples of 4; the small-M kernel
 spreads K over its wave slices in 16-row chunks, so K need only be a multiple
-of 16. Every case is checked against the oracle on the full output.
+of 16, and its last column block may be partial, so N need only be a multiple
+of 4. Every case is checked against the oracle on the full output.
 """
 from __future__ import annotations
 
@@ -131,6 +132,35 @@ def test_small_m_forced_splits_on_uneven_k(torch_cuda):
             got, plan = _run(torch_cuda, X, W, b)
             assert f"ksplit={ks} cols=128" in plan, plan
             assert_f32_parity(got, ref, K)
+    finally:
+        set_gemv_ksplit(0)
+        set_gemv_cols(0)
+
+
+@pytest.mark.parametrize("M, K, N", [(16, 4096, 50256), (16, 8192, 8100), (8, 4096, 4100), (1, 4096, 1000),
+                                     (33, 1040, 36), (64, 2048, 4)])
+def test_small_m_partial_column_blocks(M, K, N, torch_cuda):
+    """N a multiple of 4 but not of the column block: the last block is
+    partial (its lanes read the last columns and store nothing)."""
+    X, W, b = _inputs(M, K, N, M + K + N)
+    got, plan = _run(torch_cuda, X, W, b)
+    assert plan.startswith("gemv_f32"), plan
+    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+
+
+def test_small_m_every_width_on_a_partial_block(torch_cuda):
+    from mlir_edsl_hip.device import set_gemv_cols, set_gemv_ksplit
+    M, K, N = 16, 8000, 1000
+    X, W, b = _inputs(M, K, N, 11)
+    ref = oracle.dense_f32(X, W, b, "relu")
+    try:
+        for cols in (32, 64, 128, 256):
+            for ks in (1, 3):
+                set_gemv_cols(cols)
+                set_gemv_ksplit(ks)
+                got, plan = _run(torch_cuda, X, W, b, 8, 4)
+                assert f"ksplit={ks} cols={cols}" in plan, plan
+                assert_f32_parity(got, ref, K)
     finally:
         set_gemv_ksplit(0)
         set_gemv_cols(0)
