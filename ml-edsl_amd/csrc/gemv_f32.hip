@@ -29,7 +29,7 @@
 //    in flight at any moment are spread over the matrix and over the HBM
 //    channels instead of every wave hitting the same few rows.
 //  * W registers are reloaded one at a time right after the MFMAs that read
-//    them, so a wave's loads stay in flight while it computes (at M <= 32).
+//    them, so a wave's loads stay in flight while it computes.
 //    A wave that drained its loads before every batch of MFMAs streamed
 //    ~1.5 us slower at M=16, K=N=8192 (~42.7 vs ~41.2 us for the main kernel).
 // The summation order is fixed by the shape and the configuration, so
@@ -131,28 +131,19 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
         acc[mb][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(xu[mb][s], wq[c], acc[mb][c], 0, 0, 0);
   };
 
-  // Main iterations of kU steps, walked from a hashed start. For one or two
-  // row blocks the loads are a rotating pipeline: as soon as the MFMAs of W
-  // register q have been issued, q is reloaded with the next iteration's row,
-  // so every wave keeps its 4*kU W loads in flight while it computes instead
-  // of draining them before each iteration. (The scheduling barrier keeps the
-  // compiler from sinking the reloads to the end of the iteration.) Three or
-  // four row blocks do 3-4x the MFMA work per byte and need the registers for
-  // accumulators, so they load, wait and compute one iteration at a time.
+  // Main iterations of kU steps, walked from a hashed start. The loads are a
+  // rotating pipeline: as soon as the MFMAs of W register q have been issued,
+  // q is reloaded with the next iteration's row, so every wave keeps its 4*kU
+  // W loads in flight while it computes instead of draining them before each
+  // iteration. (The scheduling barrier keeps the compiler from sinking the
+  // reloads to the end of the iteration.) For three or four row blocks this
+  // also measured faster than loading, waiting and computing one iteration at
+  // a time: at K = N = 8192, M = 48 80.5 vs 91.6 us and M = 64 104 vs 115 us
+  // (M = 64 with 4 columns per lane uses all 128 registers and 8-16 bytes of
+  // scratch); at K = N = 4096 the two measure the same.
   const int nit = kwave / (16 * kU);
   const int r0 = nit > 0 ? (int)(((unsigned)blockIdx.x * 2654435761u >> 8) + (unsigned)wave * 977u) % nit : 0;
-  if constexpr (MB > 2) {
-    for (int i = 0; i < nit; ++i) {
-      int it = i + r0;
-      if (it >= nit) it -= nit;
-      vec w[4 * kU];
-      f32x4 x[kU][MB];
-      load_w(w, it * 16 * kU);
-      load_x(x, it * 16 * kU);
-#pragma unroll
-      for (int q = 0; q < 4 * kU; ++q) mfma_q(x[q / 4], q % 4, w[q]);
-    }
-  } else if (nit > 0) {
+  if (nit > 0) {
     vec w[4 * kU];
     f32x4 x[kU][MB], xn[kU][MB];
     int it = r0;
