@@ -1,7 +1,8 @@
 """Seeded random parity cases for the dense path through the C ABI.
 
 Each case draws a shape (including K = 0 and sizes that are no multiple of
-any tile), a dtype, a pattern, host or device operands, and for device
+any tile; a second set draws multiples of 4 up to 1100 with 16-byte aligned
+views, the shapes the edge tiles and padded int8 tiles serve), a dtype, a pattern, host or device operands, and for device
 operands a padded row stride and an element offset, then compares the HIP
 result with the oracle: i32 bit-exact (int8-range values take the int8 MFMA
 path, wider ones the exact i32 fallback), f32 within relative Frobenius 1e-5
@@ -24,17 +25,23 @@ _PATTERNS = {"matmul": (False, "none"), "matmul_relu": (False, "relu"), "matmul_
 _EPI = {"none": 0, "relu": 1, "leaky": 2}
 
 
-def _case(seed):
+_SMALL_DIMS = [1, 2, 3, 7, 16, 17, 31, 32, 33, 63, 64, 65, 96, 127, 128, 129, 200, 256, 300]
+# Multiples of 4 that divide no tile, up to 1100: with 16-byte aligned views
+# these take the fp32 edge tiles, partial small-M column blocks and the padded
+# int8 tiles on grids of many workgroups.
+_EDGE_DIMS = [4, 8, 12, 20, 36, 60, 100, 132, 260, 500, 516, 1000, 1028, 1100]
+
+
+def _case(seed, dims=_SMALL_DIMS, pads=(0, 0, 1, 3, 4, 9), offs=(0, 0, 1, 2, 4), k_zero=True):
     rng = np.random.default_rng(seed)
-    dims = [1, 2, 3, 7, 16, 17, 31, 32, 33, 63, 64, 65, 96, 127, 128, 129, 200, 256, 300]
     M, N = (int(rng.choice(dims)) for _ in range(2))
-    K = int(rng.choice(dims + [0]))
+    K = int(rng.choice(dims + [0] if k_zero else dims))
     dtype = "i32" if rng.random() < 0.4 else "f32"
     pats = [p for p in _PATTERNS if not (dtype == "i32" and p == "dense_leaky")]
     pattern = pats[int(rng.integers(len(pats)))]
     device = bool(rng.random() < 0.6)
-    pad = int(rng.choice([0, 0, 1, 3, 4, 9])) if device else 0
-    off = int(rng.choice([0, 0, 1, 2, 4])) if device else 0
+    pad = int(rng.choice(list(pads))) if device else 0
+    off = int(rng.choice(list(offs))) if device else 0
     wide = dtype == "i32" and rng.random() < 0.3
     return rng, M, K, N, dtype, pattern, device, pad, off, wide
 
@@ -72,8 +79,16 @@ def _device_view(torch, a, pad, off):
 
 @pytest.mark.parametrize("seed", range(60))
 def test_random_case(seed, torch_cuda):
-    torch = torch_cuda
-    rng, M, K, N, dtype, pattern, device, pad, off, wide = _case(seed)
+    _check_case(seed, _case(seed), torch_cuda)
+
+
+@pytest.mark.parametrize("seed", range(1000, 1040))
+def test_random_edge_case(seed, torch_cuda):
+    _check_case(seed, _case(seed, _EDGE_DIMS, pads=(0, 4, 8), offs=(0, 4), k_zero=False), torch_cuda)
+
+
+def _check_case(seed, case, torch):
+    rng, M, K, N, dtype, pattern, device, pad, off, wide = case
     bias, act = _PATTERNS[pattern]
     X = _draw(rng, (M, K), dtype, wide)
     W = _draw(rng, (K, N), dtype, wide)
