@@ -210,7 +210,12 @@ gemm_f32_kernel(GemmF32Args args) {
   const int half = lane >> 5;
   const int l32 = lane & 31;
 
+  // A wave raises its issue priority while it reads fragments and runs its
+  // MFMAs, so waves with MFMAs ready win issue over waves issuing loads or
+  // LDS stores (same box: c3 88.2 -> 88.5-88.8 % of peak, the 8-way c3
+  // column shard +2.7 %, c2 unchanged).
   auto compute = [&](int buf) {
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int jj = 0; jj < JP; ++jj) {
       const int j = wave_k * JP + jj;
@@ -233,6 +238,7 @@ gemm_f32_kernel(GemmF32Args args) {
             acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], bv[c], acc[i][c], 0, 0, 0);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   // K steps of the main loop: all of them, or with the edge guard the whole
