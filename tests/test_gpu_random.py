@@ -119,3 +119,15 @@ def _check_case(seed, case, torch):
             assert_f32_parity(got, ref, K)
         except AssertionError as e:
             raise AssertionError(f"{what}: {e}") from None
+
+
+def test_random_sweep(torch_cuda):
+    """Opt-in wide sweep: EDSL_RANDOM_SWEEP=N runs N more seeds of both case
+    sets in this one test (N = 20000 takes about six minutes on one MI355X)."""
+    import os
+    n = int(os.environ.get("EDSL_RANDOM_SWEEP", "0"))
+    if n <= 0:
+        pytest.skip("set EDSL_RANDOM_SWEEP=N to run N more seeds")
+    for seed in range(10000, 10000 + n):
+        _check_case(seed, _case(seed), torch_cuda)
+        _check_case(seed, _case(seed, _EDGE_DIMS, pads=(0, 4, 8), offs=(0, 4), k_zero=False), torch_cuda)
