@@ -63,9 +63,11 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
   constexpr int WK = kWavesPerWG / WN;
   constexpr int kWaveCols = 16 * CPL;
   constexpr int kGroupCols = kWaveCols * WN;
-  // 16-row steps per loop iteration: 8 W loads in flight per lane, fewer when
-  // the accumulators of 3-4 row blocks need the registers.
-  constexpr int kU = MB <= 2 ? 2 : 1;
+  // 16-row steps per loop iteration: 8 W loads in flight per lane for one row
+  // block, 4 for more. Two row blocks measured faster with one step than with
+  // two (M = 32: 21.4 vs 23.5 us at K = N = 4096, 56.5 vs 59.9 us at 8192), and
+  // three or four need the registers for their accumulators.
+  constexpr int kU = MB == 1 ? 2 : 1;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wn = wave % WN;
