@@ -242,7 +242,8 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
     }
 }
 
-// Y[m, 4j..4j+3] = epilogue(sum over splits s = 0..ksplit-1, in order).
+// Y[m, 4j..4j+3] = epilogue(sum over splits s = 0..ksplit-1, in order, plus
+// the K tail rows).
 // All split loads are issued before the first add so their latencies overlap.
 __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi, int prow) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over M * N/4
@@ -262,6 +263,12 @@ __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi
 #pragma unroll
   for (int sp = 1; sp < kMaxSplit; ++sp)
     if (sp < a.ksplit) s += v[sp];
+  // The last K % 16 rows, after the split sums, in ascending k.
+  for (int k = a.K; k < a.k_end; ++k) {
+    const float xv = a.x_tail[(int64_t)row * a.ldx_tail + k];
+    const f32x4 wv = *reinterpret_cast<const f32x4*>(a.W + (int64_t)k * a.ldw + col);
+    s += xv * wv;
+  }
   f32x4 y;
 #pragma unroll
   for (int c = 0; c < 4; ++c) y[c] = epilogue_rt(s[c], bv[c], a.alpha, epi);

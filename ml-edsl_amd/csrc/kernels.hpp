@@ -48,11 +48,17 @@ struct GemvF32Args {
   int ksplit;         // K slices reduced by a second kernel (1 = none)
   float alpha;
   float* partials;    // [ksplit][16*ceil(M/16)][N] when ksplit > 1
+  // K tail: rows K .. k_end-1 of W (k_end - K < 16), with X read from x_tail
+  // (row stride ldx_tail), are added by the reduce kernel; k_end == K: none.
+  const float* x_tail;
+  int64_t ldx_tail;
+  int k_end;
 };
 
-// A workgroup is 16 waves over `cols` adjacent columns (32, 64, 128 or 256);
-// the waves not side by side split K. Requirements (checked by the caller):
-// 1 <= M <= 64, N % cols == 0, K % (16 * gemv_f32_waves_k(cols) * ksplit) == 0,
+// A workgroup is 16 waves over `cols` adjacent columns (32, 64, 128 or 256),
+// the last block possibly partial; the waves not side by side split K, which
+// is walked in 16-row chunks. Requirements (checked by the caller):
+// 1 <= M <= 64, N % 4 == 0, K % 16 == 0, ksplit > 1 when there is a K tail,
 // 16-byte aligned X/W/Y/bias and row strides % 4 == 0.
 hipError_t launch_gemv_f32(int epi, int cols, GemvF32Args args, hipStream_t stream);
 int gemv_f32_waves_k(int cols);

@@ -122,6 +122,7 @@ struct DeviceState {
   DevBuf stage[4];  // host-operand staging: X/A, W/B, bias, Y/C
   DevBuf chain[2];  // intermediate activations of multi-layer programs (ping-pong)
   DevBuf gemv_partials{true};
+  DevBuf gemv_xstage{true};  // X rows copied to 16-byte aligned rows for the small-M kernel
   DevBuf i8_x{true}, i8_w{true}, i8_flag{true};
   unsigned epoch = 0;
   // Ordering of the launches that use the library scratch above (split-K
@@ -334,8 +335,18 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
                        L.ldx % 4 == 0 && L.ldw % 4 == 0 && L.ldy % 4 == 0;
   const int M = (int)L.M, N = (int)L.N, K = (int)L.K;
 
+  // Small M: the streaming kernel walks the first K16 = K - K % 16 rows; the
+  // reduce kernel adds the rest. X rows that are not 16-byte aligned are
+  // first copied into aligned rows (at most 64 of them); W, Y and the bias
+  // must be aligned in place.
   int gemv_cols = 0, gemv_ks = 0;
-  if (aligned && M >= 1 && M <= kGemvMaxM && K > 0 && plan_gemv(ds, N, K, &gemv_cols, &gemv_ks)) {
+  const int K16 = K & ~15;
+  const bool w_ok = al16(L.w) && al16(L.y) && (!has_bias || al16(L.bias)) && L.ldw % 4 == 0 &&
+                    L.ldy % 4 == 0;
+  if (w_ok && M >= 1 && M <= kGemvMaxM && K16 > 0 && plan_gemv(ds, N, K16, &gemv_cols, &gemv_ks)) {
+    const bool x_ok = al16(L.x) && L.ldx % 4 == 0;
+    const bool tail = K16 < K;
+    if (tail && gemv_ks == 1) gemv_ks = 2;  // the reduce kernel adds the tail
     GemvF32Args a{};
     a.X = static_cast<const float*>(L.x);
     a.W = static_cast<const float*>(L.w);
@@ -346,19 +357,31 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     a.ldy = L.ldy;
     a.M = M;
     a.N = N;
-    a.K = K;
+    a.K = K16;
+    a.k_end = K;
+    a.x_tail = static_cast<const float*>(L.x);
+    a.ldx_tail = L.ldx;
     a.alpha = L.alpha;
     a.ksplit = gemv_ks;
     const int mb = (M + 15) / 16;
-    if (a.ksplit > 1) {
+    const bool scratch = a.ksplit > 1 || !x_ok;
+    if (scratch) scratch_begin(ds, stream);
+    if (a.ksplit > 1)
       a.partials = static_cast<float*>(
           ds.gemv_partials.ensure((size_t)a.ksplit * 16 * mb * N * sizeof(float), false));
-      scratch_begin(ds, stream);
+    if (!x_ok) {
+      float* xs = static_cast<float*>(ds.gemv_xstage.ensure((size_t)M * K16 * sizeof(float), false));
+      check_hip(hipMemcpy2DAsync(xs, (size_t)K16 * sizeof(float), L.x, (size_t)L.ldx * sizeof(float),
+                                 (size_t)K16 * sizeof(float), M, hipMemcpyDeviceToDevice, stream),
+                "hipMemcpy2DAsync (X rows to aligned rows)");
+      a.X = xs;
+      a.ldx = K16;
     }
     check_hip(launch_gemv_f32(L.epi, gemv_cols, a, stream), "gemv_f32 launch");
-    if (a.ksplit > 1) scratch_end(ds, stream);
-    set_plan("gemv_f32 mb=%d ksplit=%d cols=%d grid=%d%s", mb, a.ksplit, gemv_cols,
-             ((N + gemv_cols - 1) / gemv_cols) * a.ksplit, a.ksplit > 1 ? " +reduce" : "");
+    if (scratch) scratch_end(ds, stream);
+    set_plan("gemv_f32 mb=%d ksplit=%d cols=%d grid=%d%s%s%s", mb, a.ksplit, gemv_cols,
+             ((N + gemv_cols - 1) / gemv_cols) * a.ksplit, a.ksplit > 1 ? " +reduce" : "",
+             x_ok ? "" : " +xstage", tail ? " +ktail" : "");
     return;
   }
 

@@ -54,7 +54,8 @@ def _run(torch, X, W, b, pad=0, off=0):
     return tY.cpu().numpy(), _native.last_plan()
 
 
-EDGE_SHAPES = [(300, 100, 260), (257, 68, 132), (65, 20, 36), (33, 1000, 1028), (1, 4, 4)]
+# M > 64 or K < 16 throughout: smaller M with K >= 16 takes the small-M kernel.
+EDGE_SHAPES = [(300, 100, 260), (257, 68, 132), (65, 20, 36), (97, 1000, 1028), (1, 4, 4)]
 
 
 def test_every_edge_config_on_odd_shapes(torch_cuda):
@@ -164,6 +165,52 @@ def test_small_m_every_width_on_a_partial_block(torch_cuda):
     finally:
         set_gemv_ksplit(0)
         set_gemv_cols(0)
+
+
+def _run_x_view(torch, X, W, b, x_pad, x_off, ksplit=None):
+    """Only X is a (possibly misaligned) view; W, b and Y are contiguous."""
+    from mlir_edsl_hip.device import dense_launch, set_gemv_ksplit
+    M, K = X.shape
+    N = W.shape[1]
+    buf = torch.zeros(M * (K + x_pad) + x_off, dtype=torch.float32, device="cuda")
+    tX = buf[x_off:].view(M, K + x_pad)[:, :K]
+    tX.copy_(torch.from_numpy(X))
+    tW, tb = torch.from_numpy(W).cuda(), torch.from_numpy(b).cuda()
+    tY = torch.full((M, N), float("nan"), device="cuda")
+    if ksplit is not None:
+        set_gemv_ksplit(ksplit)
+    try:
+        dense_launch(tX, tW, tb, tY, _native.EPI_BIAS_RELU)
+        torch.cuda.synchronize()
+    finally:
+        set_gemv_ksplit(0)
+    return tY.cpu().numpy(), _native.last_plan()
+
+
+@pytest.mark.parametrize("M, K, N, x_pad, x_off, tags", [
+    (16, 8191, 8192, 0, 0, ("+xstage", "+ktail")),   # contiguous X, odd K: unaligned rows
+    (16, 8192, 2048, 0, 1, ("+xstage",)),             # misaligned X base, K % 16 == 0
+    (33, 4100, 512, 0, 0, ("+ktail",)),               # aligned X, K % 16 == 4
+    (5, 1003, 1024, 2, 3, ("+xstage", "+ktail")),
+], ids=["odd-K", "misaligned-X", "aligned-tail", "both"])
+def test_small_m_k_tail_and_x_staging(M, K, N, x_pad, x_off, tags, torch_cuda):
+    X, W, b = _inputs(M, K, N, M + K + N)
+    got, plan = _run_x_view(torch_cuda, X, W, b, x_pad, x_off)
+    assert plan.startswith("gemv_f32"), plan
+    for t in tags:
+        assert t in plan, plan
+    if "+ktail" not in tags:
+        assert "+ktail" not in plan, plan
+    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+
+
+def test_small_m_k_tail_forces_the_reduce(torch_cuda):
+    """A forced single split becomes two when there is a K tail: the reduce
+    kernel adds the tail rows."""
+    X, W, b = _inputs(16, 4100, 1024, 3)
+    got, plan = _run_x_view(torch_cuda, X, W, b, 0, 0, ksplit=1)
+    assert "ksplit=2" in plan and "+ktail" in plan, plan
+    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), 4100)
 
 
 # ------------------------------------------------------------ integer path
