@@ -40,6 +40,8 @@ def _inputs(torch, g, dtype, M, K):
 CASES = [
     ("tiled_f32_chain", "f32", 512, [384, 512, 256, 320], [3, 3, 0], ["gemm_f32"] * 3),
     ("small_m_split_k", "f32", 16, [4096, 2048, 1024], [3, 1], ["gemv_f32"] * 2),
+    # K = 4099: X rows copied to aligned rows, then a 3-row K tail; K = 2052: a 4-row tail
+    ("small_m_staged_tail", "f32", 16, [4099, 2052, 1028], [3, 1], ["gemv_f32"] * 2),
     ("int8_path", "i32", 256, [384, 256, 512], [3, 3], ["narrow_i8+gemm_i8"] * 2),
 ]
 
@@ -82,6 +84,9 @@ def test_graph_replay_matches_eager(name, dtype, M, widths, epis, plans):
         yb = torch.empty(64, 8192, device="cuda")
         dense_launch(big, Wb, None, yb, 0)
         assert "ksplit=" in _native.last_plan() and "ksplit=1 " not in _native.last_plan()
+        xo = torch.randn(64, 8191, device="cuda", generator=g)  # unaligned rows: staged
+        dense_launch(xo, Wb[:8191], None, yb, 0)
+        assert "+xstage" in _native.last_plan()
         xi = torch.randint(-128, 128, (2048, 2048), device="cuda", dtype=torch.int32, generator=g)
         yi = torch.empty(2048, 2048, device="cuda", dtype=torch.int32)
         dense_launch(xi, xi, None, yi, 0)
