@@ -20,7 +20,7 @@ SPIN_CYCLES = 200_000  # ~0.1 ms
 
 
 def _problem(torch, rng, dtype, M, K, N):
-    if dtype == "f32":
+    if dtype in ("f32", "f32s"):
         X = rng.standard_normal((M, K), dtype=np.float32)
         W = rng.standard_normal((K, N), dtype=np.float32)
         b = rng.standard_normal(N, dtype=np.float32)
@@ -35,12 +35,15 @@ def _problem(torch, rng, dtype, M, K, N):
     return t, Y, ref, K
 
 
-@pytest.mark.parametrize("kinds", [("f32", "f32"), ("i32", "i32"), ("f32", "i32")])
+# f32s: small M with K = 2047, so X rows are staged into aligned rows (one
+# more scratch buffer) and the reduce kernel adds a K tail
+@pytest.mark.parametrize("kinds", [("f32", "f32"), ("i32", "i32"), ("f32", "i32"), ("f32s", "f32s"),
+                                   ("f32s", "i32")])
 def test_scratch_users_on_two_streams(kinds):
     import torch
     assert torch.cuda.is_available()
     rng = np.random.default_rng(11)
-    shapes = {"f32": (16, 2048, 2048), "i32": (256, 384, 256)}
+    shapes = {"f32": (16, 2048, 2048), "i32": (256, 384, 256), "f32s": (16, 2047, 2048)}
     streams = [torch.cuda.Stream(), torch.cuda.Stream()]
     # four rounds, each stream gets its own problem every round
     probs = [[_problem(torch, rng, kinds[j], *shapes[kinds[j]]) for j in range(2)] for _ in range(4)]
@@ -55,7 +58,7 @@ def test_scratch_users_on_two_streams(kinds):
     torch.cuda.synchronize()
     # both scratch users are exercised
     for k in set(kinds):
-        want = "ksplit=" if k == "f32" else "narrow_i8+gemm_i8"
+        want = {"f32": "ksplit=", "f32s": "+xstage", "i32": "narrow_i8+gemm_i8"}[k]
         assert any(want in p and ("ksplit=1 " not in p) for p in plans), plans
     for r, rnd in enumerate(probs):
         for j, (_, Y, ref, K) in enumerate(rnd):
