@@ -55,8 +55,12 @@ int edsl_hip_dense_i32_launch(const int32_t *X, int64_t ldx, const int32_t *W, i
                               const int32_t *bias, int32_t *Y, int64_t ldy, int64_t M,
                               int64_t N, int64_t K, int epilogue, void *stream);
 
-/* Description of the kernels the calling thread's last call launched
- * (e.g. "gemv_f32 mb=1 ksplit=4 grid=512"); returns its length. */
+/* Description of the kernels the calling thread's last call launched, e.g.
+ * "gemm_f32 cfg=f32_256x256x16_w4x4 grid=256" (a "_edge" suffix: partial
+ * edge tiles), "gemv_f32 mb=1 ksplit=4 cols=128 grid=256 +reduce" (with
+ * "+xstage": X rows copied to aligned rows; "+ktail": the reduce kernel adds
+ * the last K % 16 rows) or "narrow_i8+gemm_i8 variant=3 waves=ksplit depth=2
+ * grid=256"; returns its length. */
 int edsl_hip_last_plan(char *buf, size_t len);
 
 /* Tuning overrides: force an f32 tile configuration (index into the table
