@@ -771,6 +771,20 @@ void sync_dense_chain(int dtype, const LayerOp* layers, int n, const Mat& Y) {
   check_hip(hipGetLastError(), "kernel execution");
 }
 
+// The row stride of a matrix with a single row is never used to reach a second
+// row, so a caller may pass anything there (a (1,K) view of a column vector
+// has stride 1, a broadcast view 0). Such strides are replaced by the row
+// length, as mat_from_desc does for descriptors, so that the planner's
+// alignment tests and the X-row staging copy (whose source pitch must cover a
+// row) see a consistent layout.
+void normalize_single_row_strides(int64_t M, int64_t N, int64_t K, int64_t* ldx, int64_t* ldw, int64_t* ldy) {
+  if (M <= 1) {
+    *ldx = K;
+    *ldy = N;
+  }
+  if (K <= 1) *ldw = N;
+}
+
 void sync_dense(int dtype, int epi, float alpha, const Mat& X, const Mat& W, const Vec* b, const Mat& Y) {
   const LayerOp op{&X, &W, b, epi, alpha};
   sync_dense_chain(dtype, &op, 1, Y);
@@ -912,6 +926,7 @@ int edsl_hip_dense_f32_launch(const float* X, int64_t ldx, const float* W, int64
     if (K > 0 && M > 1 && ldx < K) fail(kErrStride, "ldx < K");
     if (N > 0 && K > 1 && ldw < N) fail(kErrStride, "ldw < N");
     if (N > 0 && M > 1 && ldy < N) fail(kErrStride, "ldy < N");
+    normalize_single_row_strides(M, N, K, &ldx, &ldw, &ldy);
     std::lock_guard<std::mutex> lock(g_mu);
     read_env_overrides();
     DeviceState& ds = device_state(nullptr);
@@ -929,6 +944,7 @@ int edsl_hip_dense_i32_launch(const int32_t* X, int64_t ldx, const int32_t* W, i
     if (K > 0 && M > 1 && ldx < K) fail(kErrStride, "ldx < K");
     if (N > 0 && K > 1 && ldw < N) fail(kErrStride, "ldw < N");
     if (N > 0 && M > 1 && ldy < N) fail(kErrStride, "ldy < N");
+    normalize_single_row_strides(M, N, K, &ldx, &ldw, &ldy);
     std::lock_guard<std::mutex> lock(g_mu);
     read_env_overrides();
     DeviceState& ds = device_state(nullptr);

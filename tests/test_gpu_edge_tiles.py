@@ -167,7 +167,7 @@ def test_small_m_every_width_on_a_partial_block(torch_cuda):
         set_gemv_cols(0)
 
 
-def _run_x_view(torch, X, W, b, x_pad, x_off, ksplit=None):
+def _run_x_view(torch, X, W, b, x_pad, x_off, ksplit=None, epi=_native.EPI_BIAS_RELU, alpha=0.0):
     """Only X is a (possibly misaligned) view; W, b and Y are contiguous."""
     from mlir_edsl_hip.device import dense_launch, set_gemv_ksplit
     M, K = X.shape
@@ -180,7 +180,7 @@ def _run_x_view(torch, X, W, b, x_pad, x_off, ksplit=None):
     if ksplit is not None:
         set_gemv_ksplit(ksplit)
     try:
-        dense_launch(tX, tW, tb, tY, _native.EPI_BIAS_RELU)
+        dense_launch(tX, tW, tb if epi & 1 else None, tY, epi, alpha)
         torch.cuda.synchronize()
     finally:
         set_gemv_ksplit(0)
@@ -202,6 +202,53 @@ def test_small_m_k_tail_and_x_staging(M, K, N, x_pad, x_off, tags, torch_cuda):
     if "+ktail" not in tags:
         assert "+ktail" not in plan, plan
     assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+
+
+_TAIL_EPIS = {"none": (_native.EPI_NONE, None, "none"), "bias": (_native.EPI_BIAS, "b", "none"),
+              "leaky": (_native.EPI_BIAS_LEAKY, "b", "leaky"), "relu_nobias": (_native.EPI_RELU, None, "relu")}
+
+
+@pytest.mark.parametrize("epi_name", sorted(_TAIL_EPIS))
+@pytest.mark.parametrize("M", [1, 32, 64])
+@pytest.mark.parametrize("K, x_pad, x_off", [(2047, 0, 0), (4099, 3, 1), (1003, 0, 2)],
+                         ids=["odd-K", "padded-offset", "offset"])
+def test_small_m_tail_and_staging_per_row_block_and_epilogue(M, K, x_pad, x_off, epi_name, torch_cuda):
+    """The staged-X and K-tail paths for one, two and four row blocks, with
+    every epilogue the reduce kernel applies after adding the tail."""
+    epi, use_b, act = _TAIL_EPIS[epi_name]
+    N = 1024
+    X, W, b = _inputs(M, K, N, 7 * M + K)
+    got, plan = _run_x_view(torch_cuda, X, W, b, x_pad, x_off, epi=epi, alpha=0.05)
+    assert plan.startswith(f"gemv_f32 mb={(M + 15) // 16}"), plan
+    assert "+ktail" in plan and "+xstage" in plan, plan
+    ref = oracle.dense_f32(X, W, b if use_b else None, act, 0.05)
+    assert_f32_parity(got, ref, K)
+
+
+@pytest.mark.parametrize("K", [8191, 1001, 4096])
+def test_single_row_x_with_any_row_stride(K, torch_cuda):
+    """A (1, K) view of a column vector has row stride 1 (and a broadcast view
+    0): with a single row the stride is never used, so any value must work."""
+    from mlir_edsl_hip.device import dense_launch
+    N = 2048
+    X, W, b = _inputs(1, K, N, K)
+    tX = torch_cuda.from_numpy(np.ascontiguousarray(X.reshape(K, 1))).cuda().T  # shape (1, K), strides (1, 1)
+    assert tX.stride() == (1, 1)
+    tW, tb = torch_cuda.from_numpy(W).cuda(), torch_cuda.from_numpy(b).cuda()
+    tY = torch_cuda.full((1, N), float("nan"), device="cuda")
+    dense_launch(tX, tW, tb, tY, _native.EPI_BIAS_RELU)
+    torch_cuda.cuda.synchronize()
+    assert _native.last_plan().startswith("gemv_f32"), _native.last_plan()
+    assert_f32_parity(tY.cpu().numpy(), oracle.dense_f32(X, W, b, "relu"), K)
+    # Row stride 0 through the C ABI directly (torch reports the view's own
+    # stride; a broadcast (1, K) row from expand() has stride 0 on dim 0).
+    tY2 = torch_cuda.full((1, N), float("nan"), device="cuda")
+    rc = _native.lib().edsl_hip_dense_f32_launch(tX.data_ptr(), 0, tW.data_ptr(), N, tb.data_ptr(),
+                                                 tY2.data_ptr(), 0, 1, N, K, _native.EPI_BIAS_RELU, 0.0,
+                                                 torch_cuda.cuda.current_stream().cuda_stream)
+    assert rc == 0, _native.last_error()
+    torch_cuda.cuda.synchronize()
+    assert np.array_equal(tY2.cpu().numpy(), tY.cpu().numpy())
 
 
 def test_small_m_k_tail_forces_the_reduce(torch_cuda):

@@ -145,16 +145,14 @@ def test_c2_dense_1024(torch_cuda):
     check(gpu_run("dense_relu", [X, W, b], device=False), ref, w.K)
 
 
-def test_c3_dense_4096_sampled_rows(torch_cuda):
+def test_c3_dense_4096_full(torch_cuda):
+    """The headline layer, every one of its 4096 x 4096 outputs against the
+    oracle (about a second of CPU time on 16 threads)."""
     w = WORKLOADS["c3"]
     X, W, b = make_inputs(w)
     got = gpu_run("dense_relu", [X, W, b], device=True)
     assert _native.last_plan().startswith("gemm_f32")
-    rows = np.sort(np.random.default_rng(0).choice(w.M, 256, replace=False))
-    ref = oracle.dense_f32(X[rows], W, b, "relu")
-    check(got[rows], ref, w.K)
-    # size-independent property over the full output: ReLU output is >= 0 or NaN-free
-    assert np.all(got >= 0) and np.isfinite(got).all()
+    check(got, oracle.dense_f32(X, W, b, "relu"), w.K)
 
 
 def test_c4_dense_small_m(torch_cuda):
@@ -176,14 +174,13 @@ def test_c4_column_shard(torch_cuda):
     check(got, oracle.dense_f32(X, W, b, "relu"), w.K)
 
 
-def test_c3_column_shard_sampled_rows(torch_cuda):
-    """One GPU's share of c3 column-sharded 8 ways, 256 sampled rows."""
+def test_c3_column_shard_full(torch_cuda):
+    """One GPU's share of c3 column-sharded 8 ways, full output."""
     w = WORKLOADS["c3s8"]
     X, W, b = make_inputs(w)
     got = gpu_run("dense_relu", [X, W, b], device=True)
     assert _native.last_plan().startswith("gemm_f32")
-    rows = np.sort(np.random.default_rng(1).choice(w.M, 256, replace=False))
-    check(got[rows], oracle.dense_f32(X[rows], W, b, "relu"), w.K)
+    check(got, oracle.dense_f32(X, W, b, "relu"), w.K)
 
 
 def test_column_shards_reassemble_the_layer(torch_cuda):
@@ -213,8 +210,7 @@ def test_c5_int_dense_bit_exact(torch_cuda):
     exact = X.astype(np.float64) @ W.astype(np.float64) + b  # |sum| < 2^53: exact
     exp = np.maximum(exact, 0).astype(np.int32)
     assert np.array_equal(got, exp)
-    rows = np.arange(0, w.M, 37)
-    assert np.array_equal(got[rows], oracle.dense_i32(X[rows], W, b, "relu"))
+    assert np.array_equal(got, oracle.dense_i32(X, W, b, "relu"))
 
 
 # ------------------------------------------------------------ integer path
