@@ -49,6 +49,24 @@ int edsl_hip_dense_f32_launch(const float *X, int64_t ldx, const float *W, int64
                               const float *bias, float *Y, int64_t ldy, int64_t M,
                               int64_t N, int64_t K, int epilogue, float alpha, void *stream);
 
+/* Allocation-free variant of edsl_hip_dense_f32_launch: same arguments,
+ * kernels and results (bit for bit, for the same plan). No counterpart in the
+ * reference: it is for callers that cannot allocate device memory -- code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. It calls no hipMalloc/hipFree and creates no events: the
+ * small-M plan's scratch (split-K partials, X rows staged to 16-byte
+ * alignment) lives in a static device array of EDSL_NOALLOC_SCRATCH_BYTES
+ * per GPU, held until the process ends. A plan that needs more scratch than
+ * that is rejected (error code -5, the message gives both sizes); the tiled
+ * plans need none. Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams or threads without ordering between them)
+ * race. */
+#define EDSL_NOALLOC_SCRATCH_BYTES (16u << 20)
+int edsl_hip_dense_f32_launch_noalloc(const float *X, int64_t ldx, const float *W, int64_t ldw,
+                                      const float *bias, float *Y, int64_t ldy, int64_t M,
+                                      int64_t N, int64_t K, int epilogue, float alpha,
+                                      void *stream);
+
 /* Y[M,N] = epilogue(X[M,K] @ W[K,N] (+ bias)), i32 wrapping arithmetic.
  * Leaky epilogues are rejected (float-only in the reference). */
 int edsl_hip_dense_i32_launch(const int32_t *X, int64_t ldx, const int32_t *W, int64_t ldw,

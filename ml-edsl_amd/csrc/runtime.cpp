@@ -329,7 +329,7 @@ bool plan_gemv(const DeviceState& ds, int64_t N, int64_t K, int* cols_out, int* 
   return true;
 }
 
-void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
+void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const FixedScratch* fixed) {
   const bool has_bias = epi_has_bias(L.epi);
   const bool aligned = al16(L.x) && al16(L.w) && al16(L.y) && (!has_bias || al16(L.bias)) &&
                        L.ldx % 4 == 0 && L.ldw % 4 == 0 && L.ldy % 4 == 0;
@@ -365,12 +365,26 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     a.ksplit = gemv_ks;
     const int mb = (M + 15) / 16;
     const bool scratch = a.ksplit > 1 || !x_ok;
-    if (scratch) scratch_begin(ds, stream);
-    if (a.ksplit > 1)
-      a.partials = static_cast<float*>(
-          ds.gemv_partials.ensure((size_t)a.ksplit * 16 * mb * N * sizeof(float), false));
+    const size_t part_bytes = a.ksplit > 1 ? (size_t)a.ksplit * 16 * mb * N * sizeof(float) : 0;
+    const size_t xs_bytes = x_ok ? 0 : (size_t)M * K16 * sizeof(float);
+    float* xs = nullptr;
+    if (fixed) {
+      // Caller-fixed scratch: partials first, the staged X rows after them.
+      // Nothing is allocated and no cross-stream ordering is added.
+      const size_t xs_off = (part_bytes + 255) & ~size_t(255);
+      if (xs_off + xs_bytes > fixed->bytes)
+        fail(kErrLimit,
+             "small-M plan (M=%d N=%d K=%d, %d splits%s) needs %zu bytes of scratch; the fixed scratch "
+             "holds %zu",
+             M, N, K, a.ksplit, x_ok ? "" : ", staged X rows", xs_off + xs_bytes, fixed->bytes);
+      if (part_bytes) a.partials = reinterpret_cast<float*>(fixed->base);
+      if (xs_bytes) xs = reinterpret_cast<float*>(fixed->base + xs_off);
+    } else {
+      if (scratch) scratch_begin(ds, stream);
+      if (part_bytes) a.partials = static_cast<float*>(ds.gemv_partials.ensure(part_bytes, false));
+      if (xs_bytes) xs = static_cast<float*>(ds.gemv_xstage.ensure(xs_bytes, false));
+    }
     if (!x_ok) {
-      float* xs = static_cast<float*>(ds.gemv_xstage.ensure((size_t)M * K16 * sizeof(float), false));
       check_hip(hipMemcpy2DAsync(xs, (size_t)K16 * sizeof(float), L.x, (size_t)L.ldx * sizeof(float),
                                  (size_t)K16 * sizeof(float), M, hipMemcpyDeviceToDevice, stream),
                 "hipMemcpy2DAsync (X rows to aligned rows)");
@@ -378,10 +392,10 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
       a.ldx = K16;
     }
     check_hip(launch_gemv_f32(L.epi, gemv_cols, a, stream), "gemv_f32 launch");
-    if (scratch) scratch_end(ds, stream);
-    set_plan("gemv_f32 mb=%d ksplit=%d cols=%d grid=%d%s%s%s", mb, a.ksplit, gemv_cols,
+    if (scratch && !fixed) scratch_end(ds, stream);
+    set_plan("gemv_f32 mb=%d ksplit=%d cols=%d grid=%d%s%s%s%s", mb, a.ksplit, gemv_cols,
              ((N + gemv_cols - 1) / gemv_cols) * a.ksplit, a.ksplit > 1 ? " +reduce" : "",
-             x_ok ? "" : " +xstage", tail ? " +ktail" : "");
+             x_ok ? "" : " +xstage", tail ? " +ktail" : "", fixed && scratch ? " +fixed-scratch" : "");
     return;
   }
 
@@ -522,7 +536,7 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
   }
 }
 
-void launch_dense(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
+void launch_dense(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const FixedScratch* fixed = nullptr) {
   check_dims(L.M, L.N, L.K);
   if (L.M == 0 || L.N == 0) {
     set_plan("empty");
@@ -530,8 +544,8 @@ void launch_dense(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
   }
   if (L.epi < 0 || L.epi > 5) fail(kErrArgument, "bad epilogue code %d", L.epi);
   if (L.dtype == EDSL_DTYPE_F32)
-    launch_f32(ds, L, stream);
-  else if (L.dtype == EDSL_DTYPE_I32)
+    launch_f32(ds, L, stream, fixed);
+  else if (L.dtype == EDSL_DTYPE_I32 && !fixed)
     launch_i32(ds, L, stream);
   else
     fail(kErrDtype, "bad dtype %d", L.dtype);
@@ -790,6 +804,22 @@ void sync_dense(int dtype, int epi, float alpha, const Mat& X, const Mat& W, con
   sync_dense_chain(dtype, &op, 1, Y);
 }
 
+void dense_f32_launch(const float* X, int64_t ldx, const float* W, int64_t ldw, const float* bias, float* Y,
+                      int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, float alpha, void* stream,
+                      const FixedScratch* fixed) {
+  if (epi_has_bias(epilogue) && !bias && N > 0) fail(kErrArgument, "epilogue adds a bias but bias is null");
+  if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) fail(kErrArgument, "null operand");
+  if (K > 0 && M > 1 && ldx < K) fail(kErrStride, "ldx < K");
+  if (N > 0 && K > 1 && ldw < N) fail(kErrStride, "ldw < N");
+  if (N > 0 && M > 1 && ldy < N) fail(kErrStride, "ldy < N");
+  normalize_single_row_strides(M, N, K, &ldx, &ldw, &ldy);
+  std::lock_guard<std::mutex> lock(g_mu);
+  read_env_overrides();
+  DeviceState& ds = device_state(nullptr);
+  DenseLaunch L{EDSL_DTYPE_F32, epilogue, alpha, X, ldx, W, ldw, bias, Y, ldy, M, N, K};
+  launch_dense(ds, L, static_cast<hipStream_t>(stream), fixed);
+}
+
 }  // namespace rt
 }  // namespace edsl
 
@@ -920,19 +950,7 @@ void edsl_hip_clear_error(void) {
 int edsl_hip_dense_f32_launch(const float* X, int64_t ldx, const float* W, int64_t ldw, const float* bias,
                               float* Y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
                               float alpha, void* stream) {
-  return guarded([&] {
-    if (epi_has_bias(epilogue) && !bias && N > 0) fail(kErrArgument, "epilogue adds a bias but bias is null");
-    if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) fail(kErrArgument, "null operand");
-    if (K > 0 && M > 1 && ldx < K) fail(kErrStride, "ldx < K");
-    if (N > 0 && K > 1 && ldw < N) fail(kErrStride, "ldw < N");
-    if (N > 0 && M > 1 && ldy < N) fail(kErrStride, "ldy < N");
-    normalize_single_row_strides(M, N, K, &ldx, &ldw, &ldy);
-    std::lock_guard<std::mutex> lock(g_mu);
-    read_env_overrides();
-    DeviceState& ds = device_state(nullptr);
-    DenseLaunch L{EDSL_DTYPE_F32, epilogue, alpha, X, ldx, W, ldw, bias, Y, ldy, M, N, K};
-    launch_dense(ds, L, static_cast<hipStream_t>(stream));
-  });
+  return guarded([&] { dense_f32_launch(X, ldx, W, ldw, bias, Y, ldy, M, N, K, epilogue, alpha, stream, nullptr); });
 }
 
 int edsl_hip_dense_i32_launch(const int32_t* X, int64_t ldx, const int32_t* W, int64_t ldw,

@@ -92,5 +92,19 @@ struct LayerOp {
 // return.
 void sync_dense_chain(int dtype, const LayerOp* layers, int n, const Mat& Y);
 
+// Device memory for the small-M kernel's split-K partials and staged X rows
+// that the caller fixes, in place of the library's grow-only per-device
+// workspaces: nothing is allocated, and no cross-stream ordering is added.
+struct FixedScratch {
+  char* base;    // device address, 256-byte aligned
+  size_t bytes;  // capacity; a plan that needs more is rejected (kErrLimit)
+};
+
+// Body of edsl_hip_dense_f32_launch (argument checks, plan, launch); with
+// `fixed` non-null every scratch buffer comes from it. Throws Failure.
+void dense_f32_launch(const float* X, int64_t ldx, const float* W, int64_t ldw, const float* bias, float* Y,
+                      int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, float alpha, void* stream,
+                      const FixedScratch* fixed);
+
 }  // namespace rt
 }  // namespace edsl

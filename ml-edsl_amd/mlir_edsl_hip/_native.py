@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libedsl_hip
 EPI_NONE, EPI_BIAS, EPI_RELU, EPI_BIAS_RELU, EPI_LEAKY, EPI_BIAS_LEAKY = range(6)
 PATTERN_MATMUL, PATTERN_MATMUL_BIAS, PATTERN_DENSE_RELU, PATTERN_DENSE_LEAKY, PATTERN_MATMUL_RELU = range(5)
 DTYPE_F32, DTYPE_I32 = 0, 1
+NOALLOC_SCRATCH_BYTES = 16 << 20  # EDSL_NOALLOC_SCRATCH_BYTES (include/edsl_hip_device.h)
 
 # Flat scalar run of one expanded memref argument (MLIR func-to-llvm):
 # allocated ptr, aligned ptr, offset, sizes[r], strides[r].
@@ -57,6 +58,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.edsl_hip_dense_f32_launch.argtypes = [vp, i64, vp, i64, vp, vp, i64, i64, i64, i64, c_int,
                                             c_float, vp]
     L.edsl_hip_dense_f32_launch.restype = c_int
+    L.edsl_hip_dense_f32_launch_noalloc.argtypes = L.edsl_hip_dense_f32_launch.argtypes
+    L.edsl_hip_dense_f32_launch_noalloc.restype = c_int
     L.edsl_hip_dense_i32_launch.argtypes = [vp, i64, vp, i64, vp, vp, i64, i64, i64, i64, c_int, vp]
     L.edsl_hip_dense_i32_launch.restype = c_int
     L.edsl_hip_last_plan.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
