@@ -78,8 +78,32 @@ int edsl_hip_module_execute_gpu_function(edsl_hip_module *m, const char *name, i
                                          void *output, const int64_t *output_shape, int output_rank,
                                          size_t element_size);
 
+/* Device-resident parameters. Replaces, for the operands a caller marks as
+ * constant across calls (weights, biases), the per-call device allocation and
+ * host-to-device copy of every operand in the reference's GPU path
+ * (cpp/src/MLIRCompiler.cpp:367-376 allocates and copies each input,
+ * :451-454 frees them), which the reference's JIT path has no way to avoid.
+ *
+ * bind_parameter copies `data` (contiguous row-major, host or device memory,
+ * `shape`/`rank` equal to the parameter's compiled type) into device memory
+ * on the current device and returns once the copy has landed. From then on a
+ * call of the function -- through its function pointer or
+ * execute_gpu_function -- that passes that same address (aligned + offset)
+ * with the same shape and contiguous rows, with that device current, reads
+ * the device copy in place: the operand is not copied in. The copy is a
+ * SNAPSHOT of the array at bind time: later writes to the array are not seen
+ * until it is bound again. Any other address runs as before (copied in).
+ * Binding again replaces the snapshot; unbind (index -1: every parameter of
+ * the function), clear() and destroy release it. index is the parameter's
+ * position in the FunctionDef (param_index maps a name to it). */
+int edsl_hip_module_bind_parameter(edsl_hip_module *m, const char *name, int index, const void *data,
+                                   const int64_t *shape, int rank);
+int edsl_hip_module_unbind_parameter(edsl_hip_module *m, const char *name, int index);
+int edsl_hip_module_param_index(edsl_hip_module *m, const char *name, const char *param, int *index);
+
 /* MLIRCompiler::getModuleIR counterpart: a text listing of the compiled
- * functions (signature and the dense form each was matched to). */
+ * functions -- signature, the dense form each was matched to, its layers and
+ * epilogues, resident parameters, and the kernels of its last run. */
 int edsl_hip_module_describe(edsl_hip_module *m, char *buf, size_t len);
 
 /* MLIRCompiler::getFailureIR counterpart: the message of the last failed

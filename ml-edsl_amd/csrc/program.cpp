@@ -543,6 +543,21 @@ struct Layer {
   float alpha = 0.0f;
 };
 
+// A parameter bound to a device-resident snapshot (bind_parameter): calls
+// that pass the same host address with the same layout read the snapshot in
+// place instead of copying the operand in.
+struct Binding {
+  const void* host = nullptr;  // address the snapshot was taken from
+  int64_t rows = 0, cols = 0;  // its layout: `rows` contiguous rows of `cols` (1-D: rows == 1)
+  std::shared_ptr<ResidentCopy> copy;
+};
+
+struct Bindings {
+  std::mutex mu;
+  std::map<int, Binding> by_param;  // parameter index -> binding
+  std::string last_plan;            // kernels of the function's last successful run
+};
+
 struct Program {
   std::string name;
   std::vector<Param> params;
@@ -552,6 +567,7 @@ struct Program {
   int slot = -1;               // trampoline slot
   int nargs = 0;               // flat scalar arguments of the memref calling convention
   std::string form;            // e.g. "relu(relu(X @ W1 + b1) @ W2 + b2)"
+  std::shared_ptr<Bindings> bound = std::make_shared<Bindings>();
 };
 
 const char* kDenseForms =
@@ -860,15 +876,55 @@ int arity_index(int nargs) {
   return -1;
 }
 
-// The layer operations of p over its bound operands (mats / vecs indexed by
-// parameter), run with the chain executor.
-void run_program(const Program& p, const std::vector<Mat>& mats, const std::vector<Vec>& vecs, const Mat& Y) {
+// The layer operations of p over its call operands (mats / vecs indexed by
+// parameter), run with the chain executor. A parameter with a device-resident
+// binding on the current device is read from its snapshot when the call
+// passes the address and layout the snapshot was taken from; any other
+// operand is copied in as usual. The snapshots are held until the
+// (synchronous) run has finished, so an unbind or rebind on another thread
+// cannot free one in use.
+void run_program(const Program& p, std::vector<Mat> mats, std::vector<Vec> vecs, const Mat& Y) {
+  std::vector<std::shared_ptr<ResidentCopy>> hold;
+  std::string resident;
+  {
+    std::lock_guard<std::mutex> lock(p.bound->mu);
+    if (!p.bound->by_param.empty()) {
+      const int dev = current_device();
+      for (auto& kv : p.bound->by_param) {
+        const int i = kv.first;
+        const Binding& b = kv.second;
+        if (b.copy->device != dev) continue;
+        bool hit = false;
+        if (p.params[i].type.shape.size() == 2) {
+          Mat& m = mats[i];
+          if (m.base == b.host && m.rows == b.rows && m.cols == b.cols && (m.rows <= 1 || m.ld == b.cols)) {
+            m.base = static_cast<char*>(b.copy->dev);
+            m.ld = b.copy->dev_ld;
+            hit = true;
+          }
+        } else {
+          Vec& v = vecs[i];
+          if (v.base == b.host && v.n == b.cols) {
+            v.base = static_cast<char*>(b.copy->dev);
+            hit = true;
+          }
+        }
+        if (hit) {
+          hold.push_back(b.copy);
+          resident += (resident.empty() ? "" : ",") + p.params[i].name;
+        }
+      }
+    }
+  }
   std::vector<LayerOp> ops;
   ops.reserve(p.layers.size());
   for (const Layer& L : p.layers)
     ops.push_back(LayerOp{L.x >= 0 ? &mats[L.x] : nullptr, &mats[L.w], L.b >= 0 ? &vecs[L.b] : nullptr, L.epi,
                           L.alpha});
   sync_dense_chain(p.dtype, ops.data(), (int)ops.size(), Y);
+  if (!resident.empty()) t_plan += " [resident: " + resident + "]";
+  std::lock_guard<std::mutex> lock(p.bound->mu);
+  p.bound->last_plan = t_plan;
 }
 
 void run_slot(int a, int s, const int64_t* v, int n) {
@@ -1001,7 +1057,7 @@ int edsl_hip_module_compile_function(edsl_hip_module* m, const void* bytes, size
     if (!m) fail(kErrArgument, "null module");
     auto p = std::make_shared<Program>(decode_function_def(bytes, len));
     std::lock_guard<std::mutex> lock(m->mu);
-    if (m->fns.count(p->name)) fail(kErrProgram, "function '%s' is already compiled", p->name.c_str());
+    if (m->fns.count(p->name)) fail(kErrArgument, "function '%s' is already compiled", p->name.c_str());
     p->slot = acquire_slot(p);
     m->fns[p->name] = p;
   });
@@ -1072,11 +1128,100 @@ int edsl_hip_module_describe(edsl_hip_module* m, char* buf, size_t len) {
         s += "%" + p.params[i].name + ": " + type_str(p.params[i].type);
       }
       s += ") -> " + type_str(p.ret) + "\n";
-      s += "  // " + p.form + " (" + (p.dtype == EDSL_DTYPE_F32 ? "f32" : "i32") +
-           "): one fused HIP launch, kernel chosen by shape at run time\n";
+      s += "  // form: " + p.form + " (" + (p.dtype == EDSL_DTYPE_F32 ? "f32" : "i32") + ", " +
+           std::to_string(p.layers.size()) + (p.layers.size() == 1 ? " layer" : " layers") + ")\n";
+      std::string h;
+      for (size_t li = 0; li < p.layers.size(); ++li) {
+        const Layer& L = p.layers[li];
+        static const char* kAct[] = {"", "relu", "leaky_relu"};
+        char line[256];
+        snprintf(line, sizeof(line), "  // layer %zu: %s @ %s%s%s%s -> one fused launch (epilogue %d%s)\n", li,
+                 L.x >= 0 ? p.params[L.x].name.c_str() : h.c_str(), p.params[L.w].name.c_str(),
+                 L.b >= 0 ? " + " : "", L.b >= 0 ? p.params[L.b].name.c_str() : "",
+                 (L.epi >> 1) ? (std::string(", then ") + kAct[L.epi >> 1]).c_str() : "", L.epi,
+                 (L.epi >> 1) == 2 ? (", alpha " + std::to_string(L.alpha)).c_str() : "");
+        s += line;
+        h = "h" + std::to_string(li);
+      }
+      std::lock_guard<std::mutex> block(p.bound->mu);
+      for (auto& b : p.bound->by_param)
+        s += "  // resident: %" + p.params[b.first].name + " on device " + std::to_string(b.second.copy->device) +
+             " (" + std::to_string(b.second.copy->bytes) + " bytes)\n";
+      if (!p.bound->last_plan.empty()) s += "  // last run: " + p.bound->last_plan + "\n";
     }
   }
   return copy_out(s, buf, len);
+}
+
+int edsl_hip_module_param_index(edsl_hip_module* m, const char* name, const char* param, int* index) {
+  return guarded([&] {
+    std::shared_ptr<Program> p;
+    {
+      if (!m) fail(kErrArgument, "null module");
+      std::lock_guard<std::mutex> lock(m->mu);
+      p = lookup(m, name);
+    }
+    if (!param) fail(kErrArgument, "null parameter name");
+    for (size_t i = 0; i < p->params.size(); ++i)
+      if (p->params[i].name == param) {
+        if (index) *index = (int)i;
+        return;
+      }
+    fail(kErrArgument, "function '%s' has no parameter '%s'", p->name.c_str(), param);
+  });
+}
+
+int edsl_hip_module_bind_parameter(edsl_hip_module* m, const char* name, int index, const void* data,
+                                   const int64_t* shape, int rank) {
+  return guarded([&] {
+    std::shared_ptr<Program> p;
+    {
+      if (!m) fail(kErrArgument, "null module");
+      std::lock_guard<std::mutex> lock(m->mu);
+      p = lookup(m, name);
+    }
+    if (index < 0 || index >= (int)p->params.size())
+      fail(kErrArgument, "function '%s' has %zu parameters, no parameter %d", p->name.c_str(), p->params.size(),
+           index);
+    const TypeSpec& t = p->params[index].type;
+    const char* nm = p->params[index].name.c_str();
+    if (t.kind != 3 || (t.shape.size() != 1 && t.shape.size() != 2))
+      fail(kErrArgument, "%s: only 1-D and 2-D tensor parameters can be bound, got %s", nm, type_str(t).c_str());
+    if (!shape && rank > 0) fail(kErrArgument, "null shape");
+    if (rank != (int)t.shape.size())
+      fail(kErrShape, "%s: rank %d, the function was compiled for rank %zu", nm, rank, t.shape.size());
+    for (int k = 0; k < rank; ++k)
+      if (shape[k] != t.shape[k])
+        fail(kErrShape, "%s: shape[%d] = %lld, the function was compiled for %lld", nm, k, (long long)shape[k],
+             (long long)t.shape[k]);
+    const int64_t rows = rank == 2 ? shape[0] : 1, cols = shape[rank - 1];
+    Binding b;
+    b.host = data;
+    b.rows = rows;
+    b.cols = cols;
+    b.copy = make_resident_copy(data, rows, cols, 4);
+    std::lock_guard<std::mutex> lock(p->bound->mu);
+    p->bound->by_param[index] = std::move(b);  // a replaced snapshot is freed once no call holds it
+  });
+}
+
+int edsl_hip_module_unbind_parameter(edsl_hip_module* m, const char* name, int index) {
+  return guarded([&] {
+    std::shared_ptr<Program> p;
+    {
+      if (!m) fail(kErrArgument, "null module");
+      std::lock_guard<std::mutex> lock(m->mu);
+      p = lookup(m, name);
+    }
+    if (index < -1 || index >= (int)p->params.size())
+      fail(kErrArgument, "function '%s' has %zu parameters, no parameter %d", p->name.c_str(), p->params.size(),
+           index);
+    std::lock_guard<std::mutex> lock(p->bound->mu);
+    if (index < 0)
+      p->bound->by_param.clear();
+    else
+      p->bound->by_param.erase(index);
+  });
 }
 
 int edsl_hip_module_last_failure(edsl_hip_module* m, char* buf, size_t len) {

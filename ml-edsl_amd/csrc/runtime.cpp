@@ -804,6 +804,46 @@ void sync_dense(int dtype, int epi, float alpha, const Mat& X, const Mat& W, con
   sync_dense_chain(dtype, &op, 1, Y);
 }
 
+int current_device() {
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  return dev;
+}
+
+ResidentCopy::~ResidentCopy() {
+  if (!dev) return;
+  int cur = -1;
+  const bool switch_dev = hipGetDevice(&cur) == hipSuccess && cur != device;
+  if (switch_dev) (void)hipSetDevice(device);
+  (void)hipFree(dev);  // the calls that read it were synchronous
+  if (switch_dev) (void)hipSetDevice(cur);
+  (void)hipGetLastError();
+}
+
+std::shared_ptr<ResidentCopy> make_resident_copy(const void* src, int64_t rows, int64_t cols, size_t esize) {
+  if (rows < 0 || cols < 0) fail(kErrShape, "negative size (%lld, %lld)", (long long)rows, (long long)cols);
+  if (!src && rows > 0 && cols > 0) fail(kErrArgument, "null data pointer");
+  std::lock_guard<std::mutex> lock(g_mu);  // the pinned staging ring is shared
+  auto c = std::make_shared<ResidentCopy>();
+  c->device = current_device();
+  c->rows = rows;
+  c->cols = cols;
+  c->dev_ld = (cols + 3) & ~int64_t(3);
+  c->bytes = std::max<size_t>((size_t)rows * (size_t)c->dev_ld * esize, 256);
+  check_hip(hipMalloc(&c->dev, c->bytes), "hipMalloc (resident parameter)");
+  if (rows > 0 && cols > 0) {
+    if (is_device_pointer(src, c->device)) {
+      check_hip(hipMemcpy2DAsync(c->dev, (size_t)c->dev_ld * esize, src, (size_t)cols * esize, (size_t)cols * esize,
+                                 rows, hipMemcpyDeviceToDevice, nullptr),
+                "hipMemcpy2DAsync (resident parameter)");
+    } else {
+      stage_h2d(c->dev, c->dev_ld, static_cast<const char*>(src), cols, rows, cols, esize, nullptr);
+    }
+    check_hip(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+  }
+  return c;
+}
+
 void dense_f32_launch(const float* X, int64_t ldx, const float* W, int64_t ldw, const float* bias, float* Y,
                       int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, float alpha, void* stream,
                       const FixedScratch* fixed) {
@@ -951,6 +991,28 @@ int edsl_hip_dense_f32_launch(const float* X, int64_t ldx, const float* W, int64
                               float* Y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
                               float alpha, void* stream) {
   return guarded([&] { dense_f32_launch(X, ldx, W, ldw, bias, Y, ldy, M, N, K, epilogue, alpha, stream, nullptr); });
+}
+
+int edsl_hip_dense_f32_launch_unfused(const float* X, int64_t ldx, const float* W, int64_t ldw,
+                                      const float* bias, float* Y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                                      int epilogue, float alpha, void* stream) {
+  return guarded([&] {
+    // The checks of dense_f32_launch, before the fill touches Y.
+    if (epilogue < 0 || epilogue > 5) fail(kErrArgument, "bad epilogue code %d", epilogue);
+    check_dims(M, N, K);
+    if (epi_has_bias(epilogue) && !bias && N > 0) fail(kErrArgument, "epilogue adds a bias but bias is null");
+    if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) fail(kErrArgument, "null operand");
+    if (K > 0 && M > 1 && ldx < K) fail(kErrStride, "ldx < K");
+    if (N > 0 && K > 1 && ldw < N) fail(kErrStride, "ldw < N");
+    if (N > 0 && M > 1 && ldy < N) fail(kErrStride, "ldy < N");
+    if (M <= 1) ldy = N;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (M > 0 && N > 0) check_hip(launch_fill_zero_f32(Y, ldy, (int)M, (int)N, s), "fill launch");
+    dense_f32_launch(X, ldx, W, ldw, nullptr, Y, ldy, M, N, K, EDSL_EPI_NONE, 0.f, stream, nullptr);
+    const std::string gemm_plan = t_plan;
+    if (M > 0 && N > 0) check_hip(launch_bias_act_f32(Y, ldy, bias, (int)M, (int)N, epilogue, alpha, s), "bias_act launch");
+    set_plan("unfused: fill | %s | bias_act epi=%d", gemm_plan.c_str(), epilogue);
+  });
 }
 
 int edsl_hip_dense_i32_launch(const int32_t* X, int64_t ldx, const int32_t* W, int64_t ldw,

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include <exception>
+#include <memory>
 #include <string>
 
 namespace edsl {
@@ -31,6 +32,7 @@ struct Failure {
 
 extern thread_local int t_err_code;
 extern thread_local std::string t_err_msg;
+extern thread_local std::string t_plan;  // edsl_hip_last_plan() of the calling thread
 
 [[noreturn]] void fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
@@ -91,6 +93,29 @@ struct LayerOp {
 // operands staged, only the last layer's output copied back), synchronous on
 // return.
 void sync_dense_chain(int dtype, const LayerOp* layers, int n, const Mat& Y);
+
+// A snapshot of a 2-D (or 1-D: rows == 1) operand held in device memory on
+// the device that was current when it was made, with rows padded to a
+// multiple of 4 elements and 16-byte alignment, so every kernel can read it in
+// place. The memory is freed when the last reference goes away.
+struct ResidentCopy {
+  int device = -1;
+  void* dev = nullptr;
+  int64_t rows = 0, cols = 0, dev_ld = 0;
+  size_t bytes = 0;
+  ResidentCopy() = default;
+  ResidentCopy(const ResidentCopy&) = delete;
+  ResidentCopy& operator=(const ResidentCopy&) = delete;
+  ~ResidentCopy();
+};
+
+// Copies rows x cols contiguous elements of esize bytes (host or device
+// memory) into a new ResidentCopy on the current device; returns once the
+// copy has landed. Throws Failure.
+std::shared_ptr<ResidentCopy> make_resident_copy(const void* src, int64_t rows, int64_t cols, size_t esize);
+
+// The current HIP device. Throws Failure.
+int current_device();
 
 // Device memory for the small-M kernel's split-K partials and staged X rows
 // that the caller fixes, in place of the library's grow-only per-device

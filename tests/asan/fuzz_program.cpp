@@ -40,7 +40,20 @@ int main(int argc, char** argv) {
   while (pos < (size_t)n) {
     size_t end = names.find('\n', pos);
     if (end == std::string::npos || end > (size_t)n) end = n;
-    (void)edsl_hip_module_get_function_pointer(m, names.substr(pos, end - pos).c_str());
+    const std::string fn = names.substr(pos, end - pos);
+    (void)edsl_hip_module_get_function_pointer(m, fn.c_str());
+    // binding: the index of a named parameter, a bind with the wrong shape
+    // (an error), a bind of the right shape when it is 1x1 .. 64x64, unbind
+    int idx = -1;
+    (void)edsl_hip_module_param_index(m, fn.c_str(), "X", &idx);
+    static float host[64 * 64 + 64];
+    for (int64_t d = 1; d <= 64; d *= 4) {
+      const int64_t shape[2] = {d, d};
+      (void)edsl_hip_module_bind_parameter(m, fn.c_str(), idx < 0 ? 0 : idx, host, shape, 2);
+      (void)edsl_hip_module_bind_parameter(m, fn.c_str(), 1, host, shape, 1);
+    }
+    edsl_hip_module_describe(m, buf, sizeof buf);
+    (void)edsl_hip_module_unbind_parameter(m, fn.c_str(), -1);
     pos = end + 1;
   }
   edsl_hip_module_clear(m);

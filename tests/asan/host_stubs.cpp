@@ -13,6 +13,27 @@ namespace rt {
 
 thread_local int t_err_code = 0;
 thread_local std::string t_err_msg;
+thread_local std::string t_plan;
+
+int current_device() { return 0; }
+
+// Host memory stands in for the device copy (the decoder only passes it on).
+ResidentCopy::~ResidentCopy() { delete[] static_cast<char*>(dev); }
+
+std::shared_ptr<ResidentCopy> make_resident_copy(const void* src, int64_t rows, int64_t cols, size_t esize) {
+  if (rows < 0 || cols < 0) fail(kErrShape, "negative size");
+  auto c = std::make_shared<ResidentCopy>();
+  c->device = 0;
+  c->rows = rows;
+  c->cols = cols;
+  c->dev_ld = (cols + 3) & ~int64_t(3);
+  c->bytes = (size_t)rows * (size_t)c->dev_ld * esize + 256;
+  c->dev = new char[c->bytes]();
+  for (int64_t r = 0; r < rows; ++r)
+    memcpy(static_cast<char*>(c->dev) + r * c->dev_ld * esize, static_cast<const char*>(src) + r * cols * esize,
+           (size_t)cols * esize);
+  return c;
+}
 
 void fail(int code, const char* fmt, ...) {
   char buf[512];

@@ -123,3 +123,117 @@ def test_reference_program_runs_three_ways(case, torch_cuda):
         call = case["execute_gpu_function"]
         assert call["input_shapes"] == case["param_shapes"] and call["element_size"] == 4
     comp.clear()
+
+
+# --------------------------------------------- device-resident parameters
+def _call_pointer(ptr, args, out):
+    types, vals = [], []
+    for a in list(args) + [out]:
+        t, v = _descriptor_types_and_values(a)
+        types += t
+        vals += v
+    _native.lib().edsl_hip_clear_error()
+    ctypes.CFUNCTYPE(None, *types)(ptr)(*vals)
+    _native.raise_on_error("function pointer")
+
+
+def _layer_inputs(M, K, N, seed):
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.float32(np.sqrt(K))).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, N).astype(np.float32)
+    return X, W, b
+
+
+@pytest.mark.parametrize("M, K, N", [(16, 8192, 8192), (300, 257, 130), (2048, 1024, 1024)],
+                         ids=["c4", "odd", "pipelined"])
+def test_bound_parameters_match_unbound_calls_and_the_oracle(M, K, N, torch_cuda):
+    """W and b bound as device-resident snapshots: calls through the function
+    pointer and execute_gpu_function that pass the same arrays read them in
+    place ([resident: W,b] in the plan) and give the unbound result bit for
+    bit; rebinding to new values changes the result; another array of the
+    same shape is copied in as usual; unbinding goes back to copying."""
+    from mlir_edsl_hip import wire
+    comp = MLIRCompiler()
+    name = "dense_bound"
+    comp.compile_function(wire.dense_layer(name, M, K, N))
+    ptr = comp.get_function_pointer(name)
+    X, W, b = _layer_inputs(M, K, N, M + K)
+    ref = oracle.dense_f32(X, W, b, "relu")
+    plain = np.empty((M, N), np.float32)
+    _call_pointer(ptr, (X, W, b), plain)
+    assert "resident" not in _native.last_plan()
+    _check(plain, ref, K)
+
+    comp.bind_parameter(name, "W", W)
+    comp.bind_parameter(name, 2, b)
+    bound = np.empty((M, N), np.float32)
+    _call_pointer(ptr, (X, W, b), bound)
+    assert _native.last_plan().endswith("[resident: W,b]"), _native.last_plan()
+    assert np.array_equal(bound.view(np.uint32), plain.view(np.uint32))
+    raw = comp.execute_gpu_function(name, [(a.ctypes.data, list(a.shape)) for a in (X, W, b)], [M, N], 4)
+    assert _native.last_plan().endswith("[resident: W,b]"), _native.last_plan()
+    assert np.array_equal(np.frombuffer(raw, np.float32).reshape(M, N), plain)
+    desc = comp.get_module_ir()
+    assert "// resident: %W on device" in desc and "// resident: %b on device" in desc
+    assert "// last run: " in desc and "[resident: W,b]" in desc
+
+    # The snapshot is what was bound: writing the array does not change it ...
+    W2 = (W * np.float32(-0.5)).astype(np.float32)
+    W[...] = W2
+    stale = np.empty((M, N), np.float32)
+    _call_pointer(ptr, (X, W, b), stale)
+    assert np.array_equal(stale, plain)
+    # ... until it is bound again.
+    comp.bind_parameter(name, "W", W)
+    rebound = np.empty((M, N), np.float32)
+    _call_pointer(ptr, (X, W, b), rebound)
+    ref2 = oracle.dense_f32(X, W2, b, "relu")
+    _check(rebound, ref2, K)
+    assert not np.array_equal(rebound, plain)
+
+    # A different array of the same shape is copied in, not mistaken for W.
+    W3 = np.ascontiguousarray(W2[::-1])
+    other = np.empty((M, N), np.float32)
+    _call_pointer(ptr, (X, W3, b), other)
+    assert _native.last_plan().endswith("[resident: b]"), _native.last_plan()
+    _check(other, oracle.dense_f32(X, W3, b, "relu"), K)
+
+    comp.unbind_parameter(name)
+    again = np.empty((M, N), np.float32)
+    _call_pointer(ptr, (X, W, b), again)
+    assert "resident" not in _native.last_plan()
+    assert np.array_equal(again, rebound)
+    comp.clear()
+
+
+def test_bound_parameters_in_a_chain_and_with_device_operands(torch_cuda):
+    """A two-layer chain with both weights bound, called with host X; then
+    with device tensors, which never match a host snapshot."""
+    from mlir_edsl_hip import wire
+    torch = torch_cuda
+    comp = MLIRCompiler()
+    name = "chain_bound"
+    comp.compile_function(wire.dense_program(name, ("X", 64, 512), [wire.Layer("W1", 256, "b1", "relu"),
+                                                                    wire.Layer("W2", 96, "b2", "leaky", 0.1)]))
+    rng = np.random.default_rng(5)
+    X = rng.standard_normal((64, 512), dtype=np.float32)
+    W1 = (rng.standard_normal((512, 256), dtype=np.float32) / 23).astype(np.float32)
+    b1 = rng.uniform(-0.1, 0.1, 256).astype(np.float32)
+    W2 = (rng.standard_normal((256, 96), dtype=np.float32) / 16).astype(np.float32)
+    b2 = rng.uniform(-0.1, 0.1, 96).astype(np.float32)
+    args = (X, W1, b1, W2, b2)
+    ref = _reference(comp.function_form(name), list(args))
+    for p in ("W1", "W2"):
+        comp.bind_parameter(name, p, args[comp._param_index(name, p)])
+    out = np.empty((64, 96), np.float32)
+    _call_pointer(comp.get_function_pointer(name), args, out)
+    assert "[resident: W1,W2]" in _native.last_plan(), _native.last_plan()
+    _check(out, ref, 512)
+    dargs = [torch.from_numpy(a).cuda() for a in args]
+    dout = torch.empty((64, 96), device="cuda")
+    _call_pointer(comp.get_function_pointer(name), dargs, dout)
+    torch.cuda.synchronize()
+    assert "resident" not in _native.last_plan()
+    _check(dout.cpu().numpy(), ref, 512)
+    comp.clear()

@@ -257,3 +257,195 @@ def test_shape_mismatches_are_rejected(compiler):
         compiler.compile_function(_matmul_def("bad_ret", [8, 4], [4, 2], [8, 3]))
     with pytest.raises(RuntimeError, match="f32 or i32"):
         compiler.compile_function(_matmul_def("bad_elem", [8, 4], [4, 2], [8, 2], kind=2))
+
+
+# ------------------------------------------------ coexistence with the reference
+class _StubReferenceCompiler:
+    """Stands in for the reference's pybind MLIRCompiler (reference
+    cpp/src/python_bindings.cpp:8-98): records what it is handed."""
+
+    def __init__(self):
+        self.fns: dict[str, str] = {}
+        self.target = "cpu"
+        self.injected = False
+        self.opt = None
+        self.capture = False
+
+    def compile_function(self, data):
+        assert data[0] == 0x0A  # FunctionDef.name, field 1
+        name = bytes(data[2:2 + data[1]]).decode()
+        if name in self.fns:
+            raise RuntimeError(f"duplicate {name}")
+        self.fns[name] = self.target
+
+    def get_function_pointer(self, name):
+        if self.injected:
+            raise RuntimeError("Lowering pipeline failed: stub")
+        return 0x5000 + sorted(self.fns).index(name)
+
+    def has_function(self, name):
+        return name in self.fns
+
+    def list_functions(self):
+        return sorted(self.fns)
+
+    def get_module_ir(self):
+        return "module { // stub reference }\n"
+
+    def clear(self):
+        self.fns.clear()
+        self.injected = False
+
+    def get_lowering_snapshots(self):
+        return [("stub-pass", "ir")] if self.capture else []
+
+    def enable_snapshot_capture(self):
+        self.capture = True
+
+    def get_failure_ir(self):
+        return "func.func @__test_failure_inject__" if self.injected else ""
+
+    def inject_test_failure(self):
+        self.injected = True
+
+    def set_optimization_level(self, level):
+        self.opt = level
+
+    def set_target(self, target):
+        self.target = target
+
+    def execute_gpu_function(self, name, inputs, output_shape, element_size):
+        return b"stub:" + name.encode()
+
+
+class _StubReferenceModule:
+    MLIRCompiler = _StubReferenceCompiler
+
+
+@pytest.fixture
+def with_reference():
+    from mlir_edsl_hip import _mlir_backend as mb
+    mb.set_reference_backend(_StubReferenceModule)
+    try:
+        c = MLIRCompiler()
+        yield c
+        c.clear()
+    finally:
+        mb._reference_override = mb._UNSET
+
+
+def _case(fixture):
+    return next(c for c in _cases() if c["fixture"] == fixture)
+
+
+def test_scalar_and_dense_functions_in_one_session(with_reference):
+    """Dense target="gpu" programs run on the HIP kernels; programs outside the
+    dense path, and anything compiled for target="cpu", go to the reference
+    compiler; later calls are routed by name."""
+    c = with_reference
+    dense, scalar, mm = _case("dense_relu_f32"), _case("reject_scalar_function"), _case("matmul_f32")
+    c.set_target("gpu")
+    c.compile_function(_bytes(dense))
+    c.compile_function(_bytes(scalar))  # rejected by the HIP module -> reference
+    assert c.backend_of(dense["function"]) == "hip"
+    assert c.backend_of(scalar["function"]) == "reference"
+    assert c.reference.fns == {scalar["function"]: "gpu"}
+    c.set_target("cpu")
+    c.compile_function(_bytes(mm))  # CPU JIT requested -> reference, although it is dense
+    assert c.backend_of(mm["function"]) == "reference" and c.reference.fns[mm["function"]] == "cpu"
+    assert c.list_functions() == sorted([dense["function"], scalar["function"], mm["function"]])
+    assert all(c.has_function(n) for n in c.list_functions())
+    assert c.get_function_pointer(scalar["function"]) == 0x5000 + sorted(c.reference.fns).index(scalar["function"])
+    hip_ptr = c.get_function_pointer(dense["function"])
+    assert hip_ptr and hip_ptr < 0x5000 or hip_ptr > 0x6000
+    assert c.execute_gpu_function(mm["function"], [], [1], 4) == b"stub:" + mm["function"].encode()
+    ir = c.get_module_ir()
+    assert f"func @{dense['function']}(" in ir and "stub reference" in ir
+    c.set_optimization_level(3)
+    assert c.reference.opt == 3
+    c.clear()
+    assert c.list_functions() == [] and c.reference.fns == {}
+
+
+def test_dense_errors_are_not_delegated(with_reference):
+    """A duplicate dense function is an error of the HIP module, not a reason
+    to hand the program to the reference compiler."""
+    c = with_reference
+    c.set_target("gpu")
+    dense = _case("dense_relu_f32")
+    c.compile_function(_bytes(dense))
+    with pytest.raises(RuntimeError, match="already compiled"):
+        c.compile_function(_bytes(dense))
+    assert c.reference.fns == {}
+
+
+def test_injected_failure_goes_to_the_reference_compiler(with_reference):
+    # reference tests/core/test_ir_inspection.py:22-36: the scalar function runs on the reference
+    c = with_reference
+    c.set_target("cpu")
+    scalar = _case("reject_scalar_function")
+    c.compile_function(_bytes(scalar))
+    c.inject_test_failure()
+    with pytest.raises(RuntimeError, match="Lowering pipeline failed"):
+        c.get_function_pointer(scalar["function"])
+    assert "__test_failure_inject__" in c.get_failure_ir()
+
+
+def test_snapshots_are_what_the_module_did(with_reference):
+    c = with_reference
+    c.set_target("gpu")
+    c.enable_snapshot_capture()
+    dense = _case("chain_relu_then_leaky")
+    c.compile_function(_bytes(dense))
+    c.get_function_pointer(dense["function"])
+    snaps = dict(c.get_lowering_snapshots())
+    text = snaps[f"match:{dense['function']}"]
+    assert "leaky_relu(relu(X @ W1 + b1) @ W2, 0.1)" in text and "layer 1: x=-1 w=3 b=-1 epilogue=4" in text
+    assert snaps["stub-pass"] == "ir"
+
+
+def test_without_a_reference_module_other_programs_are_rejected():
+    from mlir_edsl_hip import _mlir_backend as mb
+    mb.set_reference_backend(None)
+    try:
+        c = MLIRCompiler()
+        assert c.reference is None
+        with pytest.raises(RuntimeError, match=_case("reject_scalar_function")["expected"]["reject"]):
+            c.compile_function(_bytes(_case("reject_scalar_function")))
+        c.set_target("cpu")  # no CPU JIT to hand it to: dense functions run on the HIP kernels
+        c.compile_function(_bytes(_case("matmul_f32")))
+        assert c.backend_of(_case("matmul_f32")["function"]) == "hip"
+    finally:
+        mb._reference_override = mb._UNSET
+
+
+def test_module_text_describes_the_match(compiler):
+    case = _case("chain_relu_then_leaky")
+    compiler.compile_function(_bytes(case))
+    ir = compiler.get_module_ir()
+    assert "// form: leaky_relu(relu(X @ W1 + b1) @ W2, 0.1) (f32, 2 layers)" in ir
+    assert "// layer 0: X @ W1 + b1, then relu" in ir and "// layer 1: h0 @ W2, then leaky_relu" in ir
+
+
+# -------------------------------------------- binding: argument validation
+def test_bind_parameter_validates_before_any_device_call(compiler):
+    case = _case("dense_relu_f32")  # X[16,64], W[64,32], b[32]
+    compiler.compile_function(_bytes(case))
+    name = case["function"]
+    with pytest.raises(RuntimeError, match=r"W: shape\[1\] = 33, the function was compiled for 32"):
+        compiler.bind_parameter(name, "W", np.zeros((64, 33), np.float32))
+    with pytest.raises(RuntimeError, match="no parameter 7"):
+        compiler.bind_parameter(name, 7, np.zeros((64, 32), np.float32))
+    with pytest.raises(RuntimeError, match="has no parameter 'Q'"):
+        compiler.bind_parameter(name, "Q", np.zeros((64, 32), np.float32))
+    with pytest.raises(RuntimeError, match="rank 2, the function was compiled for rank 1"):
+        compiler.bind_parameter(name, "b", np.zeros((1, 32), np.float32))
+    with pytest.raises(ValueError, match="C-contiguous"):
+        compiler.bind_parameter(name, "W", np.zeros((32, 64), np.float32).T)
+    with pytest.raises(TypeError, match="element size 8"):
+        compiler.bind_parameter(name, "W", np.zeros((64, 32), np.float64))
+    with pytest.raises(RuntimeError, match="Function not compiled: nope"):
+        compiler.bind_parameter("nope", 0, np.zeros((64, 32), np.float32))
+    compiler.unbind_parameter(name)  # nothing bound: a no-op
+    with pytest.raises(RuntimeError, match="no parameter 5"):
+        compiler.unbind_parameter(name, 5)
