@@ -67,6 +67,18 @@ int edsl_hip_dense_f32_launch_noalloc(const float *X, int64_t ldx, const float *
                                       int64_t N, int64_t K, int epilogue, float alpha,
                                       void *stream);
 
+/* The reference's unfused GPU sequence for the same layer, on this
+ * library's kernels: a fill of Y with zeros (linalg.fill), the GEMM with no
+ * epilogue, then a separate elementwise bias + activation kernel over Y --
+ * the three launches the reference's GPU pipeline runs per dense layer
+ * (reference cpp/src/MLIRLowering.cpp:495-518,
+ * tests/gpu/test_gpu_execution.py:149-154). For measuring what fusion saves;
+ * results equal edsl_hip_dense_f32_launch's bit for bit. */
+int edsl_hip_dense_f32_launch_unfused(const float *X, int64_t ldx, const float *W, int64_t ldw,
+                                      const float *bias, float *Y, int64_t ldy, int64_t M,
+                                      int64_t N, int64_t K, int epilogue, float alpha,
+                                      void *stream);
+
 /* Y[M,N] = epilogue(X[M,K] @ W[K,N] (+ bias)), i32 wrapping arithmetic.
  * Leaky epilogues are rejected (float-only in the reference). */
 int edsl_hip_dense_i32_launch(const int32_t *X, int64_t ldx, const int32_t *W, int64_t ldw,

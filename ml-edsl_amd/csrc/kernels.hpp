@@ -116,4 +116,11 @@ hipError_t launch_gemm_i8(int epi, GemmI32Args args, hipStream_t stream, int var
 // Exact wrapping i32 GEMM on the vector ALUs: any shape, any alignment.
 hipError_t launch_gemm_i32_valu(int epi, GemmI32Args args, hipStream_t stream);
 
+// ------------------------------------- the reference's unfused GPU sequence
+// Y = 0 (linalg.fill), and Y = epilogue(Y (+ bias)) in place (the bias /
+// activation generic), for comparison with the fused kernels.
+hipError_t launch_fill_zero_f32(float* Y, int64_t ldy, int M, int N, hipStream_t stream);
+hipError_t launch_bias_act_f32(float* Y, int64_t ldy, const float* bias, int M, int N, int epi, float alpha,
+                               hipStream_t stream);
+
 }  // namespace edsl

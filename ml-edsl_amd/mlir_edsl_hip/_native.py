@@ -60,6 +60,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.edsl_hip_dense_f32_launch.restype = c_int
     L.edsl_hip_dense_f32_launch_noalloc.argtypes = L.edsl_hip_dense_f32_launch.argtypes
     L.edsl_hip_dense_f32_launch_noalloc.restype = c_int
+    L.edsl_hip_dense_f32_launch_unfused.argtypes = L.edsl_hip_dense_f32_launch.argtypes
+    L.edsl_hip_dense_f32_launch_unfused.restype = c_int
     L.edsl_hip_dense_i32_launch.argtypes = [vp, i64, vp, i64, vp, vp, i64, i64, i64, i64, c_int, vp]
     L.edsl_hip_dense_i32_launch.restype = c_int
     L.edsl_hip_last_plan.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
