@@ -5,20 +5,35 @@ Headline (BASELINE.json metric): fused fp32 matmul+bias+ReLU at M=N=K=4096
 (workload c3), in TFLOP/s and as a fraction of the dense fp32 MFMA peak.
 Secondary lines (same run): the M=16, K=N=8192 layer in GB/s (c4, W rotated
 over 3 buffers so the 256 MB Infinity Cache cannot serve it), the integer
-layer 2048^3 (c5), 1024^3 (c2), the 256^3 matmul (c1), and one GPU's share
-of c4 and c3 column-sharded over 8 GPUs (c4s8: N=1024, W rotated over 12
-buffers; c3s8: N=512).
+layer 2048^3 (c5, X and W rotated over 10 buffer pairs; the cache-resident
+figure beside it), 1024^3 (c2, fused and the reference's unfused
+three-launch sequence), the 256^3 matmul (c1), and one GPU's share of c4 and
+c3 column-sharded over 8 GPUs (c4s8: N=1024, W rotated over 12 buffers;
+c3s8: N=512).
 
 A step is one call of the dense layer on device-resident inputs (the
 C-ABI launch entry point, enqueued on torch's current stream). W warmup
 steps, then K timed steps between two device synchronisations (the wall
-clock gives `value`). A second pass enqueues K more steps behind a short
-spin kernel, so the GPU never waits on the host, between two HIP events on
-the same stream: their device time / K is the average launch duration used
-for the roofline. A third pass with one event pair per launch reports the
-spread.
-The CPU baseline times the oracle (a C restatement of the reference CPU-JIT
-schedule) on a row sample of the same workload, on this host's cores.
+clock gives `value`; two events on the stream give the same region's device
+span, region_ms_per_step). A second pass enqueues K more steps behind a
+short spin kernel, so the GPU never waits on the host, between two HIP
+events on the same stream: their device time / K is the average launch
+duration used for the roofline. A third pass with one event pair per launch
+reports the spread.
+
+Every workload's inputs are generated and uploaded before the first
+measurement, and the workloads run back to back with the headline last: the
+GPU's clock takes ~20 ms of sustained load to ramp up from idle (measured:
+the first c3 launches after an idle second take 1140-1220 us, later ones
+980 us), so a headline measured first, after a few ms of warmup, would time
+the ramp.
+
+Then, on host buffers (never `value`): the reference's GPU calling pattern
+(H2D + kernels + D2H per call) for every workload, c4 with its weights bound
+device-resident, and the reference's own GPU benchmark points (matmul and
+dense at 256, 512, 1024). Last, the CPU baseline: the oracle (a C
+restatement of the reference CPU-JIT schedule) on a row sample of each
+workload, on this host's cores.
 
 Prints one JSON line on stdout.
 """
@@ -45,6 +60,17 @@ PEAK = {  # MI355X published dense peaks
 KERNEL_NAMES = {"c1": "gemm_f32_kernel", "c2": "gemm_f32_kernel", "c3": "gemm_f32_kernel",
                 "c4": "gemv_f32_kernel + gemv_reduce_kernel", "c5": "narrow_i8_kernel + gemm_i8_ksplit_kernel",
                 "c3s8": "gemm_f32_kernel", "c4s8": "gemv_f32_kernel + gemv_reduce_kernel"}
+UNITS = {"c1": "TFLOP/s", "c2": "TFLOP/s", "c3": "TFLOP/s", "c4": "GB/s", "c5": "TOP/s",
+         "c3s8": "TFLOP/s", "c4s8": "GB/s"}
+# (steps, warmup, input sets rotated) of each workload when it is not the
+# headline. The inputs that would otherwise be served from the 256 MB Infinity
+# Cache are rotated past it: c4 W 3 x 256 MiB, c4s8 W 12 x 32 MiB, c5 X and W
+# 10 x 32 MiB.
+SECONDARY_PLAN = {"c4": (200, 20, 3), "c5": (200, 20, 10), "c2": (100, 20, 1), "c1": (200, 20, 1),
+                  "c3": (50, 20, 1), "c3s8": (100, 100, 1), "c4s8": (300, 30, 12)}
+ROTATE_X = {"c5"}           # workloads whose X is rotated together with W
+RESIDENT_TOO = {"c5"}       # also measured without rotation (inputs cache-resident)
+UNFUSED_TOO = {"c2", "c3"}  # also timed as the reference's unfused three-launch sequence
 
 
 def log(msg: str) -> None:
@@ -70,25 +96,52 @@ def sleep_cycles_per_s() -> float:
     return _SLEEP_RATE
 
 
-def measure(wname: str, steps: int, warmup: int, rotate: int = 1) -> dict:
+class Prepared:
+    """A workload's host arrays and their device copies (rotated sets)."""
+
+    def __init__(self, wname: str, rotate: int):
+        import torch
+        from mlir_edsl_hip.inputs import WORKLOADS, make_inputs
+        self.w = WORKLOADS[wname]
+        self.name = wname
+        self.arrays = make_inputs(self.w)
+        dev = [torch.from_numpy(a).cuda() for a in self.arrays]
+        self.X, self.W = dev[0], dev[1]
+        self.b = dev[2] if len(dev) > 2 else None
+        self.rotate = rotate
+        self.Ws = [self.W] + [self.W.clone() for _ in range(rotate - 1)]
+        self.Xs = [self.X] + ([self.X.clone() for _ in range(rotate - 1)] if wname in ROTATE_X else [])
+        dtype = torch.float32 if self.w.dtype == "f32" else torch.int32
+        self.Y = torch.empty((self.w.M, self.w.N), dtype=dtype, device="cuda")
+
+    def free(self) -> None:
+        import torch
+        del self.X, self.W, self.Ws, self.Xs, self.Y, self.b
+        torch.cuda.empty_cache()
+
+
+def measure(p: Prepared, steps: int, warmup: int, rotate: int | None = None, unfused: bool = False) -> dict:
     import torch
 
     from mlir_edsl_hip import _native
     from mlir_edsl_hip.device import dense_launch
-    from mlir_edsl_hip.inputs import WORKLOADS, make_inputs
 
-    w = WORKLOADS[wname]
-    arrays = make_inputs(w)
-    dev = [torch.from_numpy(a).cuda() for a in arrays]
-    X, W = dev[0], dev[1]
-    b = dev[2] if len(dev) > 2 else None
-    Ws = [W] + [W.clone() for _ in range(rotate - 1)]
-    dtype = torch.float32 if w.dtype == "f32" else torch.int32
-    Y = torch.empty((w.M, w.N), dtype=dtype, device="cuda")
-    epi = _native.EPI_BIAS_RELU if w.pattern == "dense_relu" else _native.EPI_NONE
+    rotate = p.rotate if rotate is None else rotate
+    epi = _native.EPI_BIAS_RELU if p.w.pattern == "dense_relu" else _native.EPI_NONE
+    nx = min(rotate, len(p.Xs))
+    L = _native.lib()
+    M, K, N = p.w.M, p.w.K, p.w.N
 
     def launch(i: int) -> None:
-        dense_launch(X, Ws[i % rotate], b, Y, epi)
+        if unfused:
+            X, W = p.Xs[i % nx], p.Ws[i % rotate]
+            rc = L.edsl_hip_dense_f32_launch_unfused(X.data_ptr(), K, W.data_ptr(), N, p.b.data_ptr(),
+                                                     p.Y.data_ptr(), N, M, N, K, epi, 0.0,
+                                                     torch.cuda.current_stream().cuda_stream)
+            if rc != 0:
+                _native.raise_on_error("unfused launch")
+        else:
+            dense_launch(p.Xs[i % nx], p.Ws[i % rotate], p.b, p.Y, epi)
 
     for i in range(warmup):
         launch(i)
@@ -96,7 +149,7 @@ def measure(wname: str, steps: int, warmup: int, rotate: int = 1) -> dict:
     plan = _native.last_plan()
     # Timed region (the contract's): K steps between two synchronisations;
     # the wall clock gives `value`. Two events on the stream record its device
-    # span as well (reported as region_ms_per_step).
+    # span as well (region_ms_per_step).
     region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -107,7 +160,7 @@ def measure(wname: str, steps: int, warmup: int, rotate: int = 1) -> dict:
     region[1].record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    wall_region_ms = region[0].elapsed_time(region[1]) / steps
+    region_ms = region[0].elapsed_time(region[1]) / steps
     # Device time per launch with the GPU never waiting on the host: a short
     # spin kernel holds the stream while the K launches are enqueued behind
     # it, and the events bracket only the K launches. (When the host issues
@@ -132,37 +185,26 @@ def measure(wname: str, steps: int, warmup: int, rotate: int = 1) -> dict:
         ends[i].record()
     torch.cuda.synchronize()
     kms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    res = {
-        "workload": wname,
+    return {
+        "workload": p.name,
         "ms_per_step": (t1 - t0) * 1e3 / steps,
         "kernel_ms_mean": device_ms,
-        "region_ms_per_step": wall_region_ms,
+        "region_ms_per_step": region_ms,
         "event_pair_ms_median": statistics.median(kms),
         "event_pair_ms_min": min(kms),
         "plan": plan,
         "rotate_w": rotate,
+        "rotate_x": nx,
     }
-    del X, W, Ws, Y, dev
-    torch.cuda.empty_cache()
-    return res
 
 
-def measure_host_path(wname: str, calls: int) -> dict:
-    """The reference's GPU calling pattern: host arrays in, host array out,
-    through the memref-descriptor C ABI (include/edsl_hip.h). Each call copies
-    the operands to the device, runs the kernels and copies Y back."""
-    from mlir_edsl_hip import backend
-    from mlir_edsl_hip.inputs import WORKLOADS, make_inputs
-
-    w = WORKLOADS[wname]
-    arrays = make_inputs(w)
-    backend.run(w.pattern, *arrays)  # first call sizes the staging buffers
-    t0 = time.perf_counter()
-    for _ in range(calls):
-        backend.run(w.pattern, *arrays)
-    t = (time.perf_counter() - t0) / calls
-    return {"value": round(step_value(wname, t), 3), "unit": UNITS[wname], "ms_per_call": round(t * 1e3, 4),
-            "calls": calls, "what": "host numpy buffers through the memref-ABI entry: H2D + kernels + D2H"}
+def step_value(wname: str, step_s: float) -> float:
+    """Whole-step throughput in the workload's unit."""
+    from mlir_edsl_hip.inputs import WORKLOADS
+    wl = WORKLOADS[wname]
+    if UNITS[wname] == "GB/s":
+        return wl.compulsory_bytes / step_s / 1e9
+    return wl.flops / step_s / 1e12
 
 
 def load_traffic() -> dict:
@@ -199,18 +241,117 @@ def roofline_for(wname: str, r: dict, traffic: dict) -> dict:
             "kernel": KERNEL_NAMES[wname], "algorithmic_flops": w.flops}
 
 
+# ------------------------------------------------------------ host buffers
+def _mean_call_s(fn, warmup: int, calls: int) -> float:
+    for _ in range(warmup):
+        fn()
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        fn()
+    return (time.perf_counter() - t0) / calls
+
+
+def measure_host_path(wname: str, arrays, calls: int) -> dict:
+    """The reference's GPU calling pattern: host arrays in, host array out,
+    through the memref-descriptor C ABI (include/edsl_hip.h). Each call copies
+    the operands to the device, runs the kernels and copies Y back."""
+    from mlir_edsl_hip import backend
+    w_pattern = {"c1": "matmul"}.get(wname, "dense_relu")
+    t = _mean_call_s(lambda: backend.run(w_pattern, *arrays), 1, calls)
+    return {"value": round(step_value(wname, t), 3), "unit": UNITS[wname], "ms_per_call": round(t * 1e3, 4),
+            "calls": calls, "what": "host numpy buffers through the memref-ABI entry: H2D + kernels + D2H"}
+
+
+def _gpu_call(comp, name, arrays, out_shape):
+    """The reference backend's execute_gpu_function marshalling (reference
+    mlir_edsl/backend.py:248-271): (pointer, shape) pairs, raw bytes back,
+    copied into a fresh array."""
+    import numpy as np
+    inputs = [(a.ctypes.data, list(a.shape)) for a in arrays]
+    raw = comp.execute_gpu_function(name, inputs, list(out_shape), 4)
+    return np.frombuffer(raw, dtype=arrays[0].dtype).reshape(out_shape).copy()
+
+
+def measure_resident_host_path(wname: str, arrays, calls: int) -> dict:
+    """The drop-in compiler (FunctionDef -> MLIRCompiler) called the way the
+    reference front end calls execute_gpu_function, first as is (every
+    operand copied in) and then with W and b bound device-resident: only X
+    goes up and Y comes down per call."""
+    from mlir_edsl_hip import _native, wire
+    from mlir_edsl_hip._mlir_backend import MLIRCompiler
+    from mlir_edsl_hip.inputs import WORKLOADS
+    w = WORKLOADS[wname]
+    comp = MLIRCompiler()
+    name = f"bench_{wname}_resident"
+    comp.compile_function(wire.dense_layer(name, w.M, w.K, w.N, dtype=w.dtype))
+    shape = (w.M, w.N)
+    t_copy = _mean_call_s(lambda: _gpu_call(comp, name, arrays, shape), 1, calls)
+    t0 = time.perf_counter()
+    comp.bind_parameter(name, "W", arrays[1])
+    comp.bind_parameter(name, "b", arrays[2])
+    t_bind = time.perf_counter() - t0
+    t_res = _mean_call_s(lambda: _gpu_call(comp, name, arrays, shape), 2, calls * 4)
+    plan = _native.last_plan()
+    comp.clear()
+    return {"value": round(step_value(wname, t_res), 3), "unit": UNITS[wname], "ms_per_call": round(t_res * 1e3, 4),
+            "calls": calls * 4, "plan": plan, "bind_ms": round(t_bind * 1e3, 2),
+            "unbound_ms_per_call": round(t_copy * 1e3, 4),
+            "what": "MLIRCompiler.execute_gpu_function on host arrays with W and b bound device-resident "
+                    "(bind_parameter): X H2D + kernels + Y D2H per call; unbound_ms_per_call copies every "
+                    "operand, as the reference does"}
+
+
+def reference_gpu_points() -> list:
+    """The reference's GPU benchmark (reference tests/gpu/test_gpu_benchmark.py:
+    matmul and dense relu(X @ W + b) at 256, 512, 1024, np.random.rand inputs,
+    3 warmup calls, mean wall-clock ms over 10) through the drop-in compiler,
+    called the way the reference front end calls execute_gpu_function."""
+    import numpy as np
+    from mlir_edsl_hip import wire
+    from mlir_edsl_hip._mlir_backend import MLIRCompiler
+    comp = MLIRCompiler()
+    points = []
+    for kind in ("matmul", "dense"):
+        for n in (256, 512, 1024):
+            name = f"ref_bench_{kind}_{n}"
+            comp.compile_function(wire.dense_layer(name, n, n, n, bias=kind == "dense",
+                                                   act="relu" if kind == "dense" else "none"))
+            rng = np.random.default_rng(n)
+            arrays = [rng.random((n, n), dtype=np.float32), rng.random((n, n), dtype=np.float32)]
+            if kind == "dense":
+                arrays.append(rng.random(n, dtype=np.float32))
+            t = _mean_call_s(lambda: _gpu_call(comp, name, arrays, (n, n)), 3, 10)
+            points.append({"kind": kind, "size": n, "ms_per_call": round(t * 1e3, 4),
+                           "tflops": round(2 * n ** 3 / t / 1e12, 4)})
+    comp.clear()
+    return points
+
+
+# --------------------------------------------------------------- CPU side
 def cpu_model() -> str:
+    """The host CPU: model name, family / model / stepping, logical CPUs on
+    the host and in this process's affinity set."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" in line:
+                    k, v = (s.strip() for s in line.split(":", 1))
+                    if k in ("model name", "cpu family", "model", "stepping", "cpu MHz", "cpu cores",
+                             "siblings") and k not in info:
+                        info[k] = v
     except OSError:
         pass
-    return "unknown"
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 0
+    return (f"{info.get('model name', 'unknown')} (family {info.get('cpu family', '?')}, model "
+            f"{info.get('model', '?')}, stepping {info.get('stepping', '?')}, {info.get('cpu MHz', '?')} MHz; "
+            f"{os.cpu_count()} logical CPUs on the host, {avail} in this process's affinity set)")
 
 
-def cpu_baseline(wname: str, budget_s: float) -> dict:
+def cpu_baseline(wname: str, arrays, budget_s: float) -> dict:
     """The oracle (C restatement of the reference CPU-JIT schedule: OpenMP
     over 64x64 tiles, 8x8x8 fma micro-kernel, separate bias+ReLU pass; exact
     wrapping i32 for c5) on the first R rows of the workload, in the
@@ -218,10 +359,9 @@ def cpu_baseline(wname: str, budget_s: float) -> dict:
     budget (at most the whole workload); runs repeat while the budget lasts
     (at least 3) and the median is reported."""
     import oracle
-    from mlir_edsl_hip.inputs import WORKLOADS, make_inputs
+    from mlir_edsl_hip.inputs import WORKLOADS
 
     w = WORKLOADS[wname]
-    arrays = make_inputs(w)
     threads = oracle.cpu_threads()
     bias = w.pattern != "matmul"
 
@@ -261,24 +401,7 @@ def cpu_baseline(wname: str, budget_s: float) -> dict:
             "host_cpu": cpu_model()}
 
 
-UNITS = {"c1": "TFLOP/s", "c2": "TFLOP/s", "c3": "TFLOP/s", "c4": "GB/s", "c5": "TOP/s",
-         "c3s8": "TFLOP/s", "c4s8": "GB/s"}
-# (steps, warmup, W buffers rotated) of each workload when it is not the headline.
-# W is rotated over enough copies to exceed the 256 MB Infinity Cache where it
-# would otherwise be served from there: c4 3 x 256 MiB, c4s8 12 x 32 MiB.
-SECONDARY_PLAN = {"c4": (200, 20, 3), "c5": (100, 20, 1), "c2": (100, 20, 1), "c1": (200, 20, 1),
-                  "c3": (50, 10, 1), "c3s8": (100, 10, 1), "c4s8": (300, 30, 12)}
-
-
-def step_value(wname: str, step_s: float) -> float:
-    """Whole-step throughput in the workload's unit."""
-    from mlir_edsl_hip.inputs import WORKLOADS
-    wl = WORKLOADS[wname]
-    if UNITS[wname] == "GB/s":
-        return wl.compulsory_bytes / step_s / 1e9
-    return wl.flops / step_s / 1e12
-
-
+# -------------------------------------------------------------------- main
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -288,13 +411,13 @@ def main() -> int:
                     help="workload of the headline line (default c3, the BASELINE metric's config)")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--secondary", default="c4,c5,c2,c1,c4s8,c3s8",
-                    help="comma-separated workloads measured after the headline one")
+                    help="comma-separated workloads measured before the headline one")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--host-path", action="store_true",
-                    help="also time the memref-ABI entry on host (numpy) buffers for the headline "
-                         "workload: H2D copies + kernels + D2H, as the reference GPU path does "
-                         "(reported as host_path, never as value)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="CPU budget of the headline's baseline (each secondary gets a third)")
+    ap.add_argument("--no-host-path", action="store_true",
+                    help="skip the host-buffer measurements (reference calling pattern, resident "
+                         "weights, the reference's GPU benchmark points)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES (3 times) and exit; "
                          "its FETCH_SIZE / WRITE_SIZE counters calibrate the traffic figures")
@@ -326,39 +449,88 @@ def main() -> int:
     traffic = load_traffic()
     head_name = args.workload
     w = WORKLOADS[head_name]
-    rotate = SECONDARY_PLAN[head_name][2]
-    log(f"[bench] {head_name} {w.description}: warmup {args.warmup}, steps {args.steps}")
-    head = measure(head_name, args.steps, args.warmup, rotate=rotate)
-    log(f"[bench] {head_name} done: {head['ms_per_step']:.4f} ms/step, kernel "
-        f"{head['kernel_ms_mean'] * 1e3:.1f} us [{head['plan']}]")
+    names = [] if args.no_secondary else [x.strip() for x in args.secondary.split(",") if x.strip()]
+    names = [n for n in names if n != head_name] + [head_name]
+    prepared = {}
+    for n in names:
+        prepared[n] = Prepared(n, SECONDARY_PLAN[n][2])
+    torch.cuda.synchronize()
+    log(f"[bench] inputs of {', '.join(names)} generated and resident")
+
+    # Device-resident timing, back to back, headline last.
+    results = {}
+    for n in names:
+        p = prepared[n]
+        if n == head_name:
+            log(f"[bench] {n} {p.w.description}: warmup {args.warmup}, steps {args.steps}")
+            r = measure(p, args.steps, args.warmup)
+        else:
+            steps, warm, _ = SECONDARY_PLAN[n]
+            r = measure(p, steps, warm)
+        val = step_value(n, r["ms_per_step"] * 1e-3)
+        r.update({"value": round(val, 3), "unit": UNITS[n], "roofline": roofline_for(n, r, traffic),
+                  "config": {"M": p.w.M, "K": p.w.K, "N": p.w.N, "seed": p.w.seed, "dtype": p.w.dtype}})
+        if n in RESIDENT_TOO and p.rotate > 1:
+            rr = measure(p, SECONDARY_PLAN[n][0], SECONDARY_PLAN[n][1], rotate=1)
+            r["inputs_cache_resident"] = {
+                "ms_per_step": rr["ms_per_step"], "kernel_ms_mean": rr["kernel_ms_mean"],
+                "value": round(step_value(n, rr["ms_per_step"] * 1e-3), 3), "unit": UNITS[n],
+                "roofline": roofline_for(n, rr, traffic),
+                "what": "the same layer with one input set, which the 256 MB Infinity Cache holds"}
+        if n in UNFUSED_TOO:
+            steps = args.steps if n == head_name else SECONDARY_PLAN[n][0]
+            ru = measure(p, max(10, steps // 2), SECONDARY_PLAN[n][1], unfused=True)
+            r["unfused_reference_sequence"] = {
+                "ms_per_step": round(ru["ms_per_step"], 5), "kernel_ms_mean": round(ru["kernel_ms_mean"], 5),
+                "value": round(step_value(n, ru["ms_per_step"] * 1e-3), 3), "unit": UNITS[n],
+                "launches": 3, "plan": ru["plan"],
+                "fused_speedup_device": round(ru["kernel_ms_mean"] / r["kernel_ms_mean"], 3),
+                "what": "fill + GEMM without epilogue + separate bias/ReLU kernel: the reference GPU "
+                        "lowering's three launches (reference cpp/src/MLIRLowering.cpp:495-518), on this "
+                        "library's kernels"}
+        log(f"[bench] {n} done: {val:.2f} {UNITS[n]}, kernel {r['kernel_ms_mean'] * 1e3:.1f} us, region "
+            f"{r['region_ms_per_step'] * 1e3:.1f} us/step [{r['plan']}]")
+        results[n] = r
+    head = results[head_name]
+    for p in prepared.values():
+        p.free()
+
+    # Host buffers: the reference's calling pattern, resident weights, the
+    # reference's own GPU benchmark points.
+    host, ref_points = {}, None
+    if not args.no_host_path:
+        for n in names:
+            steps = 10 if WORKLOADS[n].flops < 2e11 else 5
+            host[n] = measure_host_path(n, prepared[n].arrays, steps)
+            log(f"[bench] host path {n}: {host[n]['ms_per_call']:.3f} ms/call")
+        if "c4" in names and WORKLOADS["c4"].dtype == "f32":
+            host["c4_resident"] = measure_resident_host_path("c4", prepared["c4"].arrays, 10)
+            log(f"[bench] c4 with W, b resident: {host['c4_resident']['ms_per_call']:.3f} ms/call "
+                f"(every operand copied: {host['c4_resident']['unbound_ms_per_call']:.3f})")
+        ref_points = reference_gpu_points()
+        log("[bench] reference GPU benchmark points: " +
+            ", ".join(f"{q['kind']} {q['size']}: {q['ms_per_call']:.3f} ms" for q in ref_points))
+
+    cpu = {}
+    if not args.no_cpu_baseline:
+        for n in names:
+            budget = args.cpu_seconds if n == head_name else args.cpu_seconds / 3
+            log(f"[bench] cpu baseline (oracle, row sample of {n}, {budget:.0f} s)")
+            cpu[n] = cpu_baseline(n, prepared[n].arrays, budget)
+            log(f"[bench] cpu baseline {n}: {cpu[n]['value']} {cpu[n]['unit']} on {cpu[n]['cores']} threads")
 
     secondary = []
-    if not args.no_secondary:
-        for wname in [x.strip() for x in args.secondary.split(",") if x.strip()]:
-            if wname == head_name:
-                continue
-            steps, warm, rot = SECONDARY_PLAN[wname]
-            log(f"[bench] {wname} {WORKLOADS[wname].description}")
-            r = measure(wname, steps, warm, rotate=rot)
-            wl = WORKLOADS[wname]
-            val = step_value(wname, r["ms_per_step"] * 1e-3)
-            r.update({"value": round(val, 3), "unit": UNITS[wname],
-                      "roofline": roofline_for(wname, r, traffic),
-                      "config": {"M": wl.M, "K": wl.K, "N": wl.N, "seed": wl.seed, "dtype": wl.dtype}})
-            log(f"[bench] {wname} done: {val:.2f} {UNITS[wname]}, kernel {r['kernel_ms_mean'] * 1e3:.1f} us "
-                f"[{r['plan']}]")
-            secondary.append(r)
-
-    host = None
-    if args.host_path:
-        host = measure_host_path(head_name, max(3, args.steps // 5))
-        log(f"[bench] host path: {host['value']:.2f} {host['unit']} ({host['ms_per_call']:.3f} ms/call)")
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        log(f"[bench] cpu baseline (oracle, row sample of {head_name})")
-        cpu = cpu_baseline(head_name, args.cpu_seconds)
-        log(f"[bench] cpu baseline: {cpu['value']} {cpu['unit']} on {cpu['cores']} threads")
+    for n in names:
+        if n == head_name:
+            continue
+        r = results[n]
+        if n in host:
+            r["host_path"] = host[n]
+        if n == "c4" and "c4_resident" in host:
+            r["host_path_resident_weights"] = host["c4_resident"]
+        if n in cpu:
+            r["cpu_baseline"] = cpu[n]
+        secondary.append(r)
 
     value = step_value(head_name, head["ms_per_step"] * 1e-3)
     line = {
@@ -369,6 +541,8 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(head["ms_per_step"], 4),
+        "region_ms_per_step": round(head["region_ms_per_step"], 4),
+        "kernel_ms_mean": round(head["kernel_ms_mean"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -377,13 +551,22 @@ def main() -> int:
                 "(c5: ints in [-8,7], b in [-512,511])",
         "config": {"workload": f"{head_name}: {w.description}", "M": w.M, "N": w.N, "K": w.K,
                    "seed": w.seed, "parallelism": "single GPU", "plan": head["plan"],
-                   "w_buffers_rotated": rotate},
+                   "w_buffers_rotated": head["rotate_w"], "x_buffers_rotated": head["rotate_x"]},
         "roofline": roofline_for(head_name, head, traffic),
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu.get(head_name),
         "secondary": secondary,
     }
-    if host is not None:
-        line["host_path"] = host
+    for k in ("unfused_reference_sequence", "inputs_cache_resident"):
+        if k in head:
+            line[k] = head[k]
+    if head_name in host:
+        line["host_path"] = host[head_name]
+    if ref_points is not None:
+        line["reference_gpu_benchmark"] = {
+            "points": ref_points,
+            "what": "the reference's GPU benchmark (tests/gpu/test_gpu_benchmark.py): matmul and dense "
+                    "relu(X@W+b) at 256/512/1024 on host arrays through the drop-in compiler's "
+                    "execute_gpu_function, 3 warmup calls, mean of 10"}
     print(json.dumps(line), flush=True)
     return 0
 
