@@ -16,9 +16,12 @@
 // transposed on the way), and flags any out-of-range value. The packed copies
 // are padded with zeros to multiples of the 128-wide tile in M, N and K, so
 // any shape runs on the matrix cores; the GEMM stores only the real M x N.
-// The GEMM reads the flag: if set, the whole grid takes the exact
-// wrapping-i32 vector-ALU path on the original i32 tensors instead. The flag
-// is compared against a per-call epoch, so it never needs clearing.
+// The pre-pass writes one range flag per 64x64 tile of X and of W on every
+// call (1: some value outside int8, else 0). Each GEMM workgroup reads the
+// flags of the X row panels and W column panels its tile uses; if any is set,
+// that tile alone takes the exact wrapping-i32 vector-ALU path on the
+// original i32 tensors instead. Every flag is rewritten by every call, so a
+// replayed graph never sees a previous call's state.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -122,12 +125,31 @@ __global__ void __launch_bounds__(256) narrow_i8_kernel(NarrowI8Args a, int vec_
       pk[tile_packed_offset(bj + e, 4 * bi) >> 2] = w;
     }
   }
-  __syncthreads();
+  const int tile_bad = __syncthreads_or(bad ? 1 : 0);
   const int frag = tid >> 6, lane = tid & 63;
   const int rb = (r0 >> 5) + (frag >> 1), kt = (k0 >> 5) + (frag & 1);
   const i32x4 out = reinterpret_cast<const i32x4*>(pk)[tid];
   *reinterpret_cast<i32x4*>(dst + ((((int64_t)rb * (a.Kp >> 5) + kt) * 64 + lane) << 4)) = out;
-  if (__any(bad) && (tid & 63) == 0) *a.flag = a.epoch;
+  if (tid == 0) {
+    // Written on every call: X flags [Mp/64][Kp/64], W flags [Np/64][Kp/64].
+    uint8_t* f = dst == a.X8p ? a.flags_x : a.flags_w;
+    f[(int64_t)(r0 / kNarrowTile) * (a.Kp / kNarrowTile) + k0 / kNarrowTile] = tile_bad ? 1 : 0;
+  }
+}
+
+// Whether the tile at (m0, n0) must take the exact i32 path: any range flag
+// of its two 64-row X panels or its two 64-column W panels is set. Uniform
+// over the workgroup (NT threads). Flag rows of one panel are Kp/64 bytes,
+// an even count, and the two panels of a 128-wide tile are adjacent, so the
+// 2*Kp/64 flags are read as 4-byte words.
+template <int NT>
+__device__ __forceinline__ bool tile_out_of_range(const GemmI32Args& a, int m0, int n0) {
+  const int kt = a.Kp / kNarrowTile;
+  const uint32_t* fx = reinterpret_cast<const uint32_t*>(a.flags_x + (int64_t)(m0 / kNarrowTile) * kt);
+  const uint32_t* fw = reinterpret_cast<const uint32_t*>(a.flags_w + (int64_t)(n0 / kNarrowTile) * kt);
+  int bad = 0;
+  for (int i = threadIdx.x; i < kt / 2; i += NT) bad |= (fx[i] | fw[i]) != 0;
+  return __syncthreads_or(bad) != 0;
 }
 
 // ------------------------------------------------- exact i32 vector-ALU tile
@@ -219,7 +241,7 @@ __global__ void __launch_bounds__(256) gemm_i8_kernel(GemmI32Args a) {
   tile_coords(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
   const int m0 = tm * kI8Tile, n0 = tn * kI8Tile;
 
-  if (*a.flag == a.epoch) {  // some value outside int8: exact i32 path
+  if (tile_out_of_range<256>(a, m0, n0)) {  // some value outside int8: exact i32 path
     valu_tile_i32<EPI, 256>(a, m0, n0, valu);
     return;
   }
@@ -327,7 +349,7 @@ gemm_i8_ksplit_kernel(GemmI32Args a) {
   tile_coords(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
   const int m0 = tm * kI8Tile, n0 = tn * kI8Tile;
 
-  if (*a.flag == a.epoch) {  // some value outside int8: exact i32 path
+  if (tile_out_of_range<256>(a, m0, n0)) {  // some value outside int8: exact i32 path
     valu_tile_i32<EPI, 256>(a, m0, n0, *reinterpret_cast<ValuSmem*>(red));
     return;
   }
@@ -505,17 +527,18 @@ int gemm_i8_depth(int variant, int K) {
   return 1;
 }
 
-bool gemm_i8_ksplit(int variant) {
+const char* gemm_i8_layout(int variant) {
   if (variant < 0 || variant >= kI8Variants) variant = kI8DefaultVariant;
-  return kI8Table[variant].ksplit;
+  return kI8Table[variant].ksplit ? "ksplit" : "quadrant";
 }
 
 hipError_t launch_gemm_i8(int epi, GemmI32Args a, hipStream_t stream, int variant) {
   if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.Kp % kI8Tile || a.Kp < a.K) return hipErrorInvalidValue;
   a.tiles_m = (a.M + kI8Tile - 1) / kI8Tile;
   a.tiles_n = (a.N + kI8Tile - 1) / kI8Tile;
+  if (variant < 0 || variant >= kI8Variants) variant = kI8DefaultVariant;
   const int d = gemm_i8_depth(variant, a.Kp);
-  if (gemm_i8_ksplit(variant)) {
+  if (kI8Table[variant].ksplit) {
     switch (d) {
       case 1: return launch_i8_depth<true, 1>(epi, a, stream);
       case 2: return launch_i8_depth<true, 2>(epi, a, stream);

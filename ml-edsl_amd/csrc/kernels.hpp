@@ -81,8 +81,11 @@ struct NarrowI8Args {
   int64_t ldx, ldw;
   int M, N, K;        // real sizes
   int Mp, Np, Kp;     // padded sizes (multiples of kI8Tile)
-  unsigned* flag;     // set to `epoch` when a value lies outside [-128, 127]
-  unsigned epoch;
+  // Range flags, one byte per 64x64 tile, all written on every call: 1 when the
+  // tile holds a value outside [-128, 127], else 0. X: [Mp/64][Kp/64]; W:
+  // [Np/64][Kp/64] (indexed by W's column tile, then its k tile).
+  uint8_t* flags_x;
+  uint8_t* flags_w;
 };
 
 struct GemmI32Args {
@@ -96,8 +99,10 @@ struct GemmI32Args {
   int M, N, K;
   int Kp;             // K of the packed copies (int8 path; a multiple of kI8Tile)
   int tiles_m, tiles_n;
-  const unsigned* flag;  // fast path only when *flag != epoch
-  unsigned epoch;
+  // Range flags of the narrowing pass (int8 path): a tile takes the exact i32
+  // path when a flag of its X row panels or W column panels is set.
+  const uint8_t* flags_x;
+  const uint8_t* flags_w;
 };
 
 constexpr int kI8Tile = 128;   // tile of the int8 MFMA path; packed copies are padded to it
@@ -111,7 +116,7 @@ hipError_t launch_narrow_i8(NarrowI8Args args, hipStream_t stream);
 constexpr int kI8Variants = 4;
 constexpr int kI8DefaultVariant = 3;
 int gemm_i8_depth(int variant, int K);
-bool gemm_i8_ksplit(int variant);
+const char* gemm_i8_layout(int variant);
 hipError_t launch_gemm_i8(int epi, GemmI32Args args, hipStream_t stream, int variant = -1);
 // Exact wrapping i32 GEMM on the vector ALUs: any shape, any alignment.
 hipError_t launch_gemm_i32_valu(int epi, GemmI32Args args, hipStream_t stream);

@@ -123,8 +123,7 @@ struct DeviceState {
   DevBuf chain[2];  // intermediate activations of multi-layer programs (ping-pong)
   DevBuf gemv_partials{true};
   DevBuf gemv_xstage{true};  // X rows copied to 16-byte aligned rows for the small-M kernel
-  DevBuf i8_x{true}, i8_w{true}, i8_flag{true};
-  unsigned epoch = 0;
+  DevBuf i8_x{true}, i8_w{true}, i8_flags{true};
   // Ordering of the launches that use the library scratch above (split-K
   // partials, packed int8 operands and flag) across streams.
   hipStream_t ws_stream = nullptr;  // stream of the last such launch
@@ -501,8 +500,9 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     const size_t xs = (size_t)Mp * Kp, ws = (size_t)Np * Kp;
     int8_t* x8 = static_cast<int8_t*>(ds.i8_x.ensure(xs, false));
     int8_t* w8 = static_cast<int8_t*>(ds.i8_w.ensure(ws, false));
-    unsigned* flag = static_cast<unsigned*>(ds.i8_flag.ensure(sizeof(unsigned), true));
-    if (++ds.epoch == 0) ++ds.epoch;
+    // One range flag per 64x64 tile of the padded X and W (rewritten by every call).
+    const size_t fx = (size_t)(Mp / 64) * (Kp / 64), fw = (size_t)(Np / 64) * (Kp / 64);
+    uint8_t* flags = static_cast<uint8_t*>(ds.i8_flags.ensure(fx + fw, false));
     NarrowI8Args n{};
     n.X = a.X;
     n.W = a.W;
@@ -516,19 +516,19 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     n.Mp = Mp;
     n.Np = Np;
     n.Kp = Kp;
-    n.flag = flag;
-    n.epoch = ds.epoch;
+    n.flags_x = flags;
+    n.flags_w = flags + fx;
     scratch_begin(ds, stream);
     check_hip(launch_narrow_i8(n, stream), "narrow_i8 launch");
     a.A8p = x8;
     a.B8p = w8;
-    a.flag = flag;
-    a.epoch = ds.epoch;
+    a.flags_x = flags;
+    a.flags_w = flags + fx;
     const int variant = (g_force_i8 >= 0 && g_force_i8 < kI8Variants) ? g_force_i8 : kI8DefaultVariant;
     check_hip(launch_gemm_i8(L.epi, a, stream, variant), "gemm_i8 launch");
     scratch_end(ds, stream);
-    set_plan("narrow_i8+gemm_i8 variant=%d waves=%s depth=%d grid=%d", variant,
-             gemm_i8_ksplit(variant) ? "ksplit" : "quadrant", gemm_i8_depth(variant, Kp),
+    set_plan("narrow_i8+gemm_i8 variant=%d waves=%s depth=%d grid=%d", variant, gemm_i8_layout(variant),
+             gemm_i8_depth(variant, Kp),
              (Mp / kI8Tile) * (Np / kI8Tile));
   } else {
     check_hip(launch_gemm_i32_valu(L.epi, a, stream), "gemm_i32_valu launch");

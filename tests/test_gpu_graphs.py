@@ -112,3 +112,46 @@ def test_graph_replay_matches_eager(name, dtype, M, widths, epis, plans):
         assert_f32_parity(outs[-1].cpu().numpy(), oracle.dense_f32(prev, W.cpu().numpy(), bias, act), W.shape[0])
     else:
         assert np.array_equal(outs[-1].cpu().numpy(), oracle.dense_i32(prev, W.cpu().numpy(), bias, act))
+
+
+def _exact_i32(X, W, b):
+    y = X.astype(np.int64) @ W.astype(np.int64) + b.astype(np.int64)
+    return np.maximum((y + 2**31) % 2**32 - 2**31, 0).astype(np.int32)
+
+
+def test_int8_range_flags_on_replay():
+    """A captured integer layer replayed on inputs that leave int8 and come
+    back: out of range, in range, out of range (elsewhere), in range. The
+    narrowing pass rewrites every tile's range flag on every call, so each
+    replay is exact and none inherits the previous one's fallback."""
+    import torch
+    M, K, N = 512, 384, 256
+    rng = np.random.default_rng(33)
+    W = rng.integers(-128, 128, size=(K, N), dtype=np.int32)
+    b = rng.integers(-2**20, 2**20, size=(N,), dtype=np.int32)
+    tW, tb = torch.from_numpy(W).cuda(), torch.from_numpy(b).cuda()
+    tX = torch.zeros((M, K), dtype=torch.int32, device="cuda")
+    tY = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    good = rng.integers(-128, 128, size=(M, K), dtype=np.int32)
+    bad1 = good.copy()
+    bad1[3, 5] = 70000          # first 128-row tile only
+    bad2 = good.copy()
+    bad2[400, 380] = -300       # last row tile, last k tile
+    bad2[130, 0] = 2**30        # second row tile
+    tX.copy_(torch.from_numpy(good))
+    dense_launch(tX, tW, tb, tY, _native.EPI_BIAS_RELU)  # sizes the workspaces
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            dense_launch(tX, tW, tb, tY, _native.EPI_BIAS_RELU)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for step, Xv in enumerate((bad1, good, bad2, good, bad1)):
+        tX.copy_(torch.from_numpy(Xv))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(tY.cpu().numpy(), _exact_i32(Xv, W, b)), f"replay {step}"

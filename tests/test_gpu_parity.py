@@ -237,6 +237,31 @@ def test_int8_path_falls_back_when_values_leave_int8(torch_cuda):
     assert np.array_equal(got3, (X2.astype(np.int64) @ W2.astype(np.int64)).astype(np.int32))
 
 
+def test_int8_fallback_is_per_tile(torch_cuda):
+    """Values outside int8 in a few 64x64 tiles of X and W: the tiles whose
+    panels hold them take the exact i32 path, the others the int8 path, and
+    every output is exact, for every variant."""
+    from mlir_edsl_hip.device import set_i8_variant
+    rng = np.random.default_rng(16)
+    M, K, N = 640, 768, 896
+    X = rng.integers(-128, 128, size=(M, K), dtype=np.int32)
+    W = rng.integers(-128, 128, size=(K, N), dtype=np.int32)
+    b = rng.integers(-2**20, 2**20, size=(N,), dtype=np.int32)
+    X[200, 700] = 129
+    X[639, 0] = -2**31
+    W[64, 895] = 2**20
+    exact = X.astype(np.int64) @ W.astype(np.int64) + b
+    exp = np.maximum((exact + 2**31) % 2**32 - 2**31, 0).astype(np.int32)
+    try:
+        for v in range(_native.lib().edsl_hip_i8_variant_count()):
+            set_i8_variant(v)
+            got = gpu_run("dense_relu", [X, W, b], device=True)
+            assert _native.last_plan().startswith(f"narrow_i8+gemm_i8 variant={v}")
+            assert np.array_equal(got, exp), f"variant {v}"
+    finally:
+        set_i8_variant(-1)
+
+
 def test_every_int8_variant(torch_cuda):
     from mlir_edsl_hip.device import set_i8_variant
     rng = np.random.default_rng(15)
