@@ -51,6 +51,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_dense_i32.argtypes = [i32p, i32p, i32p, i32p, i64, i64, i64, ctypes.c_int,
                                        ctypes.c_int]
         L.oracle_dense_i32.restype = ctypes.c_int
+        L.oracle_dense_f32_vec.argtypes = L.oracle_dense_f32.argtypes
+        L.oracle_dense_f32_vec.restype = ctypes.c_int
         L.oracle_static_tiles.argtypes = [i64, i64, i64]
         L.oracle_static_tiles.restype = ctypes.c_int
         L.oracle_set_mutation.argtypes = [ctypes.c_int]
@@ -82,6 +84,26 @@ def dense_f32(X, W, b=None, act: str = "none", alpha: float = 0.0, threads: int 
                                 epilogue_code(bias, act), alpha, threads)
     if rc != 0:
         raise ValueError(f"oracle_dense_f32 rejected epilogue {act!r}")
+    return Y
+
+
+def dense_f32_vec(X, W, b=None, act: str = "none", alpha: float = 0.0, threads: int = 0) -> np.ndarray:
+    """dense_f32 with the reference JIT's 8-wide vector FMAs (bit-identical;
+    static-tile shapes only). For timing the CPU baseline."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    W = np.ascontiguousarray(W, dtype=np.float32)
+    M, K = X.shape
+    K2, N = W.shape
+    assert K == K2, (X.shape, W.shape)
+    bias = b is not None
+    bb = np.ascontiguousarray(b if bias else np.zeros(max(N, 1)), dtype=np.float32)
+    Y = np.empty((M, N), dtype=np.float32)
+    rc = lib().oracle_dense_f32_vec(_ptr(X, ctypes.c_float), _ptr(W, ctypes.c_float),
+                                    _ptr(bb, ctypes.c_float), _ptr(Y, ctypes.c_float), M, N, K,
+                                    epilogue_code(bias, act), alpha, threads)
+    if rc != 0:
+        raise ValueError(f"oracle_dense_f32_vec rejected the call (code {rc}): shape {M}x{K}x{N} "
+                         f"needs static 8x8x8 tiles")
     return Y
 
 

@@ -16,6 +16,10 @@
 #include <omp.h>
 #endif
 
+#if defined(__AVX2__) && defined(__FMA__)
+#include <immintrin.h>
+#endif
+
 /* Planted mistakes, for the tests that show the pinning checks catch them:
  *  1  W read transposed (W[n][k] instead of W[k][n]; square shapes only)
  *  2  bias dropped
@@ -146,6 +150,65 @@ int oracle_dense_f32(const float *X, const float *W, const float *b, float *Y, i
       Y[m * N + n] = y;
     }
   return 0;
+}
+
+/* The same lowering, with the 8x8x8 micro-kernel on 8-wide vectors as the
+ * reference JIT emits it: each outer product is one vector.fma over a row of
+ * the C tile (reference MLIRLoweringPasses.cpp:242-260; x86Vector lowering,
+ * MLIRLowering.cpp:422-424), here one 256-bit FMA per row and k. Every C
+ * element sees the same fmaf chain in the same k order as micro_fma_8x8x8,
+ * so the results are bit-identical; it exists to time the reference's CPU
+ * schedule at its own vector width (the benchmark's CPU baseline). Static
+ * tiles only (oracle_static_tiles true); no planted-mistake hooks. */
+int oracle_dense_f32_vec(const float *X, const float *W, const float *b, float *Y, int64_t M,
+                         int64_t N, int64_t K, int epilogue, float alpha, int threads) {
+#if defined(__AVX2__) && defined(__FMA__)
+  if (epilogue < 0 || epilogue > 5) return -1;
+  if (!oracle_static_tiles(M, N, K)) return -2;
+  const int has_bias = epilogue & 1;
+  const int act = (epilogue >> 1) & 3;
+  for (int64_t i = 0; i < M * N; ++i) Y[i] = 0.0f; /* linalg.fill */
+  const int64_t tiles_m = (M + 63) / 64, tiles_n = (N + 63) / 64;
+  const int64_t tiles = tiles_m * tiles_n;
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : omp_get_max_threads())
+  for (int64_t t = 0; t < tiles; ++t) {
+    const int64_t m0 = (t / tiles_n) * 64, n0 = (t % tiles_n) * 64;
+    const int64_t mh = M - m0 < 64 ? M - m0 : 64;
+    const int64_t nh = N - n0 < 64 ? N - n0 : 64;
+    for (int64_t mi = 0; mi < mh; mi += 8)
+      for (int64_t ni = 0; ni < nh; ni += 8)
+        for (int64_t ki = 0; ki < K; ki += 8) {
+          float *c0 = Y + (m0 + mi) * N + n0 + ni;
+          __m256 c[8];
+          for (int m = 0; m < 8; ++m) c[m] = _mm256_loadu_ps(c0 + m * N);
+          for (int k = 0; k < 8; ++k) {
+            const __m256 w = _mm256_loadu_ps(W + (ki + k) * N + n0 + ni);
+            for (int m = 0; m < 8; ++m)
+              c[m] = _mm256_fmadd_ps(_mm256_set1_ps(X[(m0 + mi + m) * K + ki + k]), w, c[m]);
+          }
+          for (int m = 0; m < 8; ++m) _mm256_storeu_ps(c0 + m * N, c[m]);
+        }
+  }
+  if (!has_bias && act == ACT_NONE) return 0;
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) {
+      float y = Y[m * N + n];
+      if (has_bias) y = y + b[n];
+      if (act == ACT_RELU) {
+        y = (y > 0.0f || y != y) ? y : 0.0f;
+      } else if (act == ACT_LEAKY) {
+        const float pos = (y > 0.0f || y != y) ? y : 0.0f;
+        const float neg = (y < 0.0f || y != y || y == 0.0f) ? y : 0.0f;
+        const float scaled = neg * alpha;
+        y = pos + scaled;
+      }
+      Y[m * N + n] = y;
+    }
+  return 0;
+#else
+  (void)X; (void)W; (void)b; (void)Y; (void)M; (void)N; (void)K; (void)epilogue; (void)alpha; (void)threads;
+  return -3;
+#endif
 }
 
 int oracle_dense_i32(const int32_t *X, const int32_t *W, const int32_t *b, int32_t *Y, int64_t M,

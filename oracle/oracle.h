@@ -58,6 +58,13 @@ int oracle_dense_f32(const float *X, const float *W, const float *b, float *Y, i
 int oracle_dense_i32(const int32_t *X, const int32_t *W, const int32_t *b, int32_t *Y,
                      int64_t M, int64_t N, int64_t K, int epilogue, int threads);
 
+/* oracle_dense_f32 with the 8x8x8 micro-kernel on 8-wide FMA vectors, as the
+ * reference JIT emits it (bit-identical results; static-tile shapes only:
+ * returns -2 otherwise, -3 when built without AVX2/FMA). For timing the
+ * reference's CPU schedule at its own vector width. */
+int oracle_dense_f32_vec(const float *X, const float *W, const float *b, float *Y, int64_t M,
+                         int64_t N, int64_t K, int epilogue, float alpha, int threads);
+
 /* Test hook: plant a known mistake (0 = none) so the tests can show that the
  * checks pinning this oracle catch it. See oracle.c for the list. */
 void oracle_set_mutation(int mutation);

@@ -221,3 +221,31 @@ def test_rows_are_independent():
     part = oracle.dense_f32(X[np.concatenate([rows, np.arange(64 - rows.size) + 1])], W, b, "relu")
     assert np.array_equal(full[rows].view(np.uint32), part[:rows.size].view(np.uint32))
     assert math.isfinite(float(full.sum()))
+
+
+# ------------------------------------------------ vectorised timing twin
+@pytest.mark.parametrize("M, K, N", [(8, 8, 8), (64, 64, 64), (16, 256, 512), (192, 96, 40), (256, 1024, 192)])
+@pytest.mark.parametrize("act", ["none", "relu", "leaky"])
+def test_vector_twin_is_bit_identical(M, K, N, act):
+    """oracle_dense_f32_vec (the bench's CPU baseline: the reference JIT's
+    8x8x8 schedule on 8-wide FMA vectors) must round exactly like the scalar
+    restatement it times, special values included."""
+    rng = np.random.default_rng(M + K + N)
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    W = rng.standard_normal((K, N), dtype=np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    X[0, 0] = np.nan
+    if M > 1:
+        X[1, 1] = np.inf
+    b[-1] = -np.inf
+    for bias in (b, None):
+        ref = oracle.dense_f32(X, W, bias, act, 0.07)
+        got = oracle.dense_f32_vec(X, W, bias, act, 0.07)
+        assert np.array_equal(ref.view(np.uint32), got.view(np.uint32))
+
+
+@pytest.mark.parametrize("M, K, N", [(65, 8, 8), (200, 96, 72), (64, 12, 64)])
+def test_vector_twin_only_takes_static_tiles(M, K, N):
+    assert not oracle.static_tiles(M, N, K)
+    with pytest.raises(ValueError, match="static 8x8x8 tiles"):
+        oracle.dense_f32_vec(np.ones((M, K), np.float32), np.ones((K, N), np.float32))
