@@ -54,8 +54,7 @@ int edsl_hip_dense_f32_launch(const float *X, int64_t ldx, const float *W, int64
  * reference: it is for callers that cannot allocate device memory -- code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc. It calls no hipMalloc/hipFree and creates no events: the
- * small-M plan's scratch (split-K partials, X rows staged to 16-byte
- * alignment) lives in a static device array of EDSL_NOALLOC_SCRATCH_BYTES
+ * small-M plan's scratch (its split-K partials) lives in a static device array of EDSL_NOALLOC_SCRATCH_BYTES
  * per GPU, held until the process ends. A plan that needs more scratch than
  * that is rejected (error code -5, the message gives both sizes); the tiled
  * plans need none. Every call on a GPU shares that GPU's array: calls that
@@ -88,7 +87,7 @@ int edsl_hip_dense_i32_launch(const int32_t *X, int64_t ldx, const int32_t *W, i
 /* Description of the kernels the calling thread's last call launched, e.g.
  * "gemm_f32 cfg=f32_256x256x16_w4x4 grid=256" (a "_edge" suffix: partial
  * edge tiles), "gemv_f32 mb=1 ksplit=4 cols=128 grid=256 +reduce" (with
- * "+xstage": X rows copied to aligned rows; "+ktail": the reduce kernel adds
+ * "+xunaligned": X rows read with 4-byte loads; "+ktail": the reduce kernel adds
  * the last K % 16 rows) or "narrow_i8+gemm_i8 variant=3 waves=ksplit depth=2
  * grid=256"; returns its length. */
 int edsl_hip_last_plan(char *buf, size_t len);

@@ -56,7 +56,10 @@ __device__ __forceinline__ float epilogue_rt(float acc, float b, float alpha, in
   }
 }
 
-template <int MB, int CPL, int WN>
+// XV: X rows are 16-byte aligned (row stride % 4 == 0) and are read with one
+// 16-byte load per row block and step; otherwise with four 4-byte loads
+// (X is small and read from the caches, so this costs little against W).
+template <int MB, int CPL, int WN, bool XV>
 __global__ void __launch_bounds__(kWavesPerWG * 64)
 gemv_f32_kernel(GemvF32Args a, int epi) {
   using vec = typename std::conditional<CPL == 4, f32x4, f32x2>::type;
@@ -123,7 +126,13 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) x[u][mb] = *reinterpret_cast<const f32x4*>(xp[mb] + k + 16 * u);
+      for (int mb = 0; mb < MB; ++mb) {
+        const float* p = xp[mb] + k + 16 * u;
+        if constexpr (XV)
+          x[u][mb] = *reinterpret_cast<const f32x4*>(p);
+        else
+          x[u][mb] = f32x4{p[0], p[1], p[2], p[3]};
+      }
   };
   auto mfma_q = [&](const f32x4 (&xu)[MB], int s, const vec& wq) {
 #pragma unroll
@@ -275,18 +284,24 @@ __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi
   *reinterpret_cast<f32x4*>(a.Y + (int64_t)row * a.ldy + col) = y;
 }
 
-template <int MB>
-hipError_t launch_mb(int cols, int epi, const GemvF32Args& a, hipStream_t stream) {
+template <int MB, bool XV>
+hipError_t launch_mb_x(int cols, int epi, const GemvF32Args& a, hipStream_t stream) {
   const dim3 grid(((a.N + cols - 1) / cols) * a.ksplit);
   const dim3 block(kWavesPerWG * 64);
   switch (cols) {
-    case 32: hipLaunchKernelGGL((gemv_f32_kernel<MB, 2, 1>), grid, block, 0, stream, a, epi); break;
-    case 64: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 1>), grid, block, 0, stream, a, epi); break;
-    case 128: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 2>), grid, block, 0, stream, a, epi); break;
-    case 256: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 4>), grid, block, 0, stream, a, epi); break;
+    case 32: hipLaunchKernelGGL((gemv_f32_kernel<MB, 2, 1, XV>), grid, block, 0, stream, a, epi); break;
+    case 64: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 1, XV>), grid, block, 0, stream, a, epi); break;
+    case 128: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 2, XV>), grid, block, 0, stream, a, epi); break;
+    case 256: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 4, XV>), grid, block, 0, stream, a, epi); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <int MB>
+hipError_t launch_mb(int cols, int epi, const GemvF32Args& a, hipStream_t stream) {
+  const bool xv = reinterpret_cast<uintptr_t>(a.X) % 16 == 0 && a.ldx % 4 == 0;
+  return xv ? launch_mb_x<MB, true>(cols, epi, a, stream) : launch_mb_x<MB, false>(cols, epi, a, stream);
 }
 
 }  // namespace

@@ -59,9 +59,11 @@ struct GemvF32Args {
 // the last block possibly partial; the waves not side by side split K, which
 // is walked in 16-row chunks. Requirements (checked by the caller):
 // 1 <= M <= 64, N % 4 == 0, K % 16 == 0, ksplit > 1 when there is a K tail,
-// 16-byte aligned X/W/Y/bias and row strides % 4 == 0.
+// 16-byte aligned W/Y/bias and row strides % 4 == 0 (X may have any
+// alignment and row stride: unaligned rows are read with 4-byte loads).
 hipError_t launch_gemv_f32(int epi, int cols, GemvF32Args args, hipStream_t stream);
 int gemv_f32_waves_k(int cols);
+
 int gemv_f32_max_ksplit();
 constexpr int kGemvMaxM = 64;
 

@@ -2,12 +2,12 @@
 // a fixed, statically sized device array instead of library allocations.
 //
 // The small-M (weight-streaming) plan needs scratch beyond the caller's
-// operands: the split-K partial tiles that the reduce kernel sums, and, for X
-// rows that are not 16-byte aligned, an aligned copy of X. The ordinary entry
-// point takes them from grow-only per-device buffers that it allocates with
-// hipMalloc on first use. This entry point takes them from `scratch` below, so
-// it never allocates: callers that cannot call hipMalloc (code under HIP graph
-// capture, serving loops, harnesses that forbid it) can use it.
+// operands: the split-K partial tiles that the reduce kernel sums. The
+// ordinary entry point takes them from a grow-only per-device buffer that it
+// allocates with hipMalloc on first use. This entry point takes them from
+// `scratch` below, so it never allocates: callers that cannot call hipMalloc
+// (code under HIP graph capture, serving loops, harnesses that forbid it) can
+// use it.
 //
 // `scratch` is a file-scope __device__ array: every GPU the library runs on
 // holds its own copy, for the life of the process. In host code its name is
@@ -17,7 +17,7 @@
 //
 // All calls on one GPU share that GPU's array and it keeps the last call's
 // contents. Nothing in it needs to start at zero: every partial a reduce reads
-// was written by the same call, and the staged X rows are copied in full.
+// was written by the same call.
 // Calls that overlap on one GPU (two streams, two threads) race on it.
 #include <hip/hip_runtime.h>
 

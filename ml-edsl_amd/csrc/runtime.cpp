@@ -122,7 +122,6 @@ struct DeviceState {
   DevBuf stage[4];  // host-operand staging: X/A, W/B, bias, Y/C
   DevBuf chain[2];  // intermediate activations of multi-layer programs (ping-pong)
   DevBuf gemv_partials{true};
-  DevBuf gemv_xstage{true};  // X rows copied to 16-byte aligned rows for the small-M kernel
   DevBuf i8_x{true}, i8_w{true}, i8_flags{true};
   // Ordering of the launches that use the library scratch above (split-K
   // partials, packed int8 operands and flag) across streams.
@@ -335,9 +334,8 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   const int M = (int)L.M, N = (int)L.N, K = (int)L.K;
 
   // Small M: the streaming kernel walks the first K16 = K - K % 16 rows; the
-  // reduce kernel adds the rest. X rows that are not 16-byte aligned are
-  // first copied into aligned rows (at most 64 of them); W, Y and the bias
-  // must be aligned in place.
+  // reduce kernel adds the rest. X rows need no alignment (unaligned ones are
+  // read with 4-byte loads); W, Y and the bias must be aligned in place.
   int gemv_cols = 0, gemv_ks = 0;
   const int K16 = K & ~15;
   const bool w_ok = al16(L.w) && al16(L.y) && (!has_bias || al16(L.bias)) && L.ldw % 4 == 0 &&
@@ -363,38 +361,24 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     a.alpha = L.alpha;
     a.ksplit = gemv_ks;
     const int mb = (M + 15) / 16;
-    const bool scratch = a.ksplit > 1 || !x_ok;
-    const size_t part_bytes = a.ksplit > 1 ? (size_t)a.ksplit * 16 * mb * N * sizeof(float) : 0;
-    const size_t xs_bytes = x_ok ? 0 : (size_t)M * K16 * sizeof(float);
-    float* xs = nullptr;
+    const bool scratch = a.ksplit > 1;
+    const size_t part_bytes = scratch ? (size_t)a.ksplit * 16 * mb * N * sizeof(float) : 0;
     if (fixed) {
-      // Caller-fixed scratch: partials first, the staged X rows after them.
-      // Nothing is allocated and no cross-stream ordering is added.
-      const size_t xs_off = (part_bytes + 255) & ~size_t(255);
-      if (xs_off + xs_bytes > fixed->bytes)
-        fail(kErrLimit,
-             "small-M plan (M=%d N=%d K=%d, %d splits%s) needs %zu bytes of scratch; the fixed scratch "
-             "holds %zu",
-             M, N, K, a.ksplit, x_ok ? "" : ", staged X rows", xs_off + xs_bytes, fixed->bytes);
+      // Caller-fixed scratch: nothing is allocated and no cross-stream
+      // ordering is added.
+      if (part_bytes > fixed->bytes)
+        fail(kErrLimit, "small-M plan (M=%d N=%d K=%d, %d splits) needs %zu bytes of scratch; the fixed scratch holds %zu",
+             M, N, K, a.ksplit, part_bytes, fixed->bytes);
       if (part_bytes) a.partials = reinterpret_cast<float*>(fixed->base);
-      if (xs_bytes) xs = reinterpret_cast<float*>(fixed->base + xs_off);
-    } else {
-      if (scratch) scratch_begin(ds, stream);
-      if (part_bytes) a.partials = static_cast<float*>(ds.gemv_partials.ensure(part_bytes, false));
-      if (xs_bytes) xs = static_cast<float*>(ds.gemv_xstage.ensure(xs_bytes, false));
-    }
-    if (!x_ok) {
-      check_hip(hipMemcpy2DAsync(xs, (size_t)K16 * sizeof(float), L.x, (size_t)L.ldx * sizeof(float),
-                                 (size_t)K16 * sizeof(float), M, hipMemcpyDeviceToDevice, stream),
-                "hipMemcpy2DAsync (X rows to aligned rows)");
-      a.X = xs;
-      a.ldx = K16;
+    } else if (scratch) {
+      scratch_begin(ds, stream);
+      a.partials = static_cast<float*>(ds.gemv_partials.ensure(part_bytes, false));
     }
     check_hip(launch_gemv_f32(L.epi, gemv_cols, a, stream), "gemv_f32 launch");
     if (scratch && !fixed) scratch_end(ds, stream);
     set_plan("gemv_f32 mb=%d ksplit=%d cols=%d grid=%d%s%s%s%s", mb, a.ksplit, gemv_cols,
              ((N + gemv_cols - 1) / gemv_cols) * a.ksplit, a.ksplit > 1 ? " +reduce" : "",
-             x_ok ? "" : " +xstage", tail ? " +ktail" : "", fixed && scratch ? " +fixed-scratch" : "");
+             x_ok ? "" : " +xunaligned", tail ? " +ktail" : "", fixed && scratch ? " +fixed-scratch" : "");
     return;
   }
 

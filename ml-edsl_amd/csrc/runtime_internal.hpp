@@ -117,8 +117,8 @@ std::shared_ptr<ResidentCopy> make_resident_copy(const void* src, int64_t rows, 
 // The current HIP device. Throws Failure.
 int current_device();
 
-// Device memory for the small-M kernel's split-K partials and staged X rows
-// that the caller fixes, in place of the library's grow-only per-device
+// Device memory for the small-M kernel's split-K partials that the caller
+// fixes, in place of the library's grow-only per-device
 // workspaces: nothing is allocated, and no cross-stream ordering is added.
 struct FixedScratch {
   char* base;    // device address, 256-byte aligned

@@ -188,12 +188,12 @@ def _run_x_view(torch, X, W, b, x_pad, x_off, ksplit=None, epi=_native.EPI_BIAS_
 
 
 @pytest.mark.parametrize("M, K, N, x_pad, x_off, tags", [
-    (16, 8191, 8192, 0, 0, ("+xstage", "+ktail")),   # contiguous X, odd K: unaligned rows
-    (16, 8192, 2048, 0, 1, ("+xstage",)),             # misaligned X base, K % 16 == 0
-    (33, 4100, 512, 0, 0, ("+ktail",)),               # aligned X, K % 16 == 4
-    (5, 1003, 1024, 2, 3, ("+xstage", "+ktail")),
+    (16, 8191, 8192, 0, 0, ("+xunaligned", "+ktail")),   # contiguous X, odd K: unaligned rows
+    (16, 8192, 2048, 0, 1, ("+xunaligned",)),             # misaligned X base, K % 16 == 0
+    (33, 4100, 512, 0, 0, ("+ktail",)),                   # aligned X, K % 16 == 4
+    (5, 1003, 1024, 2, 3, ("+xunaligned", "+ktail")),
 ], ids=["odd-K", "misaligned-X", "aligned-tail", "both"])
-def test_small_m_k_tail_and_x_staging(M, K, N, x_pad, x_off, tags, torch_cuda):
+def test_small_m_k_tail_and_unaligned_x(M, K, N, x_pad, x_off, tags, torch_cuda):
     X, W, b = _inputs(M, K, N, M + K + N)
     got, plan = _run_x_view(torch_cuda, X, W, b, x_pad, x_off)
     assert plan.startswith("gemv_f32"), plan
@@ -212,15 +212,16 @@ _TAIL_EPIS = {"none": (_native.EPI_NONE, None, "none"), "bias": (_native.EPI_BIA
 @pytest.mark.parametrize("M", [1, 32, 64])
 @pytest.mark.parametrize("K, x_pad, x_off", [(2047, 0, 0), (4099, 3, 1), (1003, 0, 2)],
                          ids=["odd-K", "padded-offset", "offset"])
-def test_small_m_tail_and_staging_per_row_block_and_epilogue(M, K, x_pad, x_off, epi_name, torch_cuda):
-    """The staged-X and K-tail paths for one, two and four row blocks, with
-    every epilogue the reduce kernel applies after adding the tail."""
+def test_small_m_tail_and_unaligned_x_per_row_block_and_epilogue(M, K, x_pad, x_off, epi_name, torch_cuda):
+    """Unaligned X rows (read with 4-byte loads) and the K tail for one, two
+    and four row blocks, with every epilogue the reduce kernel applies after
+    adding the tail."""
     epi, use_b, act = _TAIL_EPIS[epi_name]
     N = 1024
     X, W, b = _inputs(M, K, N, 7 * M + K)
     got, plan = _run_x_view(torch_cuda, X, W, b, x_pad, x_off, epi=epi, alpha=0.05)
     assert plan.startswith(f"gemv_f32 mb={(M + 15) // 16}"), plan
-    assert "+ktail" in plan and "+xstage" in plan, plan
+    assert "+ktail" in plan and "+xunaligned" in plan, plan
     ref = oracle.dense_f32(X, W, b if use_b else None, act, 0.05)
     assert_f32_parity(got, ref, K)
 

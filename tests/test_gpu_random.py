@@ -3,7 +3,8 @@
 Each case draws a shape (including K = 0 and sizes that are no multiple of
 any tile; a second set draws multiples of 4 up to 1100 with 16-byte aligned
 views, the shapes the edge tiles and padded int8 tiles serve), a dtype, a pattern, host or device operands, and for device
-operands a padded row stride and an element offset, then compares the HIP
+operands a padded row stride and an element offset (a third set: small M
+with X misaligned on its own and K often not a multiple of 16), then compares the HIP
 result with the oracle: i32 bit-exact (int8-range values take the int8 MFMA
 path, wider ones the exact i32 fallback), f32 within relative Frobenius 1e-5
 and max|delta| <= 1e-4*sqrt(K).
@@ -121,6 +122,47 @@ def _check_case(seed, case, torch):
             raise AssertionError(f"{what}: {e}") from None
 
 
+# Small M with X's own row pad and element offset (often misaligned) while W,
+# b and Y stay 16-byte aligned, and K often not a multiple of 16: the
+# small-M kernel with X rows staged to aligned rows and the K tail added by
+# the reduce kernel, at one to four row blocks.
+_SMALL_M = [1, 5, 16, 17, 32, 48, 64]
+_SMALL_M_K = [1003, 2047, 4099, 4096, 8191]
+_SMALL_M_N = [64, 1000, 1028, 2048, 4100]
+
+
+def _check_small_m(seed, torch):
+    rng = np.random.default_rng(seed)
+    M, K, N = int(rng.choice(_SMALL_M)), int(rng.choice(_SMALL_M_K)), int(rng.choice(_SMALL_M_N))
+    pattern = str(rng.choice(list(_PATTERNS)))
+    bias, act = _PATTERNS[pattern]
+    x_pad, x_off = int(rng.choice([0, 1, 2, 3, 5])), int(rng.choice([0, 1, 2, 3]))
+    w_pad, w_off = int(rng.choice([0, 4])), int(rng.choice([0, 4]))
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.float32(np.sqrt(K))).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, N).astype(np.float32) if bias else None
+    alpha = float(np.float32(rng.uniform(0.01, 0.5)))
+    tX = _device_view(torch, X, x_pad, x_off)
+    tW = _device_view(torch, W, w_pad, w_off)
+    tb = _device_view(torch, b, 0, w_off) if bias else None
+    tY = _device_view(torch, np.zeros((M, N), np.float32), w_pad, w_off)
+    dense_launch(tX, tW, tb, tY, (1 if bias else 0) | (_EPI[act] << 1), alpha)
+    torch.cuda.synchronize()
+    plan = _native.last_plan()
+    what = f"seed={seed} {pattern} M={M} K={K} N={N} x_pad={x_pad} x_off={x_off} w_pad={w_pad} " \
+           f"w_off={w_off} [{plan}]"
+    assert plan.startswith("gemv_f32"), what
+    try:
+        assert_f32_parity(tY.cpu().numpy(), oracle.dense_f32(X, W, b, act, alpha), K)
+    except AssertionError as e:
+        raise AssertionError(f"{what}: {e}") from None
+
+
+@pytest.mark.parametrize("seed", range(2000, 2030))
+def test_random_small_m_case(seed, torch_cuda):
+    _check_small_m(seed, torch_cuda)
+
+
 def test_random_sweep(torch_cuda):
     """Opt-in wide sweep: EDSL_RANDOM_SWEEP=N runs N more seeds of both case
     sets in this one test (N = 20000 takes about six minutes on one MI355X)."""
@@ -131,3 +173,5 @@ def test_random_sweep(torch_cuda):
     for seed in range(10000, 10000 + n):
         _check_case(seed, _case(seed), torch_cuda)
         _check_case(seed, _case(seed, _EDGE_DIMS, pads=(0, 4, 8), offs=(0, 4), k_zero=False), torch_cuda)
+        if seed % 10 == 0:
+            _check_small_m(seed, torch_cuda)
