@@ -137,6 +137,16 @@ struct DeviceState {
 };
 
 constexpr int kMaxDevices = 64;
+// Two locks, always taken in this order when both are held:
+//  g_host_mu: the host-buffer path -- staging buffers, ping-pong buffers,
+//    the pipeline's streams, the pinned ring and its copy threads -- held
+//    for a whole synchronous host-buffer call;
+//  g_mu: device state, tuning overrides and the launch workspaces (split-K
+//    partials, packed int8 operands, their cross-stream ordering), held only
+//    while a launch is planned and enqueued.
+// A device launch from one thread therefore never waits for another thread's
+// host-to-device or device-to-host copies.
+std::mutex g_host_mu;
 std::mutex g_mu;
 DeviceState g_dev[kMaxDevices];
 int g_force_cfg = -1;
@@ -629,7 +639,10 @@ bool pipelined_host_layer(DeviceState& ds, int dev, int dtype, const LayerOp& op
     L.ldx = dldx;
     L.y = dy + r0 * dldy * (int64_t)es;
     L.ldy = dldy;
-    launch_dense(ds, L, ds.pipe_run);
+    {
+      std::lock_guard<std::mutex> lock(g_mu);
+      launch_dense(ds, L, ds.pipe_run);
+    }
     if (i == 0) plan0 = t_plan;
     check_hip(hipEventRecord(ds.ev_g[i], ds.pipe_run), "hipEventRecord");
     if (i > 0) download(i - 1);  // overlaps block i's kernel
@@ -668,11 +681,18 @@ void sync_dense_chain(int dtype, const LayerOp* layers, int n, const Mat& Y) {
     return;
   }
 
-  std::lock_guard<std::mutex> lock(g_mu);
-  read_env_overrides();
+  std::lock_guard<std::mutex> host_lock(g_host_mu);
   int dev = 0;
-  DeviceState& ds = device_state(&dev);
-  if (n == 1 && !g_no_pipeline) {
+  DeviceState* dsp = nullptr;
+  bool no_pipeline = false;
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    read_env_overrides();
+    dsp = &device_state(&dev);
+    no_pipeline = g_no_pipeline;
+  }
+  DeviceState& ds = *dsp;
+  if (n == 1 && !no_pipeline) {
     bool done = false;
     try {
       done = pipelined_host_layer(ds, dev, dtype, layers[0], Y);
@@ -758,7 +778,10 @@ void sync_dense_chain(int dtype, const LayerOp* layers, int n, const Mat& Y) {
       L.y = ystage;
       L.ldy = ystage_ld;
     }
-    launch_dense(ds, L, stream);
+    {
+      std::lock_guard<std::mutex> lock(g_mu);
+      launch_dense(ds, L, stream);
+    }
     if (n > 1) plans += (i ? " | " : "") + t_plan;
     prev = L.y;
     prev_ld = L.ldy;
@@ -807,7 +830,7 @@ ResidentCopy::~ResidentCopy() {
 std::shared_ptr<ResidentCopy> make_resident_copy(const void* src, int64_t rows, int64_t cols, size_t esize) {
   if (rows < 0 || cols < 0) fail(kErrShape, "negative size (%lld, %lld)", (long long)rows, (long long)cols);
   if (!src && rows > 0 && cols > 0) fail(kErrArgument, "null data pointer");
-  std::lock_guard<std::mutex> lock(g_mu);  // the pinned staging ring is shared
+  std::lock_guard<std::mutex> lock(g_host_mu);  // the pinned staging ring is shared
   auto c = std::make_shared<ResidentCopy>();
   c->device = current_device();
   c->rows = rows;
