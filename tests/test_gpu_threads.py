@@ -95,3 +95,55 @@ def test_concurrent_callers():
     assert not any(t.is_alive() for t in threads), "a caller thread did not finish"
     if errors:
         raise errors[0]
+
+
+def test_device_launches_do_not_wait_for_host_copies():
+    """One thread makes host-buffer calls of the c3 size (copies of 128 MiB
+    in and 64 MiB out, ~5 ms each); another enqueues small device launches
+    on its own stream meanwhile. The launch lock is held only while a launch
+    is enqueued, so no enqueue waits for a host call's copies: the slowest
+    one stays far below a host call's duration."""
+    import time
+
+    import torch
+    rng = np.random.default_rng(7)
+    M = K = N = 4096
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / 64).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, N).astype(np.float32)
+    backend.run("dense_relu", X, W, b)  # sizes the staging buffers
+    host_times, enqueue_times, errors = [], [], []
+    stop = threading.Event()
+
+    def host_calls():
+        try:
+            for _ in range(8):
+                t0 = time.perf_counter()
+                backend.run("dense_relu", X, W, b)
+                host_times.append(time.perf_counter() - t0)
+        except Exception as e:  # noqa: BLE001 -- reported below
+            errors.append(repr(e))
+        finally:
+            stop.set()
+
+    s = torch.cuda.Stream()
+    x = torch.randn(16, 512, device="cuda")
+    w = torch.randn(512, 256, device="cuda")
+    y = torch.empty(16, 256, device="cuda")
+    dense_launch(x, w, None, y, _native.EPI_NONE, stream=s)  # warm: plan, workspace
+    torch.cuda.synchronize()
+    t = threading.Thread(target=host_calls)
+    t.start()
+    while not stop.is_set():
+        t0 = time.perf_counter()
+        dense_launch(x, w, None, y, _native.EPI_NONE, stream=s)
+        enqueue_times.append(time.perf_counter() - t0)
+        time.sleep(0.0002)
+    t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    slow_host = min(host_times)
+    enqueue_times.sort()
+    p99 = enqueue_times[int(0.99 * (len(enqueue_times) - 1))]
+    assert len(enqueue_times) > 20, len(enqueue_times)
+    assert p99 < 0.25 * slow_host, (p99, slow_host, enqueue_times[-5:])
