@@ -124,7 +124,7 @@ def _check_case(seed, case, torch):
 
 # Small M with X's own row pad and element offset (often misaligned) while W,
 # b and Y stay 16-byte aligned, and K often not a multiple of 16: the
-# small-M kernel with X rows staged to aligned rows and the K tail added by
+# small-M kernel reading unaligned X rows in place and the K tail added by
 # the reduce kernel, at one to four row blocks.
 _SMALL_M = [1, 5, 16, 17, 32, 48, 64]
 _SMALL_M_K = [1003, 2047, 4099, 4096, 8191]
