@@ -23,6 +23,7 @@
 //  * A tiles are stored row-major in LDS with the 16-byte chunk index XOR-ed by
 //    a row hash, so the 16 lanes of a ds_read_b128 phase hit distinct banks.
 //  * Workgroups map to tiles XCD-aware (common.hpp: tile_coords).
+//  * C is written with non-temporal stores.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -82,7 +83,8 @@ __device__ __forceinline__ void static_for(F&& f) {
 //    masked per vector (N % 4 == 0, so a vector of CP <= 4 columns is all in
 //    or all out).
 //  kGuardAll: any shape and alignment; element-wise checked scalar loads/stores.
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int WAVES_K, int PF, int EPI, int GUARD>
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int WAVES_K, int PF, int EPI, int GUARD,
+          int SCHED = 0>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64)
 gemm_f32_kernel(GemmF32Args args) {
   constexpr int NT = WAVES_M * WAVES_N * WAVES_K * 64;
@@ -103,6 +105,13 @@ gemm_f32_kernel(GemmF32Args args) {
   constexpr int A_LD = A_F4 / NT;
   constexpr int B_LD = B_F4 / NT;
 
+  // SCHED 0: a K step's LDS stores follow its MFMAs. SCHED 1 (tiles with
+  // loads several steps ahead): the next step's LDS stores are issued right
+  // after the step's first fragment reads, ahead of its MFMAs, so the LDS
+  // writes them while the matrix cores run (c2 1024^3: 23.4-23.5 -> 23.0-23.1
+  // us on one box).
+  static_assert(SCHED == 0 || SCHED == 1, "schedule");
+  static_assert(SCHED == 0 || (PF >= 2 && GUARD != kGuardAll), "schedule 1: prefetching vector tiles");
   __shared__ f32x4 sA[2][A_F4];
   __shared__ float sB[2][BK * BN];
 
@@ -241,6 +250,39 @@ gemm_f32_kernel(GemmF32Args args) {
     __builtin_amdgcn_s_setprio(0);
   };
 
+  // SCHED 1: as compute(), with mid() issued right after the first 8-k
+  // group's fragment reads.
+  auto compute_mid = [&](int buf, auto&& mid) {
+    __builtin_amdgcn_s_setprio(1);
+    static_for<JP>([&](auto jjc) {
+      constexpr int jj = decltype(jjc)::value;
+      const int j = wave_k * JP + jj;
+      f32x4 a[RB];
+      float bv[4][CP];
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int row = wave_m * WM + i * 32 + l32;
+        const int q = 2 * j + half;
+        a[i] = sA[buf][row * KCH + (q ^ a_swizzle<KCH>(row))];
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) load_b_frag<CP>(&sB[buf][(8 * j + 4 * half + s) * BN + wave_n * WN + CP * l32], bv[s]);
+      if constexpr (jj == 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        mid();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int c = 0; c < CP; ++c)
+            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], bv[s][c], acc[i][c], 0, 0, 0);
+    });
+    __builtin_amdgcn_s_setprio(0);
+  };
+
   // K steps of the main loop: all of them, or with the edge guard the whole
   // ones only (the partial step follows the loop).
   const int nk = GUARD == kGuardEdge ? K / BK : (K + BK - 1) / BK;
@@ -281,9 +323,14 @@ gemm_f32_kernel(GemmF32Args args) {
       // Keep the loads ahead of this step's MFMAs (the scheduler would
       // otherwise sink them and shorten their lead).
       __builtin_amdgcn_sched_barrier(0);
-      compute(kt & 1);
-      __builtin_amdgcn_sched_barrier(0);
-      store_lds(Ic<(C + 1) % PF>{}, (kt + 1) & 1);
+      if constexpr (SCHED == 1) {
+        // LDS buffer (kt + 1) & 1 was last read before the previous barrier.
+        compute_mid(kt & 1, [&] { store_lds(Ic<(C + 1) % PF>{}, (kt + 1) & 1); });
+      } else {
+        compute(kt & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        store_lds(Ic<(C + 1) % PF>{}, (kt + 1) & 1);
+      }
       __syncthreads();
     };
     int kt = 0;
@@ -299,8 +346,12 @@ gemm_f32_kernel(GemmF32Args args) {
       }
       static_for<PF>([&](auto s) {
         constexpr int C = decltype(s)::value;
-        compute((kt + C) & 1);
-        if constexpr (C + 1 < PF) {
+        if constexpr (SCHED == 1 && C + 1 < PF) {
+          compute_mid((kt + C) & 1, [&] { store_lds(Ic<C + 1>{}, (kt + C + 1) & 1); });
+        } else {
+          compute((kt + C) & 1);
+        }
+        if constexpr (SCHED != 1 && C + 1 < PF) {
           __builtin_amdgcn_sched_barrier(0);
           store_lds(Ic<C + 1>{}, (kt + C + 1) & 1);
         }
@@ -396,14 +447,14 @@ gemm_f32_kernel(GemmF32Args args) {
       float* dst = args.C + (int64_t)row * args.ldc + col0;
       if constexpr (GUARD != kGuardAll) {
         if (GUARD == kGuardNone || (row < M && col0 < N)) {
+          // Non-temporal: C is not read again by this kernel (c2 23.0 ->
+          // 22.6 us on one box; c1, c3 and the c3 column shard unchanged).
           if constexpr (CP == 4) {
-            f32x4 t = {v[0], v[1], v[2], v[3]};
-            *reinterpret_cast<f32x4*>(dst) = t;
+            __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4*>(dst));
           } else if constexpr (CP == 2) {
-            f32x2 t = {v[0], v[1]};
-            *reinterpret_cast<f32x2*>(dst) = t;
+            __builtin_nontemporal_store(f32x2{v[0], v[1]}, reinterpret_cast<f32x2*>(dst));
           } else {
-            *dst = v[0];
+            __builtin_nontemporal_store(v[0], dst);
           }
         }
       } else {
@@ -441,7 +492,8 @@ gemm_f32_kernel(GemmF32Args args) {
 //      workgroup per CU, nothing else on the CU to hide a step's loads)
 //      24.1-24.4 vs 24.6-25.0 us for 22; at 4096x512x4096 (two per CU) 171
 //      vs 163 us. Three steps ahead, and 64-deep steps four ahead, measured
-//      no better than 22.
+//      no better than 22. Its LDS stores are issued ahead of the MFMAs
+//      (SCHED 1); the same order on 22 measured 1 % slower at 4096x512x4096.
 //  25: 32x32x64 (k4) with all four 64-deep K steps of a 256-deep K loaded
 //      up front (256^3: 7.54 vs 7.31 TFLOP/s for 17)
 //  26-30: edge-tile twins of 23, 2, 24, 22 and 25 (kGuardEdge) for shapes
@@ -481,13 +533,13 @@ const GemmF32Config kConfigs[] = {
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
-template <int BM, int BN, int BK, int WMW, int WNW, int WKW, int GUARD, int PF = 1>
+template <int BM, int BN, int BK, int WMW, int WNW, int WKW, int GUARD, int PF = 1, int SCHED = 0>
 hipError_t launch_cfg(int epi, const GemmF32Args& a, hipStream_t stream) {
   const dim3 grid(a.tiles_m * a.tiles_n);
   const dim3 block(WMW * WNW * WKW * 64);
 #define EDSL_F32_CASE(E)                                                                           \
   case E:                                                                                          \
-    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WMW, WNW, WKW, PF, E, GUARD>), grid, block, 0, \
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WMW, WNW, WKW, PF, E, GUARD, SCHED>), grid, block, 0, \
                        stream, a);                                                                 \
     break;
   switch (epi) {
@@ -535,11 +587,11 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case 21: return launch_cfg<64, 64, 64, 2, 2, 4, kGuardNone>(epi, a, stream);
     case 22: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardNone, 2>(epi, a, stream);
     case 23: return launch_cfg<256, 256, 16, 4, 4, 1, kGuardNone>(epi, a, stream);
-    case 24: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardNone, 4>(epi, a, stream);
+    case 24: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardNone, 4, 1>(epi, a, stream);
     case 25: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardNone, 4>(epi, a, stream);
     case 26: return launch_cfg<256, 256, 16, 4, 4, 1, kGuardEdge>(epi, a, stream);
     case 27: return launch_cfg<128, 128, 16, 2, 2, 1, kGuardEdge>(epi, a, stream);
-    case 28: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardEdge, 4>(epi, a, stream);
+    case 28: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardEdge, 4, 1>(epi, a, stream);
     case 29: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardEdge, 2>(epi, a, stream);
     case 30: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardEdge, 4>(epi, a, stream);
     default: return hipErrorInvalidValue;
