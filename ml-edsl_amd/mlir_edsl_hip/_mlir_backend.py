@@ -108,6 +108,23 @@ def _raise(where: str) -> None:
     raise RuntimeError(msg if msg else f"{where} failed (code {code})")
 
 
+_new_bytes = ctypes.pythonapi.PyBytes_FromStringAndSize
+_new_bytes.restype = ctypes.py_object
+_new_bytes.argtypes = [ctypes.c_void_p, ctypes.c_ssize_t]
+_bytes_data = ctypes.pythonapi.PyBytes_AsString
+_bytes_data.restype = ctypes.c_void_p
+_bytes_data.argtypes = [ctypes.py_object]
+
+
+def _output_bytes(nbytes: int):
+    """A new, not yet shared bytes object of nbytes (> 0) bytes, left
+    uninitialised, and the address of its contents: the runtime writes the
+    result there, as a C extension fills a bytes object before returning it
+    (no zero fill and no copy of the result into a second object)."""
+    out = _new_bytes(None, nbytes)
+    return out, _bytes_data(out)
+
+
 _INJECTED = "__test_failure_inject__"
 _REFERENCE_MODULES = ("mlir_edsl._mlir_backend_ref", "_mlir_backend_ref")
 _UNSET = object()
@@ -319,17 +336,21 @@ class MLIRCompiler:
         out_elems = 1
         for d in output_shape:
             out_elems *= int(d)
-        out = ctypes.create_string_buffer(out_elems * int(element_size))
+        nbytes = out_elems * int(element_size)
+        if nbytes > 0:
+            out, out_ptr = _output_bytes(nbytes)
+        else:  # the shared empty bytes object is never written
+            out, out_ptr = b"", ctypes.cast(ctypes.create_string_buffer(1), ctypes.c_void_p)
         oshape = (ctypes.c_int64 * len(output_shape))(*[int(d) for d in output_shape])
         rc = _L().edsl_hip_module_execute_gpu_function(
-            self._m, name.encode(), n, ptrs, shapes, ranks, ctypes.cast(out, ctypes.c_void_p), oshape,
-            len(output_shape), int(element_size))
+            self._m, name.encode(), n, ptrs, shapes, ranks, out_ptr, oshape, len(output_shape),
+            int(element_size))
         if rc != 0:
             _raise("execute_gpu_function")
         if self._capture:  # the kernels of the latest run of each function
             run = (f"run:{name}", _native.last_plan())
             self._snapshots = [sn for sn in self._snapshots if sn[0] != run[0]] + [run]
-        return out.raw
+        return out
 
     # ----------------------------------------------------------- extension
     def _param_index(self, name: str, param) -> int:

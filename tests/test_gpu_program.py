@@ -118,7 +118,13 @@ def test_reference_program_runs_three_ways(case, torch_cuda):
         # 3) execute_gpu_function with (pointer, shape) pairs, element size from the dtype
         raw = comp.execute_gpu_function(name, [(a.ctypes.data, list(a.shape)) for a in args],
                                         list(ref.shape), ref.dtype.itemsize)
+        assert type(raw) is bytes and len(raw) == ref.nbytes  # the reference returns py::bytes
         _check(np.frombuffer(raw, dtype=ref.dtype).reshape(ref.shape), ref, K)
+        # a second call returns a new object; the first result is unchanged
+        first = bytes(raw)
+        raw2 = comp.execute_gpu_function(name, [(a.ctypes.data, list(a.shape)) for a in args],
+                                         list(ref.shape), ref.dtype.itemsize)
+        assert raw2 is not raw and raw == first and raw2 == first
     if "execute_gpu_function" in case:  # the reference front end's call has the same shapes
         call = case["execute_gpu_function"]
         assert call["input_shapes"] == case["param_shapes"] and call["element_size"] == 4
