@@ -6,6 +6,7 @@ import of the ops that need it fails with :class:`NativeLibraryError`.
 from __future__ import annotations
 
 import ctypes
+import importlib.util
 import os
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libedsl_hip.so")
@@ -82,6 +83,22 @@ def _declare(L: ctypes.CDLL) -> None:
     L.edsl_hip_f32_config_name.restype = c_int
 
 
+def _share_torch_hip_runtime() -> None:
+    """Map torch's own HIP runtime, when torch is installed, before the
+    library. torch ships a libamdhip64 with the same SONAME as the system one
+    the library is linked against, but asks for it under another file name:
+    had the library come first, importing torch later would map a second HIP
+    runtime, and two in one process fail to find the device. Mapped first
+    (by path, without importing torch), it serves both: the library's
+    dependency matches its SONAME and torch's its file."""
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.origin:
+        return
+    runtime = os.path.join(os.path.dirname(spec.origin), "lib", "libamdhip64.so")
+    if os.path.exists(runtime):
+        ctypes.CDLL(runtime)
+
+
 def lib() -> ctypes.CDLL:
     """The loaded runtime library (loaded once per process)."""
     global _lib
@@ -90,6 +107,7 @@ def lib() -> ctypes.CDLL:
             raise NativeLibraryError(
                 f"{LIB_PATH} is not built; run __graft_entry__.build() (or "
                 "python -m mlir_edsl_hip.build) first")
+        _share_torch_hip_runtime()
         try:
             L = ctypes.CDLL(LIB_PATH)
         except OSError as e:

@@ -59,9 +59,29 @@ def build(jobs: int = 4, verbose: bool = False) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
+    ext = build_launch_module()
     if verbose:
         print(f"built {LIB_PATH}")
+        print(f"built {ext}")
     return LIB_PATH
+
+
+def build_launch_module() -> str:
+    """The CPython binding of the device launch entries (csrc/pylaunch.c),
+    linked against libedsl_hip.so next to it (found through $ORIGIN, so the
+    process maps the one library that _native also loads)."""
+    import sysconfig
+    out = os.path.join(PKG_DIR, "_launch" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out + ".tmp"
+    cc = os.environ.get("CC") or shutil.which("gcc") or "cc"
+    cmd = [cc, "-O2", "-fPIC", "-shared", "-Wall", "-Werror", f"-I{sysconfig.get_paths()['include']}",
+           os.path.join(CSRC, "pylaunch.c"), "-o", tmp, f"-L{PKG_DIR}", "-l:" + LIB_NAME,
+           "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"building the launch module failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

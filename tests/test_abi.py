@@ -7,6 +7,7 @@ import glob
 import os
 import re
 import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -187,3 +188,49 @@ def test_config_table_is_exposed():
     names = _native.f32_config_names()
     assert len(names) >= 5 and all(n.startswith("f32_") for n in names)
     assert any("guard" in n for n in names)
+
+
+def test_fastcall_launch_module_reaches_the_same_library():
+    """The METH_FASTCALL binding (csrc/pylaunch.c) is built beside the
+    library, maps the same library instance that ctypes loads (one set of
+    runtime state, one last-error slot), and reports the entries' status
+    codes; argument errors are Python errors. No call here reaches a kernel."""
+    from mlir_edsl_hip import device
+    L = _native.lib()
+    device._torch_module()  # loads the binding after the library
+    assert device._launch is not None, "the launch module is not built"
+    maps = {line.split()[-1] for line in open("/proc/self/maps") if "libedsl_hip" in line}
+    assert len(maps) == 1, maps
+    # bias epilogue with a null bias: rejected by the library before any device call
+    rc = device._launch.dense_f32(0, 4, 0, 4, None, 0, 4, 4, 4, 4, 1, 0.0, 0)
+    assert rc == _native.last_error()[0] != 0
+    assert "bias" in _native.last_error()[1]
+    rc = device._launch.dense_i32(0, 4, 0, 4, None, 0, 4, 4, 4, 4, 1, 0)
+    assert rc != 0 and "bias" in _native.last_error()[1]
+    # ldx < K with M > 1: the stride check, through both bindings, same code
+    rc_fast = device._launch.dense_f32(8, 2, 8, 4, None, 8, 4, 4, 4, 4, 0, 0.0, 0)
+    rc_ctypes = L.edsl_hip_dense_f32_launch(8, 2, 8, 4, None, 8, 4, 4, 4, 4, 0, 0.0, 0)
+    assert rc_fast == rc_ctypes != 0
+    with pytest.raises(TypeError, match="13 arguments"):
+        device._launch.dense_f32(1, 2, 3)
+    with pytest.raises(TypeError):
+        device._launch.dense_i32(0, "4", 0, 4, None, 0, 4, 4, 4, 4, 1, 0)
+
+
+@pytest.mark.parametrize("order", ["library_first", "torch_first"])
+def test_one_hip_runtime_whichever_loads_first(order):
+    """torch carries its own HIP runtime with the system one's SONAME; the
+    library must share it in either import order (two runtimes in one process
+    cannot both open the device). Run in a fresh process."""
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "if %r == 'torch_first':\n    import torch\n"
+        "from mlir_edsl_hip import _native, device\n"
+        "_native.lib()\n"
+        "import torch\n"
+        "device._torch_module()\n"
+        "maps = {l.split()[-1] for l in open('/proc/self/maps') if 'libamdhip64' in l}\n"
+        "print(len(maps))\n" % (os.path.join(os.path.dirname(os.path.dirname(__file__)), "ml-edsl_amd"), order))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip().splitlines()[-1] == "1", out.stdout

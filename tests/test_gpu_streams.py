@@ -67,3 +67,49 @@ def test_scratch_users_on_two_streams(kinds):
                 assert np.array_equal(got, ref), f"round {r} stream {j}"
             else:
                 assert_f32_parity(got, ref, K)
+
+
+def test_launch_without_a_stream_uses_the_current_one():
+    """dense_launch without a stream argument enqueues on torch's current
+    stream, read through torch's raw-handle accessor: the same handle as
+    torch.cuda.current_stream(), inside and outside a stream context."""
+    import torch
+    from mlir_edsl_hip import device
+    device._torch_module()
+    assert device._raw_stream() == torch.cuda.current_stream().cuda_stream
+    rng = np.random.default_rng(12)
+    (X, W, b), Y, ref, K = _problem(torch, rng, "f32", 64, 256, 128)
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        assert device._raw_stream() == s.cuda_stream
+        torch.cuda._sleep(SPIN_CYCLES)
+        dense_launch(X, W, b, Y, _native.EPI_BIAS_RELU)
+        done = torch.cuda.Event()
+        done.record()
+    done.synchronize()
+    assert_f32_parity(Y.cpu().numpy(), ref, K)
+    assert device._raw_stream() == torch.cuda.current_stream().cuda_stream
+
+
+def test_dense_launch_operand_errors_name_the_operand():
+    import torch
+    d = "cuda"
+    X, W, b, Y = (torch.zeros(4, 8, device=d), torch.zeros(8, 16, device=d), torch.zeros(16, device=d),
+                  torch.zeros(4, 16, device=d))
+    cases = [
+        ((X, W.int(), b, Y), TypeError, "W has dtype"),
+        ((X, W, b, Y.cpu()), ValueError, "Y must be a GPU tensor"),
+        ((X, torch.zeros(16, 8, device=d).t(), b, Y), ValueError, "W must have unit inner stride"),
+        ((X, W, b, torch.zeros(4, 15, device=d)), ValueError, "shape mismatch"),
+        ((X, torch.zeros(7, 16, device=d), b, Y), ValueError, "shape mismatch"),
+        ((X, W, torch.zeros(15, device=d), Y), ValueError, "bias shape"),
+        ((X, W, torch.zeros(32, device=d)[::2], Y), ValueError, "b must have unit inner stride"),
+        ((X.reshape(4, 8, 1), W, b, Y), ValueError, "2-D"),
+    ]
+    for args, exc, msg in cases:
+        with pytest.raises(exc, match=msg):
+            dense_launch(*args, _native.EPI_BIAS_RELU)
+    dense_launch(X, W, b, Y, _native.EPI_BIAS_RELU)  # the same operands, correct, still launch
+    torch.cuda.synchronize()
+    assert torch.equal(Y, torch.zeros_like(Y))

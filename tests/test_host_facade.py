@@ -136,3 +136,15 @@ def test_execute_gpu_function_builds_no_reference_cycles():
     finally:
         gc.enable()
     assert unreachable < 20, unreachable  # the per-call arrays left ~1000 here
+
+
+def test_dense_launch_rejects_host_tensors_before_any_device_call():
+    # The combined operand check fails on a CPU tensor and the detailed
+    # checks name the operand; nothing reaches the library.
+    import torch
+    from mlir_edsl_hip.device import dense_launch
+    X, W, Y = torch.zeros(4, 8), torch.zeros(8, 16), torch.zeros(4, 16)
+    with pytest.raises(ValueError, match="X must be a GPU tensor"):
+        dense_launch(X, W, None, Y, 0)
+    with pytest.raises(TypeError, match="unsupported dtype"):
+        dense_launch(X.double(), W.double(), None, Y.double(), 0)
