@@ -96,7 +96,10 @@ def _share_torch_hip_runtime() -> None:
         return
     runtime = os.path.join(os.path.dirname(spec.origin), "lib", "libamdhip64.so")
     if os.path.exists(runtime):
-        ctypes.CDLL(runtime)
+        try:
+            ctypes.CDLL(runtime)
+        except OSError:  # unusable: the library brings the system runtime
+            pass
 
 
 def lib() -> ctypes.CDLL:
