@@ -165,7 +165,9 @@ def test_random_small_m_case(seed, torch_cuda):
 
 def test_random_sweep(torch_cuda):
     """Opt-in wide sweep: EDSL_RANDOM_SWEEP=N runs N more seeds of both case
-    sets in this one test (N = 20000 takes about six minutes on one MI355X)."""
+    sets (and a small-M case every tenth seed) in this one test. N = 20000
+    takes about seven and a half minutes on one MI355X; run it with -s to see
+    a progress line every 1000 seeds."""
     import os
     n = int(os.environ.get("EDSL_RANDOM_SWEEP", "0"))
     if n <= 0:
@@ -175,3 +177,5 @@ def test_random_sweep(torch_cuda):
         _check_case(seed, _case(seed, _EDGE_DIMS, pads=(0, 4, 8), offs=(0, 4), k_zero=False), torch_cuda)
         if seed % 10 == 0:
             _check_small_m(seed, torch_cuda)
+        if (seed - 9999) % 1000 == 0:  # progress, visible with pytest -s
+            print(f"random sweep: {seed - 9999} of {n} seeds passed", flush=True)
