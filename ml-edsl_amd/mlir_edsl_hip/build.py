@@ -74,7 +74,7 @@ def build_launch_module() -> str:
     out = os.path.join(PKG_DIR, "_launch" + sysconfig.get_config_var("EXT_SUFFIX"))
     tmp = out + ".tmp"
     cc = os.environ.get("CC") or shutil.which("gcc") or "cc"
-    cmd = [cc, "-O2", "-fPIC", "-shared", "-Wall", "-Werror", f"-I{sysconfig.get_paths()['include']}",
+    cmd = [cc, "-O2", "-fPIC", "-shared", "-Wall", f"-I{sysconfig.get_paths()['include']}",
            os.path.join(CSRC, "pylaunch.c"), "-o", tmp, f"-L{PKG_DIR}", "-l:" + LIB_NAME,
            "-Wl,-rpath,$ORIGIN"]
     res = subprocess.run(cmd, capture_output=True, text=True)
