@@ -82,6 +82,11 @@ __device__ __forceinline__ void static_for(F&& f) {
 //    step follows it once, with loads past K skipped and zero. Stores are
 //    masked per vector (N % 4 == 0, so a vector of CP <= 4 columns is all in
 //    or all out).
+//  kGuardScalar: as kGuardEdge (whole K steps in the loop, then the partial
+//    step; rows past M read row M-1, columns past N read column N-1), with
+//    4-byte loads and stores: rows of any alignment, K and N of any value.
+//    A chunk's 4 k of an A row are consecutive (one address, immediate
+//    offsets); B columns are clamped only in tiles that reach past N.
 //  kGuardAll: any shape and alignment; element-wise checked scalar loads/stores.
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int WAVES_K, int PF, int EPI, int GUARD,
           int SCHED = 0>
@@ -154,6 +159,15 @@ gemm_f32_kernel(GemmF32Args args) {
         } else {
           ra[S][i] = *reinterpret_cast<const f32x4*>(src);
         }
+      } else if constexpr (GUARD == kGuardScalar) {
+        const float* src = args.A + (int64_t)min(gm, M - 1) * args.lda + gk;
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (decltype(tail)::value) v[e] = gk + e < K ? src[e] : 0.0f;
+          else v[e] = src[e];
+        }
+        ra[S][i] = v;
       } else {
         f32x4 v;
 #pragma unroll
@@ -180,6 +194,21 @@ gemm_f32_kernel(GemmF32Args args) {
         } else {
           rb[S][i] = *reinterpret_cast<const f32x4*>(src);
         }
+      } else if constexpr (GUARD == kGuardScalar) {
+        const bool in_k = !decltype(tail)::value || gk < K;
+        const float* src = args.B + (int64_t)(in_k ? gk : K - 1) * args.ldb;
+        f32x4 v;
+        if (n0 + BN <= N) {  // uniform: the tile lies inside N
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = src[gn + e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = src[min(gn + e, N - 1)];
+        }
+        if constexpr (decltype(tail)::value) {
+          if (!in_k) v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        rb[S][i] = v;
       } else {
         f32x4 v;
 #pragma unroll
@@ -285,7 +314,8 @@ gemm_f32_kernel(GemmF32Args args) {
 
   // K steps of the main loop: all of them, or with the edge guard the whole
   // ones only (the partial step follows the loop).
-  const int nk = GUARD == kGuardEdge ? K / BK : (K + BK - 1) / BK;
+  constexpr bool kPartialStep = GUARD == kGuardEdge || GUARD == kGuardScalar;
+  const int nk = kPartialStep ? K / BK : (K + BK - 1) / BK;
   const std::false_type body{};
   if constexpr (PF == 1) {
     if (nk > 0) {
@@ -368,7 +398,7 @@ gemm_f32_kernel(GemmF32Args args) {
       });
     }
   }
-  if constexpr (GUARD == kGuardEdge) {
+  if constexpr (kPartialStep) {
     // The partial last K step (K % BK != 0), zero past K. Every path above
     // ended with a barrier, so LDS buffer nk & 1 is free.
     if (nk * BK < K) {
@@ -445,7 +475,7 @@ gemm_f32_kernel(GemmF32Args args) {
 #pragma unroll
       for (int c = 0; c < CP; ++c) v[c] = apply_epilogue_f32<EPI>(acc[i][c][r], bvals[c], alpha);
       float* dst = args.C + (int64_t)row * args.ldc + col0;
-      if constexpr (GUARD != kGuardAll) {
+      if constexpr (GUARD == kGuardNone || GUARD == kGuardEdge) {
         if (GUARD == kGuardNone || (row < M && col0 < N)) {
           // Non-temporal: C is not read again by this kernel (c2 23.0 ->
           // 22.6 us on one box; c1, c3 and the c3 column shard unchanged).
@@ -456,6 +486,12 @@ gemm_f32_kernel(GemmF32Args args) {
           } else {
             __builtin_nontemporal_store(v[0], dst);
           }
+        }
+      } else if constexpr (GUARD == kGuardScalar) {
+        if (row < M) {
+#pragma unroll
+          for (int c = 0; c < CP; ++c)
+            if (col0 + c < N) __builtin_nontemporal_store(v[c], dst + c);
         }
       } else {
         if (row < M) {
@@ -498,6 +534,10 @@ gemm_f32_kernel(GemmF32Args args) {
 //      up front (256^3: 7.54 vs 7.31 TFLOP/s for 17)
 //  26-30: edge-tile twins of 23, 2, 24, 22 and 25 (kGuardEdge) for shapes
 //      the tile does not divide
+//  31-35: any-shape twins of the same five (kGuardScalar: 4-byte loads and
+//      stores at clamped addresses), for operands whose rows are not 16-byte
+//      aligned or whose K or N is not a multiple of 4; these layers stay on
+//      the large MFMA tiles instead of the small guarded 64x64x16 one
 const GemmF32Config kConfigs[] = {
     {256, 256, 16, 2, 2, kGuardNone, "f32_256x256x16_w2x2"},
     {256, 256, 16, 4, 2, kGuardNone, "f32_256x256x16_w4x2"},
@@ -530,6 +570,11 @@ const GemmF32Config kConfigs[] = {
     {64, 64, 32, 2, 2, kGuardEdge, "f32_64x64x32_w2x2_k2_pf4_edge"},
     {64, 64, 64, 2, 2, kGuardEdge, "f32_64x64x64_w2x2_k2_pf2_edge"},
     {32, 32, 64, 1, 1, kGuardEdge, "f32_32x32x64_w1x1_k4_pf4_edge"},
+    {256, 256, 16, 4, 4, kGuardScalar, "f32_256x256x16_w4x4_anyshape"},
+    {128, 128, 16, 2, 2, kGuardScalar, "f32_128x128x16_w2x2_anyshape"},
+    {64, 64, 32, 2, 2, kGuardScalar, "f32_64x64x32_w2x2_k2_pf4_anyshape"},
+    {64, 64, 64, 2, 2, kGuardScalar, "f32_64x64x64_w2x2_k2_pf2_anyshape"},
+    {32, 32, 64, 1, 1, kGuardScalar, "f32_32x32x64_w1x1_k4_pf4_anyshape"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -594,6 +639,11 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case 28: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardEdge, 4, 1>(epi, a, stream);
     case 29: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardEdge, 2>(epi, a, stream);
     case 30: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardEdge, 4>(epi, a, stream);
+    case 31: return launch_cfg<256, 256, 16, 4, 4, 1, kGuardScalar>(epi, a, stream);
+    case 32: return launch_cfg<128, 128, 16, 2, 2, 1, kGuardScalar>(epi, a, stream);
+    case 33: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardScalar, 4, 1>(epi, a, stream);
+    case 34: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardScalar, 2>(epi, a, stream);
+    case 35: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardScalar, 4>(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

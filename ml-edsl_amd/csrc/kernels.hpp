@@ -24,6 +24,7 @@ enum : int {
   kGuardNone = 0,  // M, N, K multiples of the tile; 16-byte aligned operands and row strides
   kGuardEdge = 1,  // partial edge tiles; 16-byte aligned operands, strides, N and K multiples of 4
   kGuardAll = 2,   // any shape and alignment (element-wise checks)
+  kGuardScalar = 3,  // partial edge tiles, any alignment, K and N: 4-byte accesses at clamped addresses
 };
 
 struct GemmF32Config {

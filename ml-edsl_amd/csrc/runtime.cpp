@@ -399,11 +399,12 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   auto fits = [&](int c) {
     const GemmF32Config& g = gemm_f32_config(c);
     if (g.guard == kGuardNone) return aligned && K > 0 && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
-    return g.guard == kGuardEdge && edge_ok;
+    if (g.guard == kGuardEdge) return edge_ok;
+    return K > 0;  // kGuardScalar, kGuardAll: any shape, stride and alignment
   };
   if (g_force_cfg >= 0 && g_force_cfg < gemm_f32_num_configs() && fits(g_force_cfg)) {
     cfg = g_force_cfg;
-  } else if (aligned && K > 0) {
+  } else if (K > 0) {
     // Measured on MI355X: 256x256x16 with 16 waves at 4096^3 (992 us; 256x256x32 with 8 waves
     // 1012 us, the next in line); at 1024^3 the 64x64x64 tile with two
     // waves per output block splitting K and global loads two K steps ahead (24.9 us) beats
@@ -417,18 +418,25 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     // At 256^3 the 32x32x64 tile with four K waves loads all four K steps
     // up front (25: 7.54-7.56 TFLOP/s against 7.31 for 17, one step ahead;
     // 2 steps ahead, 8 K waves, or 128-deep steps measured lower).
-    // Each entry: the configuration for shapes the tile divides, and its
-    // edge-tile twin (partial tiles at the M, N, K edges) or -1.
-    static const int kOrder[][2] = {{23, 26}, {5, -1}, {0, -1}, {6, -1}, {2, 27}, {24, 28},
-                                    {22, 29}, {21, -1}, {14, -1}, {15, -1}, {3, -1}, {25, 30}};
+    // Each entry: the configuration for shapes the tile divides, its
+    // edge-tile twin (partial tiles at the M, N, K edges, 16-byte aligned
+    // rows) and its any-shape twin (element-checked loads and stores: rows
+    // of any alignment, K and N of any value), or -1. The any-shape twins
+    // keep unaligned layers on the same large tiles (2001^3: 57.8 TFLOP/s on
+    // the small guarded tile alone).
+    static const int kOrder[][3] = {{23, 26, 31}, {5, -1, -1}, {0, -1, -1}, {6, -1, -1}, {2, 27, 32},
+                                    {24, 28, 33}, {22, 29, 34}, {21, -1, -1}, {14, -1, -1}, {15, -1, -1},
+                                    {3, -1, -1}, {25, 30, 35}};
     int best = -1, first_rejected = -1;
     int64_t best_tiles = 0;
     for (const auto& e : kOrder) {
-      const int c = fits(e[0]) ? e[0] : (e[1] >= 0 && fits(e[1]) ? e[1] : -1);
+      int c = -1;
+      for (int t = 0; t < 3 && c < 0; ++t)
+        if (e[t] >= 0 && fits(e[t])) c = e[t];
       if (c < 0) continue;
       const GemmF32Config& g = gemm_f32_config(c);
       const int64_t tiles = (int64_t)((M + g.bm - 1) / g.bm) * ((N + g.bn - 1) / g.bn);
-      if ((c == 24 || c == 28) && tiles > ds.cus) continue;
+      if (e[0] == 24 && tiles > ds.cus) continue;
       if (tiles >= ds.cus) {
         // Tiles larger than 64x64 that need more than one round of
         // workgroups are taken only when the last round keeps at least

@@ -2,7 +2,8 @@
 
 The fp32 tiles have edge variants (partial tiles at the M, N and K edges,
 16-byte vector loads at clamped addresses, masked stores) for 16-byte aligned
-operands whose K, N and row strides are multiples of 4; the small-M kernel
+operands whose K, N and row strides are multiples of 4, and any-shape variants
+(element-checked 4-byte loads and stores) for every other layout; the small-M kernel
 spreads K over its wave slices in 16-row chunks, so K need only be a multiple
 of 16, and its last column block may be partial, so N need only be a multiple
 of 4. Every case is checked against the oracle on the full output.
@@ -105,12 +106,50 @@ def test_aligned_shapes_keep_their_tiles(torch_cuda):
         assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
 
 
-def test_unaligned_k_takes_the_checked_tile(torch_cuda):
-    """K not a multiple of 4 leaves rows unaligned: the element-checked tile."""
+def test_unaligned_k_takes_an_any_shape_tile(torch_cuda):
+    """K not a multiple of 4 leaves rows unaligned: an element-checked tile."""
     X, W, b = _inputs(70, 37, 50, 9)
     got, plan = _run(torch_cuda, X, W, b)
-    assert "guard" in plan, plan
+    assert "anyshape" in plan, plan
     assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), 37)
+
+
+# K and N of every residue mod 4, M past and below the tiles; with an odd row
+# pitch and an element offset no row is 16-byte aligned.
+ODD_SHAPES = [(300, 101, 259), (257, 37, 133), (65, 3, 7), (97, 1001, 1029), (1, 1, 1), (130, 2002, 66)]
+
+
+def test_every_any_shape_config_on_odd_shapes(torch_cuda):
+    from mlir_edsl_hip.device import set_f32_config
+    names = _native.f32_config_names()
+    anyshape = [(c, n) for c, n in enumerate(names) if n.endswith("_anyshape")]
+    assert len(anyshape) == 5
+    try:
+        for cfg, name in anyshape:
+            set_f32_config(cfg)
+            for i, (M, K, N) in enumerate(ODD_SHAPES):
+                X, W, b = _inputs(M, K, N, 200 + i)
+                ref = oracle.dense_f32(X, W, b, "relu")
+                for pad, off in ((0, 0), (3, 1)):
+                    got, plan = _run(torch_cuda, X, W, b, pad, off)
+                    assert name in plan, (name, plan, (M, K, N))
+                    assert_f32_parity(got, ref, K)
+    finally:
+        set_f32_config(-1)
+
+
+@pytest.mark.parametrize("shape, pad_off, tile", [
+    ((2001, 2001, 2001), (0, 0), "f32_128x128x16_w2x2_anyshape"),
+    ((1025, 1025, 1025), (0, 0), "f32_64x64x64_w2x2_k2_pf2_anyshape"),
+    # K = N = 2048 but every row misaligned by an element offset
+    ((2048, 2048, 2048), (0, 1), "f32_128x128x16_w2x2_anyshape"),
+], ids=["2001^3", "1025^3", "2048^3-offset"])
+def test_auto_plan_takes_any_shape_tiles(shape, pad_off, tile, torch_cuda):
+    M, K, N = shape
+    X, W, b = _inputs(M, K, N, M + 3 * K + N)
+    got, plan = _run(torch_cuda, X, W, b, *pad_off)
+    assert f"cfg={tile} " in plan, plan
+    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
 
 
 @pytest.mark.parametrize("M, K, N", [(16, 8000, 8192), (16, 8000, 1024), (3, 4112, 2048), (40, 1040, 512)])
