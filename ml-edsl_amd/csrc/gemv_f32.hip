@@ -59,7 +59,11 @@ __device__ __forceinline__ float epilogue_rt(float acc, float b, float alpha, in
 // XV: X rows are 16-byte aligned (row stride % 4 == 0) and are read with one
 // 16-byte load per row block and step; otherwise with four 4-byte loads
 // (X is small and read from the caches, so this costs little against W).
-template <int MB, int CPL, int WN, bool XV>
+// WV: W, Y and the bias are 16-byte aligned, their row strides and N
+// multiples of 4: a lane's CPL columns are one vector load or store, all in
+// or all out of range. Otherwise every column is a 4-byte access; columns
+// past N read column N - 1 and are not stored.
+template <int MB, int CPL, int WN, bool XV, bool WV>
 __global__ void __launch_bounds__(kWavesPerWG * 64)
 gemv_f32_kernel(GemvF32Args a, int epi) {
   using vec = typename std::conditional<CPL == 4, f32x4, f32x2>::type;
@@ -97,10 +101,25 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
     for (int c = 0; c < CPL; ++c) acc[mb][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int64_t ldw = a.ldw;
-  // Lanes whose columns lie past N (a partial last column block) read the
-  // last CPL columns instead; their results are never stored. N % 4 == 0, so
-  // a lane's CPL columns are all in or all out.
-  const float* wbase = a.W + (int64_t)(kbeg + 4 * lg) * ldw + min(n0 + CPL * li, a.N - CPL);
+  // WV: lanes whose columns lie past N (a partial last column block) read
+  // the last CPL columns instead; their results are never stored. N % 4 ==
+  // 0, so a lane's CPL columns are all in or all out. Otherwise wbase is the
+  // row start and cofs the lane's columns, each clamped to N - 1.
+  const int col_lane = n0 + CPL * li;
+  const float* wbase = a.W + (int64_t)(kbeg + 4 * lg) * ldw + (WV ? min(col_lane, a.N - CPL) : 0);
+  int cofs[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) cofs[c] = min(col_lane + c, a.N - 1);
+  auto load_row = [&](const float* row) {
+    if constexpr (WV) {
+      return __builtin_nontemporal_load(reinterpret_cast<const vec*>(row));
+    } else {
+      vec v;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) v[c] = __builtin_nontemporal_load(row + cofs[c]);
+      return v;
+    }
+  };
   // Rows of X past M read row 0 instead: MFMA output row i depends only on
   // A row i, and those output rows are never stored.
   const float* xp[MB];
@@ -117,9 +136,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
     constexpr int U = sizeof(w) / sizeof(w[0]) / 4;
     const float* wp = wbase + (int64_t)k * ldw;
 #pragma unroll
-    for (int q = 0; q < 4 * U; ++q)
-      w[q] = __builtin_nontemporal_load(
-          reinterpret_cast<const vec*>(wp + (int64_t)(16 * (q / 4) + q % 4) * ldw));
+    for (int q = 0; q < 4 * U; ++q) w[q] = load_row(wp + (int64_t)(16 * (q / 4) + q % 4) * ldw);
   };
   auto load_x = [&](auto& x, int k) {
     constexpr int U = sizeof(x) / sizeof(x[0]);
@@ -169,8 +186,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
 #pragma unroll
       for (int q = 0; q < 4 * kU; ++q) {
         mfma_q(x[q / 4], q % 4, w[q]);
-        w[q] = __builtin_nontemporal_load(
-            reinterpret_cast<const vec*>(wp + (int64_t)(16 * (q / 4) + q % 4) * ldw));
+        w[q] = load_row(wp + (int64_t)(16 * (q / 4) + q % 4) * ldw);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
@@ -221,7 +237,14 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
     vec bv;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) bv[c] = 0.0f;
-    if (epi_has_bias(epi)) bv = *reinterpret_cast<const vec*>(a.bias + col);
+    if (epi_has_bias(epi)) {
+      if constexpr (WV) {
+        bv = *reinterpret_cast<const vec*>(a.bias + col);
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) bv[c] = col + c < a.N ? a.bias[col + c] : 0.0f;
+      }
+    }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -231,7 +254,14 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
           vec y;
 #pragma unroll
           for (int c = 0; c < CPL; ++c) y[c] = epilogue_rt(acc[mb][c][r], bv[c], a.alpha, epi);
-          *reinterpret_cast<vec*>(a.Y + (int64_t)row * a.ldy + col) = y;
+          float* dst = a.Y + (int64_t)row * a.ldy + col;
+          if constexpr (WV) {
+            *reinterpret_cast<vec*>(dst) = y;
+          } else {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c)
+              if (col + c < a.N) dst[c] = y[c];
+          }
         }
       }
     return;
@@ -246,7 +276,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
         vec p;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) p[c] = acc[mb][c][r];
-        *reinterpret_cast<vec*>(a.partials + ((int64_t)split * prow + row) * a.N + col) = p;
+        *reinterpret_cast<vec*>(a.partials + ((int64_t)split * prow + row) * a.ldp + col) = p;
       }
     }
 }
@@ -254,9 +284,13 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
 // Y[m, 4j..4j+3] = epilogue(sum over splits s = 0..ksplit-1, in order, plus
 // the K tail rows).
 // All split loads are issued before the first add so their latencies overlap.
+// WV as for gemv_f32_kernel: otherwise the bias, the tail rows of W and Y
+// are 4-byte accesses, columns past N neither read nor written. The partials
+// always have an aligned row pitch (ldp, a multiple of 4).
+template <bool WV>
 __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi, int prow) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over M * N/4
-  const int n4 = a.N / 4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over M * ceil(N/4)
+  const int n4 = (a.N + 3) / 4;
   if (idx >= (int64_t)a.M * n4) return;
   const int row = (int)(idx / n4);
   const int col = 4 * (int)(idx % n4);
@@ -265,9 +299,16 @@ __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi
   for (int sp = 0; sp < kMaxSplit; ++sp)
     if (sp < a.ksplit)
       v[sp] = __builtin_nontemporal_load(
-          reinterpret_cast<const f32x4*>(a.partials + ((int64_t)sp * prow + row) * a.N + col));
+          reinterpret_cast<const f32x4*>(a.partials + ((int64_t)sp * prow + row) * a.ldp + col));
   f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (epi_has_bias(epi)) bv = *reinterpret_cast<const f32x4*>(a.bias + col);
+  if (epi_has_bias(epi)) {
+    if constexpr (WV) {
+      bv = *reinterpret_cast<const f32x4*>(a.bias + col);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) bv[c] = col + c < a.N ? a.bias[col + c] : 0.0f;
+    }
+  }
   f32x4 s = v[0];
 #pragma unroll
   for (int sp = 1; sp < kMaxSplit; ++sp)
@@ -275,24 +316,38 @@ __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi
   // The last K % 16 rows, after the split sums, in ascending k.
   for (int k = a.K; k < a.k_end; ++k) {
     const float xv = a.x_tail[(int64_t)row * a.ldx_tail + k];
-    const f32x4 wv = *reinterpret_cast<const f32x4*>(a.W + (int64_t)k * a.ldw + col);
+    const float* wr = a.W + (int64_t)k * a.ldw + col;
+    f32x4 wv;
+    if constexpr (WV) {
+      wv = *reinterpret_cast<const f32x4*>(wr);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) wv[c] = col + c < a.N ? wr[c] : 0.0f;
+    }
     s += xv * wv;
   }
   f32x4 y;
 #pragma unroll
   for (int c = 0; c < 4; ++c) y[c] = epilogue_rt(s[c], bv[c], a.alpha, epi);
-  *reinterpret_cast<f32x4*>(a.Y + (int64_t)row * a.ldy + col) = y;
+  float* dst = a.Y + (int64_t)row * a.ldy + col;
+  if constexpr (WV) {
+    *reinterpret_cast<f32x4*>(dst) = y;
+  } else {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (col + c < a.N) dst[c] = y[c];
+  }
 }
 
-template <int MB, bool XV>
+template <int MB, bool XV, bool WV>
 hipError_t launch_mb_x(int cols, int epi, const GemvF32Args& a, hipStream_t stream) {
   const dim3 grid(((a.N + cols - 1) / cols) * a.ksplit);
   const dim3 block(kWavesPerWG * 64);
   switch (cols) {
-    case 32: hipLaunchKernelGGL((gemv_f32_kernel<MB, 2, 1, XV>), grid, block, 0, stream, a, epi); break;
-    case 64: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 1, XV>), grid, block, 0, stream, a, epi); break;
-    case 128: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 2, XV>), grid, block, 0, stream, a, epi); break;
-    case 256: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 4, XV>), grid, block, 0, stream, a, epi); break;
+    case 32: hipLaunchKernelGGL((gemv_f32_kernel<MB, 2, 1, XV, WV>), grid, block, 0, stream, a, epi); break;
+    case 64: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 1, XV, WV>), grid, block, 0, stream, a, epi); break;
+    case 128: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 2, XV, WV>), grid, block, 0, stream, a, epi); break;
+    case 256: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 4, XV, WV>), grid, block, 0, stream, a, epi); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -301,12 +356,20 @@ hipError_t launch_mb_x(int cols, int epi, const GemvF32Args& a, hipStream_t stre
 template <int MB>
 hipError_t launch_mb(int cols, int epi, const GemvF32Args& a, hipStream_t stream) {
   const bool xv = reinterpret_cast<uintptr_t>(a.X) % 16 == 0 && a.ldx % 4 == 0;
-  return xv ? launch_mb_x<MB, true>(cols, epi, a, stream) : launch_mb_x<MB, false>(cols, epi, a, stream);
+  const bool wv = gemv_f32_vector_rows(a);
+  if (wv) return xv ? launch_mb_x<MB, true, true>(cols, epi, a, stream) : launch_mb_x<MB, false, true>(cols, epi, a, stream);
+  return xv ? launch_mb_x<MB, true, false>(cols, epi, a, stream) : launch_mb_x<MB, false, false>(cols, epi, a, stream);
 }
 
 }  // namespace
 
 int gemv_f32_waves_k(int cols) { return cols <= 64 ? kWavesPerWG : kWavesPerWG / (cols / 64); }
+
+bool gemv_f32_vector_rows(const GemvF32Args& a) {
+  auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  return al16(a.W) && al16(a.Y) && (a.bias == nullptr || al16(a.bias)) && a.ldw % 4 == 0 && a.ldy % 4 == 0 &&
+         a.N % 4 == 0;
+}
 int gemv_f32_max_ksplit() { return kMaxSplit; }
 
 hipError_t launch_gemv_f32(int epi, int cols, GemvF32Args a, hipStream_t stream) {
@@ -320,9 +383,13 @@ hipError_t launch_gemv_f32(int epi, int cols, GemvF32Args a, hipStream_t stream)
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess || a.ksplit == 1) return e;
-  const int64_t items = (int64_t)a.M * (a.N / 4);
-  hipLaunchKernelGGL(gemv_reduce_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, stream, a,
-                     epi, 16 * mb);
+  const int64_t items = (int64_t)a.M * ((a.N + 3) / 4);
+  if (gemv_f32_vector_rows(a))
+    hipLaunchKernelGGL(gemv_reduce_kernel<true>, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, stream, a,
+                       epi, 16 * mb);
+  else
+    hipLaunchKernelGGL(gemv_reduce_kernel<false>, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, stream,
+                       a, epi, 16 * mb);
   return hipGetLastError();
 }
 

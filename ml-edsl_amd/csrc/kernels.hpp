@@ -48,7 +48,8 @@ struct GemvF32Args {
   int M, N, K;
   int ksplit;         // K slices reduced by a second kernel (1 = none)
   float alpha;
-  float* partials;    // [ksplit][16*ceil(M/16)][N] when ksplit > 1
+  float* partials;    // [ksplit][16*ceil(M/16)][ldp] when ksplit > 1
+  int64_t ldp;        // partials row pitch: N rounded up to a multiple of 4
   // K tail: rows K .. k_end-1 of W (k_end - K < 16), with X read from x_tail
   // (row stride ldx_tail), are added by the reduce kernel; k_end == K: none.
   const float* x_tail;
@@ -59,11 +60,14 @@ struct GemvF32Args {
 // A workgroup is 16 waves over `cols` adjacent columns (32, 64, 128 or 256),
 // the last block possibly partial; the waves not side by side split K, which
 // is walked in 16-row chunks. Requirements (checked by the caller):
-// 1 <= M <= 64, N % 4 == 0, K % 16 == 0, ksplit > 1 when there is a K tail,
-// 16-byte aligned W/Y/bias and row strides % 4 == 0 (X may have any
-// alignment and row stride: unaligned rows are read with 4-byte loads).
+// 1 <= M <= 64, K % 16 == 0, ksplit > 1 when there is a K tail. Operands may
+// have any alignment, row strides and N: X rows that are not 16-byte aligned
+// are read with 4-byte loads, and so are W (with the bias and Y) unless
+// gemv_f32_vector_rows holds.
 hipError_t launch_gemv_f32(int epi, int cols, GemvF32Args args, hipStream_t stream);
 int gemv_f32_waves_k(int cols);
+// W, Y and the bias 16-byte aligned with row strides and N multiples of 4.
+bool gemv_f32_vector_rows(const GemvF32Args& a);
 
 int gemv_f32_max_ksplit();
 constexpr int kGemvMaxM = 64;

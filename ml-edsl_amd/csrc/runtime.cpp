@@ -309,10 +309,10 @@ bool plan_gemv(const DeviceState& ds, int64_t N, int64_t K, int* cols_out, int* 
     if (g_force_cols > 0 && cols != g_force_cols) continue;
     const int64_t wk = gemv_f32_waves_k(cols);
     // The last column block may be partial (its lanes past N read the last
-    // columns and store nothing), which needs N % 4 == 0. K is walked in
-    // 16-row chunks spread evenly over the ks x wk wave slices; the automatic
-    // plan gives every slice at least two, a forced split at least one.
-    if (N % 4 != 0 || N < 4 || K % 16 != 0) continue;
+    // columns and store nothing). K is walked in 16-row chunks spread evenly
+    // over the ks x wk wave slices; the automatic plan gives every slice at
+    // least two, a forced split at least one.
+    if (N < 1 || K % 16 != 0) continue;
     const int64_t groups = (N + cols - 1) / cols;
     int ks = 1;
     if (g_force_ksplit > 0) {
@@ -344,13 +344,21 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   const int M = (int)L.M, N = (int)L.N, K = (int)L.K;
 
   // Small M: the streaming kernel walks the first K16 = K - K % 16 rows; the
-  // reduce kernel adds the rest. X rows need no alignment (unaligned ones are
-  // read with 4-byte loads); W, Y and the bias must be aligned in place.
+  // reduce kernel adds the rest. Operands need no alignment: X rows, and W
+  // with Y and the bias, that are not 16-byte aligned in place (or N not a
+  // multiple of 4) are read and written with 4-byte accesses.
   int gemv_cols = 0, gemv_ks = 0;
   const int K16 = K & ~15;
-  const bool w_ok = al16(L.w) && al16(L.y) && (!has_bias || al16(L.bias)) && L.ldw % 4 == 0 &&
-                    L.ldy % 4 == 0;
-  if (w_ok && M >= 1 && M <= kGemvMaxM && K16 > 0 && plan_gemv(ds, N, K16, &gemv_cols, &gemv_ks)) {
+  // With W, Y or the bias not vector-aligned (4-byte W loads) the small-M
+  // kernel streams at ~2 TB/s and beats the 32x32 any-shape tile only with
+  // at most three row blocks and a K split (16x8192x8191: 121 vs 134 us,
+  // 48x4096x4097: 64.5 vs 80.1 us; 64x8192x8191, whose four row blocks spill
+  // registers: 209 vs 167 us; 16x4096x50257 on one split: 459 vs 287 us).
+  // A forced split (edsl_hip_set_gemv_ksplit) takes the small-M kernel.
+  const bool w_vec = al16(L.w) && al16(L.y) && (!has_bias || al16(L.bias)) && L.ldw % 4 == 0 &&
+                     L.ldy % 4 == 0 && N % 4 == 0;
+  const bool gemv_planned = M >= 1 && M <= kGemvMaxM && K16 > 0 && plan_gemv(ds, N, K16, &gemv_cols, &gemv_ks);
+  if (gemv_planned && (w_vec || g_force_ksplit > 0 || (M <= 48 && gemv_ks > 1))) {
     const bool x_ok = al16(L.x) && L.ldx % 4 == 0;
     const bool tail = K16 < K;
     if (tail && gemv_ks == 1) gemv_ks = 2;  // the reduce kernel adds the tail
@@ -370,9 +378,11 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     a.ldx_tail = L.ldx;
     a.alpha = L.alpha;
     a.ksplit = gemv_ks;
+    a.ldp = ((int64_t)N + 3) & ~int64_t(3);
     const int mb = (M + 15) / 16;
     const bool scratch = a.ksplit > 1;
-    const size_t part_bytes = scratch ? (size_t)a.ksplit * 16 * mb * N * sizeof(float) : 0;
+    const size_t part_bytes = scratch ? (size_t)a.ksplit * 16 * mb * a.ldp * sizeof(float) : 0;
+    if (!has_bias) a.bias = nullptr;
     if (fixed) {
       // Caller-fixed scratch: nothing is allocated and no cross-stream
       // ordering is added.
@@ -386,9 +396,10 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     }
     check_hip(launch_gemv_f32(L.epi, gemv_cols, a, stream), "gemv_f32 launch");
     if (scratch && !fixed) scratch_end(ds, stream);
-    set_plan("gemv_f32 mb=%d ksplit=%d cols=%d grid=%d%s%s%s%s", mb, a.ksplit, gemv_cols,
+    set_plan("gemv_f32 mb=%d ksplit=%d cols=%d grid=%d%s%s%s%s%s", mb, a.ksplit, gemv_cols,
              ((N + gemv_cols - 1) / gemv_cols) * a.ksplit, a.ksplit > 1 ? " +reduce" : "",
-             x_ok ? "" : " +xunaligned", tail ? " +ktail" : "", fixed && scratch ? " +fixed-scratch" : "");
+             x_ok ? "" : " +xunaligned", gemv_f32_vector_rows(a) ? "" : " +wunaligned", tail ? " +ktail" : "",
+             fixed && scratch ? " +fixed-scratch" : "");
     return;
   }
 
@@ -429,7 +440,20 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
                                     {3, -1, -1}, {25, 30, 35}};
     int best = -1, first_rejected = -1;
     int64_t best_tiles = 0;
+    // Layers of at most 64 rows that the small-M kernel cannot take (W or Y
+    // rows unaligned, N not a multiple of 4) run on the 32x32 tiles: larger
+    // tiles spend most of their MFMAs on rows past M (16x4096x50257: 287 us
+    // on 32x32 against 364-1139 us on 64x64 to 256x256 tiles and 406 us on
+    // the element-checked 64x64 tile; the same order at 16, 48 and 64 rows).
+    if (M <= kGemvMaxM) {
+      for (int c : {25, 30, 35})
+        if (fits(c)) {
+          cfg = c;
+          break;
+        }
+    }
     for (const auto& e : kOrder) {
+      if (cfg >= 0) break;
       int c = -1;
       for (int t = 0; t < 3 && c < 0; ++t)
         if (e[t] >= 0 && fits(e[t])) c = e[t];

@@ -160,6 +160,32 @@ def test_small_m_uneven_k_slices(M, K, N, torch_cuda):
     assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
 
 
+# Small M with W, Y and bias rows that are not 16-byte aligned or N not a
+# multiple of 4: 4-byte accesses, columns past N clamped on read and not
+# stored; odd K adds the tail through the reduce kernel. One to four row
+# blocks, each column width the plan picks, contiguous and misaligned views.
+@pytest.mark.parametrize("M, K, N", [(16, 8192, 8191), (16, 4096, 5003), (5, 1003, 1029), (64, 2048, 1023),
+                                     (33, 512, 7), (1, 512, 3), (48, 4096, 4097)])
+def test_small_m_unaligned_w(M, K, N, torch_cuda):
+    """The automatic plan (the small-M kernel or the 32x32 any-shape tile,
+    whichever measured faster for the shape), then the small-M kernel itself
+    under a forced split of 2."""
+    from mlir_edsl_hip.device import set_gemv_ksplit
+    X, W, b = _inputs(M, K, N, M * 7 + K + N)
+    ref = oracle.dense_f32(X, W, b, "relu")
+    for pad, off in ((0, 0), (3, 1)):
+        got, plan = _run(torch_cuda, X, W, b, pad, off)
+        assert "+wunaligned" in plan or "32x32x64" in plan, plan
+        assert_f32_parity(got, ref, K)
+        try:
+            set_gemv_ksplit(2)
+            got, plan = _run(torch_cuda, X, W, b, pad, off)
+        finally:
+            set_gemv_ksplit(0)
+        assert plan.startswith("gemv_f32") and "+wunaligned" in plan and "ksplit=2" in plan, plan
+        assert_f32_parity(got, ref, K)
+
+
 def test_small_m_forced_splits_on_uneven_k(torch_cuda):
     from mlir_edsl_hip.device import set_gemv_cols, set_gemv_ksplit
     M, K, N = 16, 8000, 1024
