@@ -59,11 +59,19 @@ __device__ __forceinline__ float epilogue_rt(float acc, float b, float alpha, in
 // XV: X rows are 16-byte aligned (row stride % 4 == 0) and are read with one
 // 16-byte load per row block and step; otherwise with four 4-byte loads
 // (X is small and read from the caches, so this costs little against W).
-// WV: W, Y and the bias are 16-byte aligned, their row strides and N
-// multiples of 4: a lane's CPL columns are one vector load or store, all in
-// or all out of range. Otherwise every column is a 4-byte access; columns
-// past N read column N - 1 and are not stored.
-template <int MB, int CPL, int WN, bool XV, bool WV>
+// WM (GemvF32Args::w_mode): kWVector -- W, Y and the bias are 16-byte
+// aligned, their row strides and N multiples of 4: a lane's CPL columns are
+// one vector load or store, all in or all out of range. Otherwise Y and the
+// bias are 4-byte accesses and columns past N are not stored; W is read
+// either with a 4-byte load per column (kWScalar; columns past N read column
+// N - 1) or, for CPL = 4, realigned (kWRealign): the lane's 4 columns lie in
+// two neighbouring 16-byte chunks of the row, both loaded whole, and a select
+// by the row's offset within its chunk (the same for all of a lane group's
+// lanes) picks them. Each chunk holds an element the lane owns or, for the
+// lane that straddles N, one of the next row's first elements, so no load
+// leaves the matrix's pages; the caller leaves the last row of W to the K
+// tail. Lanes wholly past N read columns 0..3.
+template <int MB, int CPL, int WN, bool XV, int WM>
 __global__ void __launch_bounds__(kWavesPerWG * 64)
 gemv_f32_kernel(GemvF32Args a, int epi) {
   using vec = typename std::conditional<CPL == 4, f32x4, f32x2>::type;
@@ -105,14 +113,27 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
   // the last CPL columns instead; their results are never stored. N % 4 ==
   // 0, so a lane's CPL columns are all in or all out. Otherwise wbase is the
   // row start and cofs the lane's columns, each clamped to N - 1.
+  static_assert(WM != kWRealign || CPL == 4, "realigned W rows need 4 columns per lane");
   const int col_lane = n0 + CPL * li;
-  const float* wbase = a.W + (int64_t)(kbeg + 4 * lg) * ldw + (WV ? min(col_lane, a.N - CPL) : 0);
+  const int col_w = WM == kWVector ? min(col_lane, a.N - CPL) : WM == kWRealign ? (col_lane < a.N ? col_lane : 0) : 0;
+  const float* wbase = a.W + (int64_t)(kbeg + 4 * lg) * ldw + col_w;
   int cofs[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) cofs[c] = min(col_lane + c, a.N - 1);
   auto load_row = [&](const float* row) {
-    if constexpr (WV) {
+    if constexpr (WM == kWVector) {
       return __builtin_nontemporal_load(reinterpret_cast<const vec*>(row));
+    } else if constexpr (WM == kWRealign) {
+      const int d = (int)((reinterpret_cast<uintptr_t>(row) >> 2) & 3);
+      const f32x4* p0 = reinterpret_cast<const f32x4*>(row - d);
+      const f32x4 c0 = __builtin_nontemporal_load(p0);
+      const f32x4 c1 = __builtin_nontemporal_load(d != 0 ? p0 + 1 : p0);
+      vec v;
+      v[0] = d == 0 ? c0[0] : d == 1 ? c0[1] : d == 2 ? c0[2] : c0[3];
+      v[1] = d == 0 ? c0[1] : d == 1 ? c0[2] : d == 2 ? c0[3] : c1[0];
+      v[2] = d == 0 ? c0[2] : d == 1 ? c0[3] : d == 2 ? c1[0] : c1[1];
+      v[3] = d == 0 ? c0[3] : d == 1 ? c1[0] : d == 2 ? c1[1] : c1[2];
+      return v;
     } else {
       vec v;
 #pragma unroll
@@ -238,7 +259,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) bv[c] = 0.0f;
     if (epi_has_bias(epi)) {
-      if constexpr (WV) {
+      if constexpr (WM == kWVector) {
         bv = *reinterpret_cast<const vec*>(a.bias + col);
       } else {
 #pragma unroll
@@ -255,7 +276,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
 #pragma unroll
           for (int c = 0; c < CPL; ++c) y[c] = epilogue_rt(acc[mb][c][r], bv[c], a.alpha, epi);
           float* dst = a.Y + (int64_t)row * a.ldy + col;
-          if constexpr (WV) {
+          if constexpr (WM == kWVector) {
             *reinterpret_cast<vec*>(dst) = y;
           } else {
 #pragma unroll
@@ -339,31 +360,46 @@ __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi
   }
 }
 
-template <int MB, bool XV, bool WV>
+template <int MB, bool XV, int WM>
 hipError_t launch_mb_x(int cols, int epi, const GemvF32Args& a, hipStream_t stream) {
   const dim3 grid(((a.N + cols - 1) / cols) * a.ksplit);
   const dim3 block(kWavesPerWG * 64);
+  // Two columns per lane take 4-byte W loads where four would be realigned.
+  constexpr int WM2 = WM == kWRealign ? kWScalar : WM;
   switch (cols) {
-    case 32: hipLaunchKernelGGL((gemv_f32_kernel<MB, 2, 1, XV, WV>), grid, block, 0, stream, a, epi); break;
-    case 64: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 1, XV, WV>), grid, block, 0, stream, a, epi); break;
-    case 128: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 2, XV, WV>), grid, block, 0, stream, a, epi); break;
-    case 256: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 4, XV, WV>), grid, block, 0, stream, a, epi); break;
+    case 32: hipLaunchKernelGGL((gemv_f32_kernel<MB, 2, 1, XV, WM2>), grid, block, 0, stream, a, epi); break;
+    case 64: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 1, XV, WM>), grid, block, 0, stream, a, epi); break;
+    case 128: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 2, XV, WM>), grid, block, 0, stream, a, epi); break;
+    case 256: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 4, XV, WM>), grid, block, 0, stream, a, epi); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
+template <int MB, int WM>
+hipError_t launch_mb_w(int cols, int epi, const GemvF32Args& a, hipStream_t stream) {
+  const bool xv = reinterpret_cast<uintptr_t>(a.X) % 16 == 0 && a.ldx % 4 == 0;
+  return xv ? launch_mb_x<MB, true, WM>(cols, epi, a, stream) : launch_mb_x<MB, false, WM>(cols, epi, a, stream);
+}
+
 template <int MB>
 hipError_t launch_mb(int cols, int epi, const GemvF32Args& a, hipStream_t stream) {
-  const bool xv = reinterpret_cast<uintptr_t>(a.X) % 16 == 0 && a.ldx % 4 == 0;
-  const bool wv = gemv_f32_vector_rows(a);
-  if (wv) return xv ? launch_mb_x<MB, true, true>(cols, epi, a, stream) : launch_mb_x<MB, false, true>(cols, epi, a, stream);
-  return xv ? launch_mb_x<MB, true, false>(cols, epi, a, stream) : launch_mb_x<MB, false, false>(cols, epi, a, stream);
+  switch (a.w_mode) {
+    case kWVector: return launch_mb_w<MB, kWVector>(cols, epi, a, stream);
+    case kWScalar: return launch_mb_w<MB, kWScalar>(cols, epi, a, stream);
+    case kWRealign: return launch_mb_w<MB, kWRealign>(cols, epi, a, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace
 
 int gemv_f32_waves_k(int cols) { return cols <= 64 ? kWavesPerWG : kWavesPerWG / (cols / 64); }
+
+int gemv_f32_w_mode(const GemvF32Args& a) {
+  if (gemv_f32_vector_rows(a)) return kWVector;
+  return a.N >= 4 ? kWRealign : kWScalar;
+}
 
 bool gemv_f32_vector_rows(const GemvF32Args& a) {
   auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
@@ -384,7 +420,7 @@ hipError_t launch_gemv_f32(int epi, int cols, GemvF32Args a, hipStream_t stream)
   }
   if (e != hipSuccess || a.ksplit == 1) return e;
   const int64_t items = (int64_t)a.M * ((a.N + 3) / 4);
-  if (gemv_f32_vector_rows(a))
+  if (a.w_mode == kWVector)
     hipLaunchKernelGGL(gemv_reduce_kernel<true>, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, stream, a,
                        epi, 16 * mb);
   else

@@ -50,24 +50,34 @@ struct GemvF32Args {
   float alpha;
   float* partials;    // [ksplit][16*ceil(M/16)][ldp] when ksplit > 1
   int64_t ldp;        // partials row pitch: N rounded up to a multiple of 4
-  // K tail: rows K .. k_end-1 of W (k_end - K < 16), with X read from x_tail
+  // K tail: rows K .. k_end-1 of W (k_end - K <= 16), with X read from x_tail
   // (row stride ldx_tail), are added by the reduce kernel; k_end == K: none.
   const float* x_tail;
   int64_t ldx_tail;
   int k_end;
+  int w_mode;         // kWVector, kWScalar or kWRealign (gemv_f32_w_mode)
 };
+
+// How the small-M kernel reads W: one vector per lane and row (W, Y and the
+// bias 16-byte aligned, row strides and N multiples of 4), a 4-byte load per
+// column, or two aligned 16-byte chunks realigned in registers (N >= 4; the
+// caller must leave the last row of W to the K tail).
+enum : int { kWVector = 0, kWScalar = 1, kWRealign = 2 };
 
 // A workgroup is 16 waves over `cols` adjacent columns (32, 64, 128 or 256),
 // the last block possibly partial; the waves not side by side split K, which
 // is walked in 16-row chunks. Requirements (checked by the caller):
-// 1 <= M <= 64, K % 16 == 0, ksplit > 1 when there is a K tail. Operands may
-// have any alignment, row strides and N: X rows that are not 16-byte aligned
-// are read with 4-byte loads, and so are W (with the bias and Y) unless
-// gemv_f32_vector_rows holds.
+// 1 <= M <= 64, K % 16 == 0, ksplit > 1 when there is a K tail, w_mode set
+// (kWRealign: K < the rows of W). Operands may have any alignment, row
+// strides and N: X rows that are not 16-byte aligned are read with 4-byte
+// loads; W, the bias and Y as w_mode says.
 hipError_t launch_gemv_f32(int epi, int cols, GemvF32Args args, hipStream_t stream);
 int gemv_f32_waves_k(int cols);
 // W, Y and the bias 16-byte aligned with row strides and N multiples of 4.
 bool gemv_f32_vector_rows(const GemvF32Args& a);
+// The W mode for these operands: kWVector when gemv_f32_vector_rows holds,
+// else kWRealign when N >= 4, else kWScalar.
+int gemv_f32_w_mode(const GemvF32Args& a);
 
 int gemv_f32_max_ksplit();
 constexpr int kGemvMaxM = 64;

@@ -10,8 +10,8 @@
 //  * host or device operands (host operands staged through grow-only device
 //    buffers that persist across calls instead of per-call alloc/free),
 //  * one fused kernel per dense layer (two for the int8 path: narrow + GEMM),
-//  * kernel selection by shape: small-M weight streaming, tiled MFMA, or the
-//    bounds-checked tile for odd shapes / alignments.
+//  * kernel selection by shape: small-M weight streaming or tiled MFMA, each
+//    with variants for operands of any alignment, row stride and size.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -344,21 +344,28 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   const int M = (int)L.M, N = (int)L.N, K = (int)L.K;
 
   // Small M: the streaming kernel walks the first K16 = K - K % 16 rows; the
-  // reduce kernel adds the rest. Operands need no alignment: X rows, and W
-  // with Y and the bias, that are not 16-byte aligned in place (or N not a
-  // multiple of 4) are read and written with 4-byte accesses.
+  // reduce kernel adds the rest. Operands need no alignment: X rows that are
+  // not 16-byte aligned are read with 4-byte loads; W rows that are not (or N
+  // not a multiple of 4) are realigned from 16-byte chunks or read per column,
+  // with Y and the bias written and read per element.
   int gemv_cols = 0, gemv_ks = 0;
-  const int K16 = K & ~15;
-  // With W, Y or the bias not vector-aligned (4-byte W loads) the small-M
-  // kernel streams at ~2 TB/s and beats the 32x32 any-shape tile only with
-  // at most three row blocks and a K split (16x8192x8191: 121 vs 134 us,
-  // 48x4096x4097: 64.5 vs 80.1 us; 64x8192x8191, whose four row blocks spill
-  // registers: 209 vs 167 us; 16x4096x50257 on one split: 459 vs 287 us).
-  // A forced split (edsl_hip_set_gemv_ksplit) takes the small-M kernel.
   const bool w_vec = al16(L.w) && al16(L.y) && (!has_bias || al16(L.bias)) && L.ldw % 4 == 0 &&
                      L.ldy % 4 == 0 && N % 4 == 0;
+  // Realigned W rows (two aligned 16-byte chunks per lane and row) leave the
+  // last row of W to the reduce kernel's K tail.
+  const bool w_realign = !w_vec && N >= 4;
+  const int K16 = w_realign ? ((K - 1) & ~15) : (K & ~15);
+  // With W, Y or the bias not vector-aligned the small-M kernel streams W at
+  // ~3 TB/s realigned (~2 TB/s with 4-byte loads, N < 4 or 32-column blocks)
+  // and beats the 32x32 any-shape tile when its plan splits K (16x8192x8191:
+  // 85.8 vs 134 us, 32x8192x8191: 99.5 us, 64x8192x8191: 145 vs 172 us); with
+  // enough column blocks to fill the chip on one split the tile's wider grid
+  // wins (16x4096x50257: 288 vs 315 us). 4-byte loads: at most three row
+  // blocks (four spill registers). A forced split (edsl_hip_set_gemv_ksplit)
+  // takes the small-M kernel.
   const bool gemv_planned = M >= 1 && M <= kGemvMaxM && K16 > 0 && plan_gemv(ds, N, K16, &gemv_cols, &gemv_ks);
-  if (gemv_planned && (w_vec || g_force_ksplit > 0 || (M <= 48 && gemv_ks > 1))) {
+  if (gemv_planned &&
+      (w_vec || g_force_ksplit > 0 || (gemv_ks > 1 && ((w_realign && gemv_cols > 32) || M <= 48)))) {
     const bool x_ok = al16(L.x) && L.ldx % 4 == 0;
     const bool tail = K16 < K;
     if (tail && gemv_ks == 1) gemv_ks = 2;  // the reduce kernel adds the tail
@@ -383,6 +390,9 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     const bool scratch = a.ksplit > 1;
     const size_t part_bytes = scratch ? (size_t)a.ksplit * 16 * mb * a.ldp * sizeof(float) : 0;
     if (!has_bias) a.bias = nullptr;
+    // Two columns per lane (32-column blocks) read unaligned rows per column.
+    a.w_mode = w_vec ? kWVector : (w_realign && gemv_cols > 32 ? kWRealign : kWScalar);
+    if (gemv_f32_w_mode(a) == kWVector && a.w_mode != kWVector) fail(kErrInternal, "small-M W mode mismatch");
     if (fixed) {
       // Caller-fixed scratch: nothing is allocated and no cross-stream
       // ordering is added.
@@ -398,7 +408,8 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     if (scratch && !fixed) scratch_end(ds, stream);
     set_plan("gemv_f32 mb=%d ksplit=%d cols=%d grid=%d%s%s%s%s%s", mb, a.ksplit, gemv_cols,
              ((N + gemv_cols - 1) / gemv_cols) * a.ksplit, a.ksplit > 1 ? " +reduce" : "",
-             x_ok ? "" : " +xunaligned", gemv_f32_vector_rows(a) ? "" : " +wunaligned", tail ? " +ktail" : "",
+             x_ok ? "" : " +xunaligned",
+             a.w_mode == kWVector ? "" : a.w_mode == kWRealign ? " +wrealigned" : " +wunaligned", tail ? " +ktail" : "",
              fixed && scratch ? " +fixed-scratch" : "");
     return;
   }
