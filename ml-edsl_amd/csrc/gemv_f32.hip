@@ -42,6 +42,8 @@
 namespace edsl {
 namespace {
 
+typedef float f32x3 __attribute__((ext_vector_type(3)));
+
 constexpr int kWavesPerWG = 16;
 constexpr int kMaxSplit = 16;
 
@@ -65,12 +67,9 @@ __device__ __forceinline__ float epilogue_rt(float acc, float b, float alpha, in
 // bias are 4-byte accesses and columns past N are not stored; W is read
 // either with a 4-byte load per column (kWScalar; columns past N read column
 // N - 1) or, for CPL = 4, realigned (kWRealign): the lane's 4 columns lie in
-// two neighbouring 16-byte chunks of the row, both loaded whole, and a select
-// by the row's offset within its chunk (the same for all of a lane group's
-// lanes) picks them. Each chunk holds an element the lane owns or, for the
-// lane that straddles N, one of the next row's first elements, so no load
-// leaves the matrix's pages; the caller leaves the last row of W to the K
-// tail. Lanes wholly past N read columns 0..3.
+// two neighbouring 16-byte chunks of the row, loaded whole (the second mostly
+// by the neighbouring lane), and a select by the row's offset within its
+// chunk picks them; the caller leaves the last row of W to the K tail.
 template <int MB, int CPL, int WN, bool XV, int WM>
 __global__ void __launch_bounds__(kWavesPerWG * 64)
 gemv_f32_kernel(GemvF32Args a, int epi) {
@@ -109,22 +108,77 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
     for (int c = 0; c < CPL; ++c) acc[mb][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int64_t ldw = a.ldw;
-  // WV: lanes whose columns lie past N (a partial last column block) read
-  // the last CPL columns instead; their results are never stored. N % 4 ==
-  // 0, so a lane's CPL columns are all in or all out. Otherwise wbase is the
-  // row start and cofs the lane's columns, each clamped to N - 1.
+  // kWVector: lanes whose columns lie past N (a partial last column block)
+  // read the last CPL columns instead; their results are never stored. N % 4
+  // == 0, so a lane's CPL columns are all in or all out. kWScalar: wbase is
+  // the row start and cofs the lane's columns, each clamped to N - 1.
   static_assert(WM != kWRealign || CPL == 4, "realigned W rows need 4 columns per lane");
+  // Realigned rows: every lane's column offset and every step's row offset
+  // within the wave's slice are multiples of 4, so the offset of a row within
+  // its 16-byte chunk depends only on the row's slot s = q % 4 in the step:
+  // dsh[s], the same for every lane and step.
+  //
+  // With up to three row blocks (kDefer) a lane loads one chunk per row, the
+  // one holding its first column. The next chunk, which holds the rest, is
+  // its right neighbour's, taken with a row shift (lanes 16g .. 16g+15 share
+  // a row); only lane 16g+15 has no neighbour and loads it as well (the other
+  // lanes masked off; 12 bytes, the most it needs). Both are kept until just
+  // before the MFMAs that read them, so a wave's loads stay in flight. Lanes
+  // wholly past N read the chunk at r4 = N rounded up to 4, the one after the
+  // last lane that holds a column below N, so that its neighbour finds the
+  // right chunk there. Every chunk loaded holds a column below N of its row or
+  // one of the next row's first elements (the caller leaves the last row of W
+  // to the K tail), so no load leaves the matrix's pages. With four row blocks
+  // the registers hold the accumulators instead: each lane loads both chunks
+  // and selects at once, and lanes past N read columns 0..3.
+  constexpr bool kDefer = WM == kWRealign && MB <= 3;
   const int col_lane = n0 + CPL * li;
-  const int col_w = WM == kWVector ? min(col_lane, a.N - CPL) : WM == kWRealign ? (col_lane < a.N ? col_lane : 0) : 0;
+  const int r4 = (a.N + 3) & ~3;
+  const int col_w = WM == kWVector ? min(col_lane, a.N - CPL)
+                    : kDefer       ? min(col_lane, r4)
+                    : WM == kWRealign ? (col_lane < a.N ? col_lane : 0)
+                                      : 0;
   const float* wbase = a.W + (int64_t)(kbeg + 4 * lg) * ldw + col_w;
   int cofs[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) cofs[c] = min(col_lane + c, a.N - 1);
-  auto load_row = [&](const float* row) {
+  int dsh[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    dsh[s] = (int)(((reinterpret_cast<uintptr_t>(a.W) >> 2) + (uint64_t)s * (uint64_t)ldw) & 3);
+  // Lane 16g+15 loads its second chunk when it holds a column below N.
+  const bool own_next = li == 15 && col_lane < a.N;
+  // Elements d .. d+3 (d = dsh[s]) of the lane's chunk c0 and the next one.
+  // The row shift runs on every lane (a lane masked off would read as
+  // invalid to its neighbour); the selects follow.
+  auto realign = [&](const f32x4& c0, const f32x3& own, int s) {
+    auto shl1 = [](float v) {  // lane i <- lane i + 1 of its row of 16
+      return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x101, 0xf, 0xf, false));
+    };
+    const f32x3 next{shl1(c0[0]), shl1(c0[1]), shl1(c0[2])};
+    const f32x3 c1 = li == 15 ? own : next;
+    const bool b0 = dsh[s] & 1, b1 = dsh[s] & 2;
+    const float t0 = b0 ? c0[1] : c0[0], t1 = b0 ? c0[2] : c0[1], t2 = b0 ? c0[3] : c0[2];
+    const float t3 = b0 ? c1[0] : c0[3], t4 = b0 ? c1[1] : c1[0], t5 = b0 ? c1[2] : c1[1];
+    return f32x4{b1 ? t2 : t0, b1 ? t3 : t1, b1 ? t4 : t2, b1 ? t5 : t3};
+  };
+  // The second chunk is loaded as 12 bytes, so no register of an outstanding
+  // load is dead (a dead one is reused as a temporary, and the wave then
+  // waits for the load before the temporary is written).
+  struct Chunks { f32x4 c0; f32x3 c1; };
+  using wreg = typename std::conditional<kDefer, Chunks, vec>::type;
+  auto load_row = [&](const float* row, int s) {
     if constexpr (WM == kWVector) {
       return __builtin_nontemporal_load(reinterpret_cast<const vec*>(row));
+    } else if constexpr (kDefer) {
+      const f32x4* p0 = reinterpret_cast<const f32x4*>(row - dsh[s]);
+      Chunks r;
+      r.c0 = __builtin_nontemporal_load(p0);
+      r.c1 = f32x3{0.0f, 0.0f, 0.0f};
+      if (own_next && dsh[s] != 0) r.c1 = __builtin_nontemporal_load(reinterpret_cast<const f32x3*>(p0 + 1));
+      return r;
     } else if constexpr (WM == kWRealign) {
-      const int d = (int)((reinterpret_cast<uintptr_t>(row) >> 2) & 3);
+      const int d = dsh[s];
       const f32x4* p0 = reinterpret_cast<const f32x4*>(row - d);
       const f32x4 c0 = __builtin_nontemporal_load(p0);
       const f32x4 c1 = __builtin_nontemporal_load(d != 0 ? p0 + 1 : p0);
@@ -157,7 +211,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
     constexpr int U = sizeof(w) / sizeof(w[0]) / 4;
     const float* wp = wbase + (int64_t)k * ldw;
 #pragma unroll
-    for (int q = 0; q < 4 * U; ++q) w[q] = load_row(wp + (int64_t)(16 * (q / 4) + q % 4) * ldw);
+    for (int q = 0; q < 4 * U; ++q) w[q] = load_row(wp + (int64_t)(16 * (q / 4) + q % 4) * ldw, q % 4);
   };
   auto load_x = [&](auto& x, int k) {
     constexpr int U = sizeof(x) / sizeof(x[0]);
@@ -172,7 +226,12 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
           x[u][mb] = f32x4{p[0], p[1], p[2], p[3]};
       }
   };
-  auto mfma_q = [&](const f32x4 (&xu)[MB], int s, const vec& wq) {
+  auto mfma_q = [&](const f32x4 (&xu)[MB], int s, const wreg& wr) {
+    vec wq;
+    if constexpr (kDefer)
+      wq = realign(wr.c0, wr.c1, s);
+    else
+      wq = wr;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -193,7 +252,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
   const int nit = kwave / (16 * kU);
   const int r0 = nit > 0 ? (int)(((unsigned)blockIdx.x * 2654435761u >> 8) + (unsigned)wave * 977u) % nit : 0;
   if (nit > 0) {
-    vec w[4 * kU];
+    wreg w[4 * kU];
     f32x4 x[kU][MB], xn[kU][MB];
     int it = r0;
     load_x(x, it * 16 * kU);
@@ -207,7 +266,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
 #pragma unroll
       for (int q = 0; q < 4 * kU; ++q) {
         mfma_q(x[q / 4], q % 4, w[q]);
-        w[q] = load_row(wp + (int64_t)(16 * (q / 4) + q % 4) * ldw);
+        w[q] = load_row(wp + (int64_t)(16 * (q / 4) + q % 4) * ldw, q % 4);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
@@ -221,7 +280,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
   }
   // Remaining single steps (kwave not a multiple of 16*kU).
   for (int k = nit * 16 * kU; k < kwave; k += 16) {
-    vec w[4];
+    wreg w[4];
     f32x4 x[1][MB];
     load_x(x, k);
     load_w(w, k);

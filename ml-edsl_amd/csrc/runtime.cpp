@@ -355,17 +355,23 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   // last row of W to the reduce kernel's K tail.
   const bool w_realign = !w_vec && N >= 4;
   const int K16 = w_realign ? ((K - 1) & ~15) : (K & ~15);
-  // With W, Y or the bias not vector-aligned the small-M kernel streams W at
-  // ~3 TB/s realigned (~2 TB/s with 4-byte loads, N < 4 or 32-column blocks)
-  // and beats the 32x32 any-shape tile when its plan splits K (16x8192x8191:
-  // 85.8 vs 134 us, 32x8192x8191: 99.5 us, 64x8192x8191: 145 vs 172 us); with
-  // enough column blocks to fill the chip on one split the tile's wider grid
-  // wins (16x4096x50257: 288 vs 315 us). 4-byte loads: at most three row
-  // blocks (four spill registers). A forced split (edsl_hip_set_gemv_ksplit)
-  // takes the small-M kernel.
+  // With W, Y or the bias not vector-aligned the small-M kernel streams W
+  // realigned at ~3.2-3.9 TB/s with one row block, ~2.6 with two and ~2.2
+  // with three (~2 TB/s with 4-byte loads: N < 4 or 32-column blocks). The
+  // 32x32 any-shape tile reads W once per 32 rows of M at ~2.8 TB/s. So the
+  // small-M kernel is taken realigned whenever its plan splits K
+  // (16x8192x8191: 70 vs 134 us, 48x8192x8191: 96 vs 170, 64x8192x8191: 147
+  // vs 172) and, on one split, for one or three row blocks (16x4096x50257:
+  // 257 vs 290 us, 48x4096x50257: 390 vs 495) but not two or four
+  // (32x4096x50257: 322 vs 296 us, 64x4096x50257: 531 vs 507); with 4-byte
+  // loads when the plan splits K and M <= 48 (four row blocks spill). A
+  // forced split (edsl_hip_set_gemv_ksplit) takes the small-M kernel.
   const bool gemv_planned = M >= 1 && M <= kGemvMaxM && K16 > 0 && plan_gemv(ds, N, K16, &gemv_cols, &gemv_ks);
+  const bool realigned_plan = w_realign && gemv_cols > 32;
+  const int row_blocks = (M + 15) / 16;
   if (gemv_planned &&
-      (w_vec || g_force_ksplit > 0 || (gemv_ks > 1 && ((w_realign && gemv_cols > 32) || M <= 48)))) {
+      (w_vec || g_force_ksplit > 0 || (realigned_plan && (gemv_ks > 1 || row_blocks == 1 || row_blocks == 3)) ||
+       (gemv_ks > 1 && M <= 48))) {
     const bool x_ok = al16(L.x) && L.ldx % 4 == 0;
     const bool tail = K16 < K;
     if (tail && gemv_ks == 1) gemv_ks = 2;  // the reduce kernel adds the tail
@@ -391,7 +397,7 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     const size_t part_bytes = scratch ? (size_t)a.ksplit * 16 * mb * a.ldp * sizeof(float) : 0;
     if (!has_bias) a.bias = nullptr;
     // Two columns per lane (32-column blocks) read unaligned rows per column.
-    a.w_mode = w_vec ? kWVector : (w_realign && gemv_cols > 32 ? kWRealign : kWScalar);
+    a.w_mode = w_vec ? kWVector : (realigned_plan ? kWRealign : kWScalar);
     if (gemv_f32_w_mode(a) == kWVector && a.w_mode != kWVector) fail(kErrInternal, "small-M W mode mismatch");
     if (fixed) {
       // Caller-fixed scratch: nothing is allocated and no cross-stream

@@ -190,6 +190,42 @@ def test_small_m_unaligned_w(M, K, N, torch_cuda):
         assert_f32_parity(got, ref, K)
 
 
+# Realigned W rows at every offset of a row within its 16-byte chunk: row
+# pitches N + pad and element offsets chosen so that the offset of row k
+# cycles with k when the pitch is odd; N such that the last lane of a lane
+# group (the one that loads its own second chunk) holds a column below N,
+# straddles N or lies past it, on every column width; one to three row blocks
+# (second chunk from the neighbouring lane) and four (both chunks loaded by
+# every lane). K = 1029: the last rows, the last one always, go to the tail.
+@pytest.mark.parametrize("cols", [64, 128, 256])
+@pytest.mark.parametrize("M", [1, 17, 40, 64])
+def test_realigned_w_rows(M, cols, torch_cuda):
+    from mlir_edsl_hip.device import set_gemv_cols, set_gemv_ksplit
+    K = 1029
+    checked = 0
+    for N in (5, 61, 62, 63, 64 + 58, 64 + 60, 128 + 1, 128 + 63, 256 + 2, 256 + 62, 511):
+        X, W, b = _inputs(M, K, N, M * 1000 + N)
+        ref = oracle.dense_f32(X, W, b, "relu")
+        for pad, off in ((0, 0), (1, 0), (2, 1), (3, 3), (0, 2)):
+            try:
+                set_gemv_cols(cols)
+                set_gemv_ksplit(2)
+                got, plan = _run(torch_cuda, X, W, b, pad, off)
+            finally:
+                set_gemv_ksplit(0)
+                set_gemv_cols(0)
+            what = f"M={M} K={K} N={N} pad={pad} off={off} [{plan}]"
+            vector_rows = N % 4 == 0 and pad % 4 == 0 and off % 4 == 0
+            assert plan.startswith("gemv_f32") and f"cols={cols} " in plan, what
+            assert ("+wrealigned" in plan) != vector_rows, what
+            try:
+                assert_f32_parity(got, ref, K)
+            except AssertionError as e:
+                raise AssertionError(f"{what}: {e}") from None
+            checked += 1
+    assert checked == 55
+
+
 def test_small_m_forced_splits_on_uneven_k(torch_cuda):
     from mlir_edsl_hip.device import set_gemv_cols, set_gemv_ksplit
     M, K, N = 16, 8000, 1024
