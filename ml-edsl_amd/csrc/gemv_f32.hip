@@ -46,6 +46,7 @@ typedef float f32x3 __attribute__((ext_vector_type(3)));
 
 constexpr int kWavesPerWG = 16;
 constexpr int kMaxSplit = 16;
+constexpr int kMaxTail = 16;  // rows of the K tail (GemvF32Args::k_end - K)
 
 __device__ __forceinline__ float epilogue_rt(float acc, float b, float alpha, int epi) {
   switch (epi) {
@@ -393,18 +394,27 @@ __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi
 #pragma unroll
   for (int sp = 1; sp < kMaxSplit; ++sp)
     if (sp < a.ksplit) s += v[sp];
-  // The last K % 16 rows, after the split sums, in ascending k.
-  for (int k = a.K; k < a.k_end; ++k) {
-    const float xv = a.x_tail[(int64_t)row * a.ldx_tail + k];
-    const float* wr = a.W + (int64_t)k * a.ldw + col;
-    f32x4 wv;
-    if constexpr (WV) {
-      wv = *reinterpret_cast<const f32x4*>(wr);
-    } else {
+  // The K tail (at most 16 rows), after the split sums, in ascending k. All
+  // its loads are issued before the first add (rows past k_end read row
+  // k_end - 1 and are not added), so their latencies overlap.
+  if (a.k_end > a.K) {
+    float xt[kMaxTail];
+    f32x4 wt[kMaxTail];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) wv[c] = col + c < a.N ? wr[c] : 0.0f;
+    for (int t = 0; t < kMaxTail; ++t) {
+      const int k = min(a.K + t, a.k_end - 1);
+      xt[t] = a.x_tail[(int64_t)row * a.ldx_tail + k];
+      const float* wr = a.W + (int64_t)k * a.ldw + col;
+      if constexpr (WV) {
+        wt[t] = *reinterpret_cast<const f32x4*>(wr);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) wt[t][c] = col + c < a.N ? wr[c] : 0.0f;
+      }
     }
-    s += xv * wv;
+#pragma unroll
+    for (int t = 0; t < kMaxTail; ++t)
+      if (a.K + t < a.k_end) s += xt[t] * wt[t];
   }
   f32x4 y;
 #pragma unroll
@@ -469,6 +479,7 @@ int gemv_f32_max_ksplit() { return kMaxSplit; }
 
 hipError_t launch_gemv_f32(int epi, int cols, GemvF32Args a, hipStream_t stream) {
   const int mb = (a.M + 15) / 16;
+  if (a.k_end < a.K || a.k_end - a.K > kMaxTail || (a.k_end > a.K && a.ksplit < 2)) return hipErrorInvalidValue;
   hipError_t e;
   switch (mb) {
     case 1: e = launch_mb<1>(cols, epi, a, stream); break;

@@ -301,27 +301,32 @@ void check_dims(int64_t M, int64_t N, int64_t K) {
 // runs) and 32 x 1 (8-byte loads: the per-CU request rate, not the byte
 // count, limits a streaming workgroup). A forced split
 // (edsl_hip_set_gemv_ksplit) limits the choice to the widths that can take it.
-bool plan_gemv(const DeviceState& ds, int64_t N, int64_t K, int* cols_out, int* ks_out) {
+bool plan_gemv(const DeviceState& ds, int64_t N, int64_t K, bool realign, int* cols_out, int* ks_out) {
   static const int kCols[] = {128, 256, 64, 32};
+  if (N < 1 || K % 16 != 0) return false;
   int best_cols = 0, best_ks = 0;
   int64_t best_wgs = 0;
-  for (int cols : kCols) {
-    if (g_force_cols > 0 && cols != g_force_cols) continue;
+  // K is walked in 16-row chunks spread evenly over the ks x wk wave slices;
+  // the automatic plan gives every slice at least two, a forced split at
+  // least one. Realigned rows leave the last row of W to the K tail, so K =
+  // 2^n falls one chunk short of the next split: there all slices but one
+  // get two.
+  const int64_t chunks = K / 16 + (realign ? 1 : 0);
+  // Returns true when the width fills the chip.
+  auto consider = [&](int cols) {
+    if (g_force_cols > 0 && cols != g_force_cols) return false;
     const int64_t wk = gemv_f32_waves_k(cols);
     // The last column block may be partial (its lanes past N read the last
-    // columns and store nothing). K is walked in 16-row chunks spread evenly
-    // over the ks x wk wave slices; the automatic plan gives every slice at
-    // least two, a forced split at least one.
-    if (N < 1 || K % 16 != 0) continue;
+    // columns and store nothing).
     const int64_t groups = (N + cols - 1) / cols;
     int ks = 1;
     if (g_force_ksplit > 0) {
       // A forced split is taken only by widths that can honour it.
-      if (g_force_ksplit > gemv_f32_max_ksplit() || K < 16 * wk * g_force_ksplit) continue;
+      if (g_force_ksplit > gemv_f32_max_ksplit() || K < 16 * wk * g_force_ksplit) return false;
       ks = g_force_ksplit;
     } else {
-      if (K < 32 * wk) continue;
-      while (groups * ks < ds.cus && ks * 2 <= gemv_f32_max_ksplit() && K >= 32 * wk * ks * 2) ks *= 2;
+      if (chunks < 2 * wk) return false;
+      while (groups * ks < ds.cus && ks * 2 <= gemv_f32_max_ksplit() && chunks >= 2 * wk * ks * 2) ks *= 2;
     }
     const int64_t wgs = groups * ks;
     if (wgs > best_wgs) {
@@ -329,8 +334,14 @@ bool plan_gemv(const DeviceState& ds, int64_t N, int64_t K, int* cols_out, int* 
       best_ks = ks;
       best_wgs = wgs;
     }
-    if (wgs >= ds.cus) break;
-  }
+    return wgs >= ds.cus;
+  };
+  // Realigned rows (four columns per lane) stream at 1.5-2x the rate of the
+  // 4-byte loads that 32-column blocks fall back to: those are taken only when
+  // no wider block fits.
+  for (int cols : kCols)
+    if ((!realign || cols > 32) && consider(cols)) break;
+  if (realign && best_cols == 0) consider(32);
   if (best_cols == 0) return false;
   *cols_out = best_cols;
   *ks_out = best_ks;
@@ -363,15 +374,21 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   // (16x8192x8191: 70 vs 134 us, 48x8192x8191: 96 vs 170, 64x8192x8191: 147
   // vs 172) and, on one split, for one or three row blocks (16x4096x50257:
   // 257 vs 290 us, 48x4096x50257: 390 vs 495) but not two or four
-  // (32x4096x50257: 322 vs 296 us, 64x4096x50257: 531 vs 507); with 4-byte
-  // loads when the plan splits K and M <= 48 (four row blocks spill). A
-  // forced split (edsl_hip_set_gemv_ksplit) takes the small-M kernel.
-  const bool gemv_planned = M >= 1 && M <= kGemvMaxM && K16 > 0 && plan_gemv(ds, N, K16, &gemv_cols, &gemv_ks);
+  // (32x4096x50257: 322 vs 296 us, 64x4096x50257: 531 vs 507). Below 8 MiB of
+  // W the layer is latency-bound and the tile's single launch wins
+  // (4x512x511: 8.4 vs 13.9 us; 16x1024x1023: even); at 16 MiB the small-M
+  // kernel does (8x2048x2047: 15.6 vs 30.6 us). With 4-byte loads: when the
+  // plan splits K and M <= 48 (four row blocks spill). A forced split
+  // (edsl_hip_set_gemv_ksplit) takes the small-M kernel.
+  const bool gemv_planned =
+      M >= 1 && M <= kGemvMaxM && K16 > 0 && plan_gemv(ds, N, K16, w_realign, &gemv_cols, &gemv_ks);
   const bool realigned_plan = w_realign && gemv_cols > 32;
   const int row_blocks = (M + 15) / 16;
+  const bool w_large = (int64_t)K * N * (int64_t)sizeof(float) >= (8 << 20);
   if (gemv_planned &&
-      (w_vec || g_force_ksplit > 0 || (realigned_plan && (gemv_ks > 1 || row_blocks == 1 || row_blocks == 3)) ||
-       (gemv_ks > 1 && M <= 48))) {
+      (w_vec || g_force_ksplit > 0 ||
+       (realigned_plan && w_large && (gemv_ks > 1 || row_blocks == 1 || row_blocks == 3)) ||
+       (!realigned_plan && gemv_ks > 1 && M <= 48))) {
     const bool x_ok = al16(L.x) && L.ldx % 4 == 0;
     const bool tail = K16 < K;
     if (tail && gemv_ks == 1) gemv_ks = 2;  // the reduce kernel adds the tail
