@@ -2,12 +2,14 @@
 
 Each case draws a shape (including K = 0 and sizes that are no multiple of
 any tile; a second set draws multiples of 4 up to 1100 with 16-byte aligned
-views, the shapes the edge tiles and padded int8 tiles serve), a dtype, a pattern, host or device operands, and for device
-operands a padded row stride and an element offset (a third set: small M
-with X misaligned on its own and K often not a multiple of 16), then compares the HIP
-result with the oracle: i32 bit-exact (int8-range values take the int8 MFMA
-path, wider ones the exact i32 fallback), f32 within relative Frobenius 1e-5
-and max|delta| <= 1e-4*sqrt(K).
+views, the shapes the edge tiles and padded int8 tiles serve), a dtype, a
+pattern, host or device operands, and for device operands a padded row stride
+and an element offset (a third set: small M with X misaligned on its own and K
+often not a multiple of 16; a fourth: small M with W and Y misaligned on their
+own, N often not a multiple of 4), then compares the HIP result with the
+oracle: i32 bit-exact (int8-range values take the int8 MFMA path, wider ones
+the exact i32 fallback), f32 within relative Frobenius 1e-5 and max|delta| <=
+1e-4*sqrt(K).
 """
 from __future__ import annotations
 
@@ -163,9 +165,53 @@ def test_random_small_m_case(seed, torch_cuda):
     _check_small_m(seed, torch_cuda)
 
 
+# Small M with W (and Y, which shares W's pitch and offset) misaligned by its
+# own pad and offset, N not a multiple of 4 as often as not, and W large
+# enough that the plan streams it realigned (or per column) through the
+# small-M kernel rather than the any-shape tile.
+_UW_M = [1, 3, 16, 17, 33, 48, 64]
+_UW_K = [1003, 2047, 2048, 4099, 8191]
+_UW_N = [1001, 2047, 2048, 4097, 4100, 8191]
+
+
+def _check_small_m_unaligned_w(seed, torch):
+    rng = np.random.default_rng(seed)
+    M, K, N = int(rng.choice(_UW_M)), int(rng.choice(_UW_K)), int(rng.choice(_UW_N))
+    pattern = str(rng.choice(list(_PATTERNS)))
+    bias, act = _PATTERNS[pattern]
+    x_pad, x_off = int(rng.choice([0, 1, 4])), int(rng.choice([0, 2]))
+    w_pad, w_off = int(rng.choice([0, 1, 2, 3, 5])), int(rng.choice([0, 1, 2, 3]))
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.float32(np.sqrt(K))).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, N).astype(np.float32) if bias else None
+    alpha = float(np.float32(rng.uniform(0.01, 0.5)))
+    tX = _device_view(torch, X, x_pad, x_off)
+    tW = _device_view(torch, W, w_pad, w_off)
+    tb = _device_view(torch, b, 0, w_off) if bias else None
+    tY = _device_view(torch, np.zeros((M, N), np.float32), w_pad, w_off)
+    dense_launch(tX, tW, tb, tY, (1 if bias else 0) | (_EPI[act] << 1), alpha)
+    torch.cuda.synchronize()
+    what = f"seed={seed} {pattern} M={M} K={K} N={N} x_pad={x_pad} x_off={x_off} w_pad={w_pad} " \
+           f"w_off={w_off} [{_native.last_plan()}]"
+    try:
+        assert_f32_parity(tY.cpu().numpy(), oracle.dense_f32(X, W, b, act, alpha), K)
+    except AssertionError as e:
+        raise AssertionError(f"{what}: {e}") from None
+    return _native.last_plan()
+
+
+def test_random_small_m_unaligned_w_cases(torch_cuda):
+    plans = [_check_small_m_unaligned_w(seed, torch_cuda) for seed in range(3000, 3040)]
+    # The seeds reach the realigned small-M kernel, its 4-byte column loads
+    # and the any-shape tile.
+    assert any("+wrealigned" in p for p in plans), plans
+    assert any("_anyshape" in p for p in plans), plans
+
+
 def test_random_sweep(torch_cuda):
     """Opt-in wide sweep: EDSL_RANDOM_SWEEP=N runs N more seeds of both case
-    sets (and a small-M case every tenth seed) in this one test. N = 20000
+    sets (and two small-M cases, aligned and misaligned W, every tenth seed)
+    in this one test. N = 20000
     takes about seven and a half minutes on one MI355X; run it with -s to see
     a progress line every 1000 seeds."""
     import os
@@ -177,5 +223,7 @@ def test_random_sweep(torch_cuda):
         _check_case(seed, _case(seed, _EDGE_DIMS, pads=(0, 4, 8), offs=(0, 4), k_zero=False), torch_cuda)
         if seed % 10 == 0:
             _check_small_m(seed, torch_cuda)
+        if seed % 10 == 5:
+            _check_small_m_unaligned_w(seed, torch_cuda)
         if (seed - 9999) % 1000 == 0:  # progress, visible with pytest -s
             print(f"random sweep: {seed - 9999} of {n} seeds passed", flush=True)
