@@ -248,6 +248,24 @@ gemm_f32_kernel(GemmF32Args args) {
   const int half = lane >> 5;
   const int l32 = lane & 31;
 
+  // The epilogue's bias values (columns col0 + c, c < CP), loaded before the
+  // first K step's tile so that their latency hides behind it rather than
+  // adding to the epilogue's.
+  const int col0 = n0 + wave_n * WN + CP * l32;
+  float bvals[CP];
+#pragma unroll
+  for (int c = 0; c < CP; ++c) bvals[c] = 0.0f;
+  if constexpr (epi_has_bias(EPI)) {
+    if constexpr (GUARD == kGuardNone) {
+      load_b_frag<CP>(args.bias + col0, bvals);
+    } else if constexpr (GUARD == kGuardEdge) {
+      if (col0 < N) load_b_frag<CP>(args.bias + col0, bvals);
+    } else {
+#pragma unroll
+      for (int c = 0; c < CP; ++c) bvals[c] = (col0 + c < N) ? args.bias[col0 + c] : 0.0f;
+    }
+  }
+
   // A wave raises its issue priority while it reads fragments and runs its
   // MFMAs, so waves with MFMAs ready win issue over waves issuing loads or
   // LDS stores (same box: c3 88.2 -> 88.5-88.8 % of peak, the 8-way c3
@@ -451,20 +469,6 @@ gemm_f32_kernel(GemmF32Args args) {
 
   // Epilogue: lane holds rows rbase + 8*(r/4) + 4*half + r%4 of each 32-row
   // block and columns col0 + c, c < CP.
-  const int col0 = n0 + wave_n * WN + CP * l32;
-  float bvals[CP];
-#pragma unroll
-  for (int c = 0; c < CP; ++c) bvals[c] = 0.0f;
-  if constexpr (epi_has_bias(EPI)) {
-    if constexpr (GUARD == kGuardNone) {
-      load_b_frag<CP>(args.bias + col0, bvals);
-    } else if constexpr (GUARD == kGuardEdge) {
-      if (col0 < N) load_b_frag<CP>(args.bias + col0, bvals);
-    } else {
-#pragma unroll
-      for (int c = 0; c < CP; ++c) bvals[c] = (col0 + c < N) ? args.bias[col0 + c] : 0.0f;
-    }
-  }
   const float alpha = args.alpha;
 #pragma unroll
   for (int i = 0; i < RB; ++i) {
