@@ -101,6 +101,9 @@ void edsl_hip_set_gemv_ksplit(int ksplit);
 /* Small-M column block: columns per workgroup, one of 32, 64, 128, 256;
  * 0 = automatic. */
 void edsl_hip_set_gemv_cols(int cols);
+/* Small-M kernel choice for M <= 64: 0 = automatic (the kernel or the tiles,
+ * by shape), 1 = the small-M kernel whenever it can plan the layer. */
+void edsl_hip_set_small_m(int mode);
 /* int8 GEMM variant = wave layout and operand prefetch depth in 32-k steps:
  * 0..2 give each of 4 waves a 64x64 quadrant of the 128x128 tile, depth
  * 0: 4, 1: 2, 2: 8 when K % 256 == 0, else 4; 3 gives each wave the whole

@@ -152,6 +152,7 @@ DeviceState g_dev[kMaxDevices];
 int g_force_cfg = -1;
 int g_force_ksplit = 0;
 int g_force_cols = 0;
+int g_force_small_m = 0;  // 1: the small-M kernel whenever it can plan the layer
 int g_force_i8 = -1;
 bool g_no_pipeline = false;  // EDSL_HIP_HOST_PIPELINE=0: plain staged sequence for host buffers
 
@@ -162,6 +163,7 @@ void read_env_overrides() {
   if (const char* s = getenv("EDSL_HIP_F32_CONFIG")) g_force_cfg = atoi(s);
   if (const char* s = getenv("EDSL_HIP_GEMV_KSPLIT")) g_force_ksplit = atoi(s);
   if (const char* s = getenv("EDSL_HIP_GEMV_COLS")) g_force_cols = atoi(s);
+  if (const char* s = getenv("EDSL_HIP_SMALL_M")) g_force_small_m = atoi(s);
   if (const char* s = getenv("EDSL_HIP_I8_VARIANT")) g_force_i8 = atoi(s);
   if (const char* s = getenv("EDSL_HIP_HOST_PIPELINE")) g_no_pipeline = atoi(s) == 0;
 }
@@ -379,17 +381,40 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   // (4x512x511: 8.4 vs 13.9 us; 16x1024x1023: even); at 16 MiB the small-M
   // kernel does (8x2048x2047: 15.6 vs 30.6 us). With 4-byte loads: when the
   // plan splits K and M <= 48 (four row blocks spill). A forced split
-  // (edsl_hip_set_gemv_ksplit) takes the small-M kernel.
+  // (edsl_hip_set_gemv_ksplit) or edsl_hip_set_small_m(1) takes the small-M
+  // kernel.
   const bool gemv_planned =
       M >= 1 && M <= kGemvMaxM && K16 > 0 && plan_gemv(ds, N, K16, w_realign, &gemv_cols, &gemv_ks);
   const bool realigned_plan = w_realign && gemv_cols > 32;
   const int row_blocks = (M + 15) / 16;
   const bool w_large = (int64_t)K * N * (int64_t)sizeof(float) >= (8 << 20);
+  // Vector-aligned W: the small-M kernel's parallelism comes from splitting
+  // K, the tiles' from the M x N output, so short K favours the tiles (32x32
+  // tiles read W once up to 32 rows, twice up to 64). Measured on one box,
+  // small-M kernel vs 32x32 tile: one row block 16x512x512 5.6 vs 6.2 us,
+  // 16x256x4096 8.1 vs 4.5, 1x256x256 6.1 vs 4.2; two 32x1024x1024 9.6 vs
+  // 9.4, 32x2048x1024 10.1 vs 16.2, 32x512x512 8.6 vs 6.0; three
+  // 48x2048x2048 13.6 vs 17.0, 48x1024x4096 13.6 vs 10.5; four 64x16384x4096
+  // 113 vs 128, 64x8192x4096 62 vs 63, 64x8192x8192 112 vs 112, 64x4096x8192
+  // 62 vs 54, 64x1024x1024 14.8 vs 9.5. With X rows not 16-byte aligned the
+  // tiles are the any-shape ones and the small-M kernel is kept.
+  const bool x_vec = al16(L.x) && L.ldx % 4 == 0;
+  bool vec_small_m = true;
+  if (x_vec) {
+    if (row_blocks == 1)
+      vec_small_m = K >= 512;
+    else if (row_blocks == 2)
+      vec_small_m = K >= 1024;
+    else if (row_blocks == 3)
+      vec_small_m = K >= 2048;
+    else
+      vec_small_m = (int64_t)K >= 2 * (int64_t)N;
+  }
   if (gemv_planned &&
-      (w_vec || g_force_ksplit > 0 ||
+      ((w_vec && vec_small_m) || g_force_ksplit > 0 || g_force_small_m == 1 ||
        (realigned_plan && w_large && (gemv_ks > 1 || row_blocks == 1 || row_blocks == 3)) ||
-       (!realigned_plan && gemv_ks > 1 && M <= 48))) {
-    const bool x_ok = al16(L.x) && L.ldx % 4 == 0;
+       (!w_vec && !realigned_plan && gemv_ks > 1 && M <= 48))) {
+    const bool x_ok = x_vec;
     const bool tail = K16 < K;
     if (tail && gemv_ks == 1) gemv_ks = 2;  // the reduce kernel adds the tail
     GemvF32Args a{};
@@ -1118,6 +1143,12 @@ void edsl_hip_set_gemv_ksplit(int ksplit) {
   std::lock_guard<std::mutex> lock(g_mu);
   read_env_overrides();
   g_force_ksplit = ksplit;
+}
+
+void edsl_hip_set_small_m(int mode) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  read_env_overrides();
+  g_force_small_m = mode;
 }
 
 void edsl_hip_set_gemv_cols(int cols) {

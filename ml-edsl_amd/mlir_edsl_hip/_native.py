@@ -73,6 +73,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.edsl_hip_set_gemv_ksplit.restype = None
     L.edsl_hip_set_gemv_cols.argtypes = [c_int]
     L.edsl_hip_set_gemv_cols.restype = None
+    L.edsl_hip_set_small_m.argtypes = [c_int]
+    L.edsl_hip_set_small_m.restype = None
     L.edsl_hip_set_i8_variant.argtypes = [c_int]
     L.edsl_hip_set_i8_variant.restype = None
     L.edsl_hip_i8_variant_count.argtypes = []

@@ -125,5 +125,10 @@ def set_gemv_cols(cols: int) -> None:
     _native.lib().edsl_hip_set_gemv_cols(cols)
 
 
+def set_small_m(mode: int) -> None:
+    """0: automatic; 1: the small-M kernel whenever it can plan the layer."""
+    _native.lib().edsl_hip_set_small_m(mode)
+
+
 def set_i8_variant(variant: int) -> None:
     _native.lib().edsl_hip_set_i8_variant(variant)

@@ -152,10 +152,21 @@ def test_auto_plan_takes_any_shape_tiles(shape, pad_off, tile, torch_cuda):
     assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
 
 
+def _run_small_m(torch, X, W, b, pad=0, off=0):
+    """_run with the small-M kernel taken wherever it can plan the layer (the
+    automatic choice gives short-K layers to the tiles)."""
+    from mlir_edsl_hip.device import set_small_m
+    set_small_m(1)
+    try:
+        return _run(torch, X, W, b, pad, off)
+    finally:
+        set_small_m(0)
+
+
 @pytest.mark.parametrize("M, K, N", [(16, 8000, 8192), (16, 8000, 1024), (3, 4112, 2048), (40, 1040, 512)])
 def test_small_m_uneven_k_slices(M, K, N, torch_cuda):
     X, W, b = _inputs(M, K, N, M * 3 + K)
-    got, plan = _run(torch_cuda, X, W, b)
+    got, plan = _run_small_m(torch_cuda, X, W, b)
     assert plan.startswith("gemv_f32"), plan
     assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
 
@@ -226,6 +237,22 @@ def test_realigned_w_rows(M, cols, torch_cuda):
     assert checked == 55
 
 
+# The automatic choice between the small-M kernel and the tiles for aligned
+# operands: short K goes to the tiles (32x32 tiles read W once up to 32 rows,
+# twice up to 64), long K to the small-M kernel.
+@pytest.mark.parametrize("M, K, N, kernel", [
+    (16, 512, 512, "gemv_f32"), (1, 256, 256, "gemm_f32"), (16, 256, 4096, "gemm_f32"),
+    (32, 2048, 1024, "gemv_f32"), (32, 512, 512, "gemm_f32"), (48, 2048, 2048, "gemv_f32"),
+    (48, 1024, 4096, "gemm_f32"), (64, 256, 256, "gemm_f32"), (64, 4096, 1024, "gemv_f32"),
+    (64, 4096, 8192, "gemm_f32"),
+])
+def test_auto_choice_small_m_or_tile(M, K, N, kernel, torch_cuda):
+    X, W, b = _inputs(M, K, N, M + 5 * K + N)
+    got, plan = _run(torch_cuda, X, W, b)
+    assert plan.startswith(kernel), plan
+    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+
+
 def test_small_m_forced_splits_on_uneven_k(torch_cuda):
     from mlir_edsl_hip.device import set_gemv_cols, set_gemv_ksplit
     M, K, N = 16, 8000, 1024
@@ -249,7 +276,7 @@ def test_small_m_partial_column_blocks(M, K, N, torch_cuda):
     """N a multiple of 4 but not of the column block: the last block is
     partial (its lanes read the last columns and store nothing)."""
     X, W, b = _inputs(M, K, N, M + K + N)
-    got, plan = _run(torch_cuda, X, W, b)
+    got, plan = _run_small_m(torch_cuda, X, W, b)
     assert plan.startswith("gemv_f32"), plan
     assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
 

@@ -82,7 +82,12 @@ def test_graph_replay_matches_eager(name, dtype, M, widths, epis, plans):
         big = torch.randn(64, 8192, device="cuda", generator=g)
         Wb = torch.randn(8192, 8192, device="cuda", generator=g)
         yb = torch.empty(64, 8192, device="cuda")
-        dense_launch(big, Wb, None, yb, 0)
+        from mlir_edsl_hip.device import set_small_m
+        set_small_m(1)  # four row blocks at K = N go to the tiles by default
+        try:
+            dense_launch(big, Wb, None, yb, 0)
+        finally:
+            set_small_m(0)
         assert "ksplit=" in _native.last_plan() and "ksplit=1 " not in _native.last_plan()
         xo = torch.randn(64, 8191, device="cuda", generator=g)  # unaligned rows and a K tail
         dense_launch(xo, Wb[:8191], None, yb, 0)

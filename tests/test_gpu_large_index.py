@@ -77,8 +77,13 @@ def test_small_m_weights_beyond_2_31(torch_cuda):
     W = torch.randn(K, N, device="cuda", generator=g)
     b = torch.randn(N, device="cuda", generator=g)
     Y = torch.empty(M, N, device="cuda")
-    dense_launch(X, W, b, Y, _native.EPI_BIAS_RELU)
-    torch.cuda.synchronize()
+    from mlir_edsl_hip.device import set_small_m
+    set_small_m(1)  # K = 256 alone would give the layer to the tiles
+    try:
+        dense_launch(X, W, b, Y, _native.EPI_BIAS_RELU)
+        torch.cuda.synchronize()
+    finally:
+        set_small_m(0)
     plan = _native.last_plan()
     assert plan.startswith("gemv_f32"), plan
     cols = torch.from_numpy(np.unique(np.r_[0, 1, 4096, N // 2, N - 129, N - 4, N - 1])).cuda()

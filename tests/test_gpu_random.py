@@ -148,8 +148,13 @@ def _check_small_m(seed, torch):
     tW = _device_view(torch, W, w_pad, w_off)
     tb = _device_view(torch, b, 0, w_off) if bias else None
     tY = _device_view(torch, np.zeros((M, N), np.float32), w_pad, w_off)
-    dense_launch(tX, tW, tb, tY, (1 if bias else 0) | (_EPI[act] << 1), alpha)
-    torch.cuda.synchronize()
+    from mlir_edsl_hip.device import set_small_m
+    set_small_m(1)  # aligned short-K layers would otherwise go to the tiles
+    try:
+        dense_launch(tX, tW, tb, tY, (1 if bias else 0) | (_EPI[act] << 1), alpha)
+        torch.cuda.synchronize()
+    finally:
+        set_small_m(0)
     plan = _native.last_plan()
     what = f"seed={seed} {pattern} M={M} K={K} N={N} x_pad={x_pad} x_off={x_off} w_pad={w_pad} " \
            f"w_off={w_off} [{plan}]"
