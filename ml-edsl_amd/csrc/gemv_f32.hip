@@ -14,20 +14,23 @@
 //    4*CPL-byte load. MFMA (step s, column phase c) pairs X[.][k0+4g+s] with
 //    W[k0+4g+s][n0 + CPL*(l%16) + c], so lane l%16 accumulates columns
 //    n0 + CPL*(l%16) + c: a wave owns 16*CPL columns and stores CPL per row.
-//  * A workgroup is 16 waves covering `cols` adjacent columns: WN waves side
-//    by side (cols = 16*CPL*WN), and WK = 16/WN waves splitting the
-//    workgroup's K range. The WK slices are summed in LDS, in wave order.
-//    cols = 32 (CPL 2, WN 1) gives N/32 workgroups that each own the full K:
-//    at N = 8192 that is one per CU and no cross-workgroup reduction at all.
+//  * A workgroup is NW waves (4 for one row block, 8 for more) covering
+//    `cols` adjacent columns: WN waves side by side (cols = 16*CPL*WN), and
+//    WK = NW/WN waves splitting the workgroup's K range. The WK slices are
+//    summed in LDS, in wave order. Fewer waves per CU keep fewer HBM rows
+//    open at once: 16-wave workgroups were 2-3 % slower at M=16, K=N=8192,
+//    6-10 % at M=48-64 and 10 % on realigned rows (16x8192x8191).
 //  * Wider column blocks read longer row runs but give fewer workgroups;
 //    they split K over `ksplit` workgroups to fill the chip. Each writes its
 //    partial tile, and a second small kernel sums the partials in split order
 //    and applies bias and activation. (A "last workgroup to arrive reduces"
 //    variant, with the partials exchanged through agent-scope atomics, was
 //    measured: it costs as much as the extra launch, so it is not used.)
-//  * Each wave starts its K walk at a hashed offset (wrapping), so the rows
+//  * Each K slice starts its walk at a hashed offset (wrapping), so the rows
 //    in flight at any moment are spread over the matrix and over the HBM
-//    channels instead of every wave hitting the same few rows.
+//    channels instead of every wave hitting the same few rows. Waves side by
+//    side share the offset, so a workgroup reads WN*16*CPL*4 contiguous bytes
+//    of a row at a time (a per-wave offset was ~2 % slower at M=16).
 //  * W registers are reloaded one at a time right after the MFMAs that read
 //    them, so a wave's loads stay in flight while it computes.
 //    A wave that drained its loads before every batch of MFMAs streamed
@@ -44,7 +47,8 @@ namespace {
 
 typedef float f32x3 __attribute__((ext_vector_type(3)));
 
-constexpr int kWavesPerWG = 16;
+// Waves per workgroup for MB row blocks of 16.
+constexpr int waves_per_wg(int mb) { return mb == 1 ? 4 : 8; }
 constexpr int kMaxSplit = 16;
 constexpr int kMaxTail = 16;  // rows of the K tail (GemvF32Args::k_end - K)
 
@@ -72,10 +76,12 @@ __device__ __forceinline__ float epilogue_rt(float acc, float b, float alpha, in
 // by the neighbouring lane), and a select by the row's offset within its
 // chunk picks them; the caller leaves the last row of W to the K tail.
 template <int MB, int CPL, int WN, bool XV, int WM>
-__global__ void __launch_bounds__(kWavesPerWG * 64)
+__global__ void __launch_bounds__(waves_per_wg(MB) * 64)
 gemv_f32_kernel(GemvF32Args a, int epi) {
   using vec = typename std::conditional<CPL == 4, f32x4, f32x2>::type;
-  constexpr int WK = kWavesPerWG / WN;
+  constexpr int NW = waves_per_wg(MB);
+  static_assert(NW % WN == 0, "waves side by side must divide the workgroup");
+  constexpr int WK = NW / WN;
   constexpr int kWaveCols = 16 * CPL;
   constexpr int kGroupCols = kWaveCols * WN;
   // 16-row steps per loop iteration: 8 W loads in flight per lane for one row
@@ -119,8 +125,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
   // its 16-byte chunk depends only on the row's slot s = q % 4 in the step:
   // dsh[s], the same for every lane and step.
   //
-  // With up to three row blocks (kDefer) a lane loads one chunk per row, the
-  // one holding its first column. The next chunk, which holds the rest, is
+  // A lane loads one chunk per row, the one holding its first column. The next chunk, which holds the rest, is
   // its right neighbour's, taken with a row shift (lanes 16g .. 16g+15 share
   // a row); only lane 16g+15 has no neighbour and loads it as well (the other
   // lanes masked off; 12 bytes, the most it needs). Both are kept until just
@@ -129,16 +134,11 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
   // last lane that holds a column below N, so that its neighbour finds the
   // right chunk there. Every chunk loaded holds a column below N of its row or
   // one of the next row's first elements (the caller leaves the last row of W
-  // to the K tail), so no load leaves the matrix's pages. With four row blocks
-  // the registers hold the accumulators instead: each lane loads both chunks
-  // and selects at once, and lanes past N read columns 0..3.
-  constexpr bool kDefer = WM == kWRealign && MB <= 3;
+  // to the K tail), so no load leaves the matrix's pages.
+  constexpr bool kDefer = WM == kWRealign;
   const int col_lane = n0 + CPL * li;
   const int r4 = (a.N + 3) & ~3;
-  const int col_w = WM == kWVector ? min(col_lane, a.N - CPL)
-                    : kDefer       ? min(col_lane, r4)
-                    : WM == kWRealign ? (col_lane < a.N ? col_lane : 0)
-                                      : 0;
+  const int col_w = WM == kWVector ? min(col_lane, a.N - CPL) : kDefer ? min(col_lane, r4) : 0;
   const float* wbase = a.W + (int64_t)(kbeg + 4 * lg) * ldw + col_w;
   int cofs[CPL];
 #pragma unroll
@@ -178,17 +178,6 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
       r.c1 = f32x3{0.0f, 0.0f, 0.0f};
       if (own_next && dsh[s] != 0) r.c1 = __builtin_nontemporal_load(reinterpret_cast<const f32x3*>(p0 + 1));
       return r;
-    } else if constexpr (WM == kWRealign) {
-      const int d = dsh[s];
-      const f32x4* p0 = reinterpret_cast<const f32x4*>(row - d);
-      const f32x4 c0 = __builtin_nontemporal_load(p0);
-      const f32x4 c1 = __builtin_nontemporal_load(d != 0 ? p0 + 1 : p0);
-      vec v;
-      v[0] = d == 0 ? c0[0] : d == 1 ? c0[1] : d == 2 ? c0[2] : c0[3];
-      v[1] = d == 0 ? c0[1] : d == 1 ? c0[2] : d == 2 ? c0[3] : c1[0];
-      v[2] = d == 0 ? c0[2] : d == 1 ? c0[3] : d == 2 ? c1[0] : c1[1];
-      v[3] = d == 0 ? c0[3] : d == 1 ? c1[0] : d == 2 ? c1[1] : c1[2];
-      return v;
     } else {
       vec v;
 #pragma unroll
@@ -251,7 +240,7 @@ gemv_f32_kernel(GemvF32Args a, int epi) {
   // (M = 64 with 4 columns per lane uses all 128 registers and 8-16 bytes of
   // scratch); at K = N = 4096 the two measure the same.
   const int nit = kwave / (16 * kU);
-  const int r0 = nit > 0 ? (int)(((unsigned)blockIdx.x * 2654435761u >> 8) + (unsigned)wave * 977u) % nit : 0;
+  const int r0 = nit > 0 ? (int)(((unsigned)blockIdx.x * 2654435761u >> 8) + (unsigned)wk * 977u) % nit : 0;
   if (nit > 0) {
     wreg w[4 * kU];
     f32x4 x[kU][MB], xn[kU][MB];
@@ -432,7 +421,7 @@ __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi
 template <int MB, bool XV, int WM>
 hipError_t launch_mb_x(int cols, int epi, const GemvF32Args& a, hipStream_t stream) {
   const dim3 grid(((a.N + cols - 1) / cols) * a.ksplit);
-  const dim3 block(kWavesPerWG * 64);
+  const dim3 block(waves_per_wg(MB) * 64);
   // Two columns per lane take 4-byte W loads where four would be realigned.
   constexpr int WM2 = WM == kWRealign ? kWScalar : WM;
   switch (cols) {
@@ -463,7 +452,10 @@ hipError_t launch_mb(int cols, int epi, const GemvF32Args& a, hipStream_t stream
 
 }  // namespace
 
-int gemv_f32_waves_k(int cols) { return cols <= 64 ? kWavesPerWG : kWavesPerWG / (cols / 64); }
+int gemv_f32_waves_k(int cols, int M) {
+  const int nw = waves_per_wg((M + 15) / 16);
+  return cols <= 64 ? nw : nw / (cols / 64);
+}
 
 int gemv_f32_w_mode(const GemvF32Args& a) {
   if (gemv_f32_vector_rows(a)) return kWVector;

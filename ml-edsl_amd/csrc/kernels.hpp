@@ -64,15 +64,16 @@ struct GemvF32Args {
 // caller must leave the last row of W to the K tail).
 enum : int { kWVector = 0, kWScalar = 1, kWRealign = 2 };
 
-// A workgroup is 16 waves over `cols` adjacent columns (32, 64, 128 or 256),
-// the last block possibly partial; the waves not side by side split K, which
-// is walked in 16-row chunks. Requirements (checked by the caller):
+// A workgroup is 4 waves (one row block) or 8 over `cols` adjacent columns
+// (32, 64, 128 or 256), the last block possibly partial; the waves not side
+// by side split K, which is walked in 16-row chunks. Requirements (checked by the caller):
 // 1 <= M <= 64, K % 16 == 0, ksplit > 1 when there is a K tail, w_mode set
 // (kWRealign: K < the rows of W). Operands may have any alignment, row
 // strides and N: X rows that are not 16-byte aligned are read with 4-byte
 // loads; W, the bias and Y as w_mode says.
 hipError_t launch_gemv_f32(int epi, int cols, GemvF32Args args, hipStream_t stream);
-int gemv_f32_waves_k(int cols);
+// Waves of a workgroup that split K, for this column block width and M.
+int gemv_f32_waves_k(int cols, int M);
 // W, Y and the bias 16-byte aligned with row strides and N multiples of 4.
 bool gemv_f32_vector_rows(const GemvF32Args& a);
 // The W mode for these operands: kWVector when gemv_f32_vector_rows holds,

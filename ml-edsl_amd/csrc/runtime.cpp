@@ -303,7 +303,7 @@ void check_dims(int64_t M, int64_t N, int64_t K) {
 // runs) and 32 x 1 (8-byte loads: the per-CU request rate, not the byte
 // count, limits a streaming workgroup). A forced split
 // (edsl_hip_set_gemv_ksplit) limits the choice to the widths that can take it.
-bool plan_gemv(const DeviceState& ds, int64_t N, int64_t K, bool realign, int* cols_out, int* ks_out) {
+bool plan_gemv(const DeviceState& ds, int64_t M, int64_t N, int64_t K, bool realign, int* cols_out, int* ks_out) {
   static const int kCols[] = {128, 256, 64, 32};
   if (N < 1 || K % 16 != 0) return false;
   int best_cols = 0, best_ks = 0;
@@ -317,7 +317,7 @@ bool plan_gemv(const DeviceState& ds, int64_t N, int64_t K, bool realign, int* c
   // Returns true when the width fills the chip.
   auto consider = [&](int cols) {
     if (g_force_cols > 0 && cols != g_force_cols) return false;
-    const int64_t wk = gemv_f32_waves_k(cols);
+    const int64_t wk = gemv_f32_waves_k(cols, (int)M);
     // The last column block may be partial (its lanes past N read the last
     // columns and store nothing).
     const int64_t groups = (N + cols - 1) / cols;
@@ -384,20 +384,20 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   // (edsl_hip_set_gemv_ksplit) or edsl_hip_set_small_m(1) takes the small-M
   // kernel.
   const bool gemv_planned =
-      M >= 1 && M <= kGemvMaxM && K16 > 0 && plan_gemv(ds, N, K16, w_realign, &gemv_cols, &gemv_ks);
+      M >= 1 && M <= kGemvMaxM && K16 > 0 && plan_gemv(ds, M, N, K16, w_realign, &gemv_cols, &gemv_ks);
   const bool realigned_plan = w_realign && gemv_cols > 32;
   const int row_blocks = (M + 15) / 16;
   const bool w_large = (int64_t)K * N * (int64_t)sizeof(float) >= (8 << 20);
   // Vector-aligned W: the small-M kernel's parallelism comes from splitting
   // K, the tiles' from the M x N output, so short K favours the tiles (32x32
   // tiles read W once up to 32 rows, twice up to 64). Measured on one box,
-  // small-M kernel vs 32x32 tile: one row block 16x512x512 5.6 vs 6.2 us,
-  // 16x256x4096 8.1 vs 4.5, 1x256x256 6.1 vs 4.2; two 32x1024x1024 9.6 vs
-  // 9.4, 32x2048x1024 10.1 vs 16.2, 32x512x512 8.6 vs 6.0; three
-  // 48x2048x2048 13.6 vs 17.0, 48x1024x4096 13.6 vs 10.5; four 64x16384x4096
-  // 113 vs 128, 64x8192x4096 62 vs 63, 64x8192x8192 112 vs 112, 64x4096x8192
-  // 62 vs 54, 64x1024x1024 14.8 vs 9.5. With X rows not 16-byte aligned the
-  // tiles are the any-shape ones and the small-M kernel is kept.
+  // small-M kernel vs 32x32 tile: one row block 16x512x512 5.7 vs 6.1 us,
+  // 16x256x4096 5.7 vs 4.4, 1x256x256 5.0 vs 4.2; two 32x1024x1024 7.9 vs
+  // 9.4, 32x512x512 7.5 vs 6.1; three 48x2048x2048 14.3 vs 16.9,
+  // 48x1024x4096 14.3 vs 10.4; four 64x8192x8192 101 vs 115, 64x4096x8192
+  // 52 vs 57, 64x2048x1024 11.2 vs 16.3, 64x2048x8192 32 vs 28, 64x2048x2048
+  // 17.4 vs 16.4, 64x1024x1024 10.3 vs 9.5. With X rows not 16-byte aligned
+  // the tiles are the any-shape ones and the small-M kernel is kept.
   const bool x_vec = al16(L.x) && L.ldx % 4 == 0;
   bool vec_small_m = true;
   if (x_vec) {
@@ -408,7 +408,7 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     else if (row_blocks == 3)
       vec_small_m = K >= 2048;
     else
-      vec_small_m = (int64_t)K >= 2 * (int64_t)N;
+      vec_small_m = K >= 4096 || (int64_t)K >= 2 * (int64_t)N;
   }
   if (gemv_planned &&
       ((w_vec && vec_small_m) || g_force_ksplit > 0 || g_force_small_m == 1 ||

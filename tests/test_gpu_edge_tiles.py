@@ -244,7 +244,7 @@ def test_realigned_w_rows(M, cols, torch_cuda):
     (16, 512, 512, "gemv_f32"), (1, 256, 256, "gemm_f32"), (16, 256, 4096, "gemm_f32"),
     (32, 2048, 1024, "gemv_f32"), (32, 512, 512, "gemm_f32"), (48, 2048, 2048, "gemv_f32"),
     (48, 1024, 4096, "gemm_f32"), (64, 256, 256, "gemm_f32"), (64, 4096, 1024, "gemv_f32"),
-    (64, 4096, 8192, "gemm_f32"),
+    (64, 4096, 8192, "gemv_f32"), (64, 2048, 8192, "gemm_f32"), (64, 2048, 2048, "gemm_f32"),
 ])
 def test_auto_choice_small_m_or_tile(M, K, N, kernel, torch_cuda):
     X, W, b = _inputs(M, K, N, M + 5 * K + N)
