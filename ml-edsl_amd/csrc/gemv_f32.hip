@@ -47,8 +47,8 @@ namespace {
 
 typedef float f32x3 __attribute__((ext_vector_type(3)));
 
-// Waves per workgroup for MB row blocks of 16.
-constexpr int waves_per_wg(int mb) { return mb == 1 ? 4 : 8; }
+// Waves per workgroup for MB row blocks of 16 and WN waves side by side.
+constexpr int waves_per_wg(int mb, int wn) { return (mb == 1 ? 4 : 8) > wn ? (mb == 1 ? 4 : 8) : wn; }
 constexpr int kMaxSplit = 16;
 constexpr int kMaxTail = 16;  // rows of the K tail (GemvF32Args::k_end - K)
 
@@ -76,10 +76,10 @@ __device__ __forceinline__ float epilogue_rt(float acc, float b, float alpha, in
 // by the neighbouring lane), and a select by the row's offset within its
 // chunk picks them; the caller leaves the last row of W to the K tail.
 template <int MB, int CPL, int WN, bool XV, int WM>
-__global__ void __launch_bounds__(waves_per_wg(MB) * 64)
+__global__ void __launch_bounds__(waves_per_wg(MB, WN) * 64)
 gemv_f32_kernel(GemvF32Args a, int epi) {
   using vec = typename std::conditional<CPL == 4, f32x4, f32x2>::type;
-  constexpr int NW = waves_per_wg(MB);
+  constexpr int NW = waves_per_wg(MB, WN);
   static_assert(NW % WN == 0, "waves side by side must divide the workgroup");
   constexpr int WK = NW / WN;
   constexpr int kWaveCols = 16 * CPL;
@@ -421,14 +421,14 @@ __global__ void __launch_bounds__(256) gemv_reduce_kernel(GemvF32Args a, int epi
 template <int MB, bool XV, int WM>
 hipError_t launch_mb_x(int cols, int epi, const GemvF32Args& a, hipStream_t stream) {
   const dim3 grid(((a.N + cols - 1) / cols) * a.ksplit);
-  const dim3 block(waves_per_wg(MB) * 64);
+  auto block = [](int wn) { return dim3(waves_per_wg(MB, wn) * 64); };
   // Two columns per lane take 4-byte W loads where four would be realigned.
   constexpr int WM2 = WM == kWRealign ? kWScalar : WM;
   switch (cols) {
-    case 32: hipLaunchKernelGGL((gemv_f32_kernel<MB, 2, 1, XV, WM2>), grid, block, 0, stream, a, epi); break;
-    case 64: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 1, XV, WM>), grid, block, 0, stream, a, epi); break;
-    case 128: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 2, XV, WM>), grid, block, 0, stream, a, epi); break;
-    case 256: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 4, XV, WM>), grid, block, 0, stream, a, epi); break;
+    case 32: hipLaunchKernelGGL((gemv_f32_kernel<MB, 2, 1, XV, WM2>), grid, block(1), 0, stream, a, epi); break;
+    case 64: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 1, XV, WM>), grid, block(1), 0, stream, a, epi); break;
+    case 128: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 2, XV, WM>), grid, block(2), 0, stream, a, epi); break;
+    case 256: hipLaunchKernelGGL((gemv_f32_kernel<MB, 4, 4, XV, WM>), grid, block(4), 0, stream, a, epi); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -453,8 +453,8 @@ hipError_t launch_mb(int cols, int epi, const GemvF32Args& a, hipStream_t stream
 }  // namespace
 
 int gemv_f32_waves_k(int cols, int M) {
-  const int nw = waves_per_wg((M + 15) / 16);
-  return cols <= 64 ? nw : nw / (cols / 64);
+  const int wn = cols <= 64 ? 1 : cols / 64;
+  return waves_per_wg((M + 15) / 16, wn) / wn;
 }
 
 int gemv_f32_w_mode(const GemvF32Args& a) {
