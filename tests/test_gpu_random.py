@@ -217,8 +217,8 @@ def test_random_sweep(torch_cuda):
     """Opt-in wide sweep: EDSL_RANDOM_SWEEP=N runs N more seeds of both case
     sets (and two small-M cases, aligned and misaligned W, every tenth seed)
     in this one test. N = 20000
-    takes about seven and a half minutes on one MI355X; run it with -s to see
-    a progress line every 1000 seeds."""
+    takes about eleven minutes on one MI355X; run it with -s to see a
+    progress line every 1000 seeds."""
     import os
     n = int(os.environ.get("EDSL_RANDOM_SWEEP", "0"))
     if n <= 0:
