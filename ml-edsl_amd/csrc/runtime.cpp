@@ -369,20 +369,19 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   const bool w_realign = !w_vec && N >= 4;
   const int K16 = w_realign ? ((K - 1) & ~15) : (K & ~15);
   // With W, Y or the bias not vector-aligned the small-M kernel streams W
-  // realigned at ~3.2-3.9 TB/s with one row block, ~2.6 with two and ~2.2
-  // with three (~2 TB/s with 4-byte loads: N < 4 or 32-column blocks). The
-  // 32x32 any-shape tile reads W once per 32 rows of M at ~2.8 TB/s. So the
-  // small-M kernel is taken realigned whenever its plan splits K
-  // (16x8192x8191: 70 vs 134 us, 48x8192x8191: 96 vs 170, 64x8192x8191: 147
-  // vs 172) and, on one split, for one or three row blocks (16x4096x50257:
-  // 257 vs 290 us, 48x4096x50257: 390 vs 495) but not two or four
-  // (32x4096x50257: 322 vs 296 us, 64x4096x50257: 531 vs 507). Below 8 MiB of
-  // W the layer is latency-bound and the tile's single launch wins
+  // realigned at ~3.3-4.4 TB/s with one row block (~2 TB/s with 4-byte loads:
+  // N < 4 or 32-column blocks); the 32x32 any-shape tile reads W once per 32
+  // rows of M at ~2.8 TB/s. So the small-M kernel is taken realigned whenever
+  // its plan splits K (16x8192x8191: 61 vs 134 us, 40x8192x8191: 94 vs 170,
+  // 64x8192x8191: 120 vs 172) and, on one split, for one or three row blocks
+  // (16x4096x50257: 249 vs 290 us, 48x4096x50257: 362 vs 495) but not two or
+  // four (32x4096x50257: 322 vs 296 us, 64x4096x50257: 531 vs 507). Below 8
+  // MiB of W the layer is latency-bound and the tile's single launch wins
   // (4x512x511: 8.4 vs 13.9 us; 16x1024x1023: even); at 16 MiB the small-M
   // kernel does (8x2048x2047: 15.6 vs 30.6 us). With 4-byte loads: when the
-  // plan splits K and M <= 48 (four row blocks spill). A forced split
-  // (edsl_hip_set_gemv_ksplit) or edsl_hip_set_small_m(1) takes the small-M
-  // kernel.
+  // plan splits K and M <= 48 (measured up to three row blocks). A forced
+  // split (edsl_hip_set_gemv_ksplit) or edsl_hip_set_small_m(1) takes the
+  // small-M kernel.
   const bool gemv_planned =
       M >= 1 && M <= kGemvMaxM && K16 > 0 && plan_gemv(ds, M, N, K16, w_realign, &gemv_cols, &gemv_ks);
   const bool realigned_plan = w_realign && gemv_cols > 32;
