@@ -371,17 +371,18 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   // With W, Y or the bias not vector-aligned the small-M kernel streams W
   // realigned at ~3.3-4.4 TB/s with one row block (~2 TB/s with 4-byte loads:
   // N < 4 or 32-column blocks); the 32x32 any-shape tile reads W once per 32
-  // rows of M at ~2.8 TB/s. So the small-M kernel is taken realigned whenever
-  // its plan splits K (16x8192x8191: 61 vs 134 us, 40x8192x8191: 94 vs 170,
-  // 64x8192x8191: 120 vs 172) and, on one split, for one or three row blocks
-  // (16x4096x50257: 249 vs 290 us, 48x4096x50257: 362 vs 495) but not two or
-  // four (32x4096x50257: 322 vs 296 us, 64x4096x50257: 531 vs 507). Below 8
-  // MiB of W the layer is latency-bound and the tile's single launch wins
-  // (4x512x511: 8.4 vs 13.9 us; 16x1024x1023: even); at 16 MiB the small-M
-  // kernel does (8x2048x2047: 15.6 vs 30.6 us). With 4-byte loads: when the
-  // plan splits K and M <= 48 (measured up to three row blocks). A forced
-  // split (edsl_hip_set_gemv_ksplit) or edsl_hip_set_small_m(1) takes the
-  // small-M kernel.
+  // rows of M at ~2.8 TB/s. Measured, small-M kernel vs tile: 16x8192x8191 61
+  // vs 134 us, 16x4096x50257 249 vs 290, 17x4096x50257 259 vs 283,
+  // 32x4096x50257 300 vs 292, 48x4096x50257 362 vs 495, 64x4096x50257 442 vs
+  // 498, 64x2048x50257 254 vs 258, 64x8192x8191 115 vs 166, 33x2048x4097 32
+  // vs 41; short K goes to the tile: 32x1024x32001 57 vs 49. So realigned
+  // rows take the small-M kernel for K >= 2048 (K >= 1024 with one row
+  // block), with at least 8 MiB of W: below that the layer is latency-bound
+  // and the tile's single launch wins (4x512x511: 8.4 vs 13.9 us;
+  // 16x1024x1023: even; 8x2048x2047 at 16 MiB: 15.6 vs 30.6). With 4-byte
+  // loads: when the plan splits K and M <= 48 (measured up to three row
+  // blocks). A forced split (edsl_hip_set_gemv_ksplit) or
+  // edsl_hip_set_small_m(1) takes the small-M kernel.
   const bool gemv_planned =
       M >= 1 && M <= kGemvMaxM && K16 > 0 && plan_gemv(ds, M, N, K16, w_realign, &gemv_cols, &gemv_ks);
   const bool realigned_plan = w_realign && gemv_cols > 32;
@@ -411,7 +412,7 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   }
   if (gemv_planned &&
       ((w_vec && vec_small_m) || g_force_ksplit > 0 || g_force_small_m == 1 ||
-       (realigned_plan && w_large && (gemv_ks > 1 || row_blocks == 1 || row_blocks == 3)) ||
+       (realigned_plan && w_large && (K >= 2048 || (row_blocks == 1 && K >= 1024))) ||
        (!w_vec && !realigned_plan && gemv_ks > 1 && M <= 48))) {
     const bool x_ok = x_vec;
     const bool tail = K16 < K;
