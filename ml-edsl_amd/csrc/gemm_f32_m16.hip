@@ -1,0 +1,288 @@
+// fp32 dense layer / matmul for large shapes: one wave per SIMD, 16x16 MFMA
+// blocks.
+//
+// C[M,N] = epilogue(A[M,K] x B[K,N] (+ bias[N])) -- the same op as the
+// 32x32-block tiles of gemm_f32.hip (reference
+// cpp/src/builders/LinalgBuilder.cpp:106-139, 180-239, 301-339), for shapes
+// the 128x128 tile divides, 16-byte aligned operands.
+//
+// Design (per workgroup, one 128x128 output tile, four waves of 64x64):
+//  * v_mfma_f32_16x16x4_f32: lane l supplies A[row l%16][k-slot l/16] and
+//    B[k-slot l/16][col l%16] and receives rows 4*(l/16)..+3 of column l%16.
+//    A wave tile is 4x4 such blocks: 16 independent accumulators, so the
+//    matrix core never waits on a result and the wave has room to issue its
+//    LDS reads, global loads and LDS stores between MFMAs.
+//  * Lane group g = l/16 owns k = 16j + 4g .. 16j + 4g + 3 of each 16-deep
+//    group j: one ds_read_b128 of its A row per row block gives the four
+//    k-slots of four MFMA steps, and for each of those k one ds_read_b128 of
+//    four consecutive B columns gives the B operand of the four column
+//    blocks. Column block c therefore holds output columns wn0 + 4*(l%16) + c:
+//    each lane ends with four consecutive columns of a row, one 16-byte store.
+//  * One workgroup of four waves per CU (two with 32-deep K steps): each SIMD
+//    runs one or two waves, which keep their MFMAs back to back. LDS is double
+//    buffered; the global loads run PF K steps ahead in a ring of register
+//    sets, and each step's LDS stores are issued right after the first group's
+//    fragment reads, ahead of the MFMAs. Fragments of group j+1 are read while
+//    group j's MFMAs run.
+//  * A rows are stored with the 16-byte chunk index XOR-ed by a row hash so
+//    that the 16 lanes of a ds_read_b128 phase hit distinct banks; B rows are
+//    read 256 contiguous bytes per phase.
+//  * Workgroups map to tiles XCD-aware (common.hpp: tile_coords); C is written
+//    with non-temporal stores.
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <type_traits>
+#include <utility>
+
+namespace edsl {
+namespace {
+
+template <int N>
+using Ic = std::integral_constant<int, N>;
+
+template <typename F, int... S>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, S...>) {
+  (f(Ic<S>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// 16-byte chunk position of chunk q in A row `row` (KCH chunks per row): the
+// 16 rows a ds_read_b128 phase reads at one chunk index land on 16 distinct
+// 16-byte bank groups of the 256-byte bank line.
+template <int KCH>
+__device__ __forceinline__ int a_slot(int row, int q) {
+  if constexpr (KCH >= 16) return q ^ (row % KCH);
+  else return q ^ ((row / (16 / KCH)) % KCH);
+}
+
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int BK = 32;   // K step
+constexpr int PF = 2;    // K steps of global loads in flight
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+
+template <int EPI>
+__global__ void __launch_bounds__(kThreads, 2)
+gemm_f32_m16_kernel(GemmF32Args args) {
+  constexpr int KCH = BK / 4;        // 16-byte chunks of an A row
+  constexpr int G = BK / 16;         // 16-deep groups of a K step
+  constexpr int A_F4 = kBM * KCH;
+  constexpr int B_F4 = BK * kBN / 4;
+  constexpr int A_LD = A_F4 / kThreads;
+  constexpr int B_LD = B_F4 / kThreads;
+  static_assert(BK % 16 == 0 && KCH <= 32, "BK");
+  static_assert(A_F4 % kThreads == 0 && B_F4 % kThreads == 0, "tile loads must divide evenly");
+  static_assert(PF >= 2 && PF <= 4, "global prefetch depth");
+  __shared__ f32x4 sA[2][A_F4];
+  __shared__ float sB[2][BK * kBN];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 4;
+  const int r16 = lane & 15;
+  const int wm0 = (wave >> 1) * 64;
+  const int wn0 = (wave & 1) * 64;
+  int tm, tn;
+  tile_coords(blockIdx.x, args.tiles_m, args.tiles_n, tm, tn);
+  const int m0 = tm * kBM;
+  const int n0 = tn * kBN;
+  const int nk = args.K / BK;
+
+  const float* a_src[A_LD];
+  int a_dst[A_LD];
+#pragma unroll
+  for (int i = 0; i < A_LD; ++i) {
+    const int idx = tid + i * kThreads;
+    const int r = idx / KCH;
+    const int q = idx % KCH;
+    a_src[i] = args.A + (int64_t)(m0 + r) * args.lda + 4 * q;
+    a_dst[i] = r * KCH + a_slot<KCH>(r, q);
+  }
+  const float* b_src[B_LD];
+  int b_dst[B_LD];
+#pragma unroll
+  for (int i = 0; i < B_LD; ++i) {
+    const int idx = tid + i * kThreads;
+    const int r = idx / (kBN / 4);
+    const int c = 4 * (idx % (kBN / 4));
+    b_src[i] = args.B + (int64_t)r * args.ldb + n0 + c;
+    b_dst[i] = r * kBN + c;
+  }
+
+  f32x4 ra[PF][A_LD];
+  f32x4 rb[PF][B_LD];
+  auto load_global = [&](auto set, int kt) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) ra[S][i] = *reinterpret_cast<const f32x4*>(a_src[i] + k0);
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i)
+      rb[S][i] = *reinterpret_cast<const f32x4*>(b_src[i] + (int64_t)k0 * args.ldb);
+  };
+  auto store_lds = [&](auto set, int buf) __attribute__((always_inline)) {
+    constexpr int S = decltype(set)::value;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) sA[buf][a_dst[i]] = ra[S][i];
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) *reinterpret_cast<f32x4*>(&sB[buf][b_dst[i]]) = rb[S][i];
+  };
+
+  // The epilogue's bias values, loaded before the first K step's tile so
+  // that their latency hides behind it.
+  const int col0 = n0 + wn0 + 4 * r16;
+  f32x4 bias4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (epi_has_bias(EPI)) bias4 = *reinterpret_cast<const f32x4*>(args.bias + col0);
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[i][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  struct Frag {
+    f32x4 a[4];  // row block i: A[wm0 + 16i + r16][16j + 4g .. +3]
+    f32x4 b[4];  // step s: B[16j + 4g + s][wn0 + 4*r16 .. +3]
+  };
+  auto read_frag = [&](int buf, int j, Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = wm0 + 16 * i + r16;
+      f.a[i] = sA[buf][row * KCH + a_slot<KCH>(row, 4 * j + g)];
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      f.b[s] = *reinterpret_cast<const f32x4*>(&sB[buf][(16 * j + 4 * g + s) * kBN + wn0 + 4 * r16]);
+  };
+  auto mfmas = [&](const Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[i][s], f.b[s][c], acc[i][c], 0, 0, 0);
+  };
+
+  // Fragment registers: even groups in f0, odd groups in f1 (G is even, so
+  // a step's last group is in f1). The last group's MFMAs of each K step are
+  // issued after the barrier that ends the step, behind the next step's
+  // global loads and first fragment reads, so the matrix core has work while
+  // those are in flight. f1 starts at zero: the first step's deferred MFMAs
+  // add exact zeros.
+  Frag f0, f1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f1.a[i] = f1.b[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int NW = A_LD + B_LD;  // global loads, and LDS stores, of one K step per lane
+  static_assert(G % 2 == 0 && NW % 8 == 0, "schedule");
+
+  // The instruction order inside each group of 64 MFMAs is pinned with
+  // scheduling group barriers: one fragment read per 8 MFMAs (the compiler
+  // otherwise sinks the reads to just before their first use, and every
+  // group starts with an LDS wait), with the global loads or the LDS stores
+  // of the step between them. Same box, 4096^3: 965 us, against 981 us with
+  // each group's reads issued as one burst and 986 us for the 256x256 tile
+  // of gemm_f32.hip; the same reads and stores in the first half of the
+  // group measured 980 us.
+  if (nk > 0) {
+    // PF K steps of global loads in flight, in a ring of PF register sets
+    // (step s lives in set s % PF). While step kt is computed from LDS buffer
+    // kt & 1, step kt + 1 goes to the other buffer and step kt + PF is loaded
+    // into the set step kt left. Loads past the last step repeat the last
+    // step (in bounds, never used), so the loop body has no branch.
+    static_for<PF>([&](auto s) { load_global(s, min((int)decltype(s)::value, nk - 1)); });
+    store_lds(Ic<0>{}, 0);
+    __syncthreads();
+    auto step = [&](auto cur, int kt) __attribute__((always_inline)) {
+      constexpr int C = decltype(cur)::value;
+      const int buf = kt & 1;
+      load_global(Ic<C>{}, min(kt + PF, nk - 1));
+      read_frag(buf, 0, f0);
+      mfmas(f1);  // the previous step's last group
+      static_for<8>([&](auto) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_group_barrier(0x020, NW / 8, 0);  // global loads
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);       // MFMA
+      });
+      __builtin_amdgcn_sched_barrier(0);
+      static_for<G - 1>([&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        if constexpr (j % 2 == 0) {
+          read_frag(buf, j + 1, f1);
+          mfmas(f0);
+        } else {
+          read_frag(buf, j + 1, f0);
+          mfmas(f1);
+        }
+        // The next step's LDS stores go with the first group (LDS buffer
+        // buf ^ 1 was last read before the previous barrier).
+        if constexpr (j == 0) store_lds(Ic<(C + 1) % PF>{}, buf ^ 1);
+        static_for<8>([&](auto) __attribute__((always_inline)) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+          if constexpr (j == 0) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, NW / 8, 0);  // LDS store
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+          } else {
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+          }
+        });
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + PF <= nk; kt += PF) static_for<PF>([&](auto s) { step(s, kt + decltype(s)::value); });
+    static_for<PF>([&](auto s) {
+      if (kt + decltype(s)::value < nk) step(s, kt + decltype(s)::value);
+    });
+    mfmas(f1);
+  }
+
+  // Epilogue: lane holds rows wm0 + 16i + 4g + e and columns col0 .. col0+3.
+  const float alpha = args.alpha;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = m0 + wm0 + 16 * i + 4 * g + e;
+      f32x4 v;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[c] = apply_epilogue_f32<EPI>(acc[i][c][e], bias4[c], alpha);
+      __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(args.C + (int64_t)row * args.ldc + col0));
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_f32_m16(int epi, GemmF32Args a, hipStream_t stream) {
+  if (a.M % kBM || a.N % kBN || a.K <= 0 || a.K % BK || a.tiles_m != a.M / kBM || a.tiles_n != a.N / kBN)
+    return hipErrorInvalidValue;
+  const dim3 grid(a.tiles_m * a.tiles_n);
+  const dim3 block(kThreads);
+#define EDSL_M16_CASE(E)                                                         \
+  case E:                                                                        \
+    hipLaunchKernelGGL((gemm_f32_m16_kernel<E>), grid, block, 0, stream, a);     \
+    break;
+  switch (epi) {
+    EDSL_M16_CASE(epi_code(false, ACT_NONE))
+    EDSL_M16_CASE(epi_code(true, ACT_NONE))
+    EDSL_M16_CASE(epi_code(false, ACT_RELU))
+    EDSL_M16_CASE(epi_code(true, ACT_RELU))
+    EDSL_M16_CASE(epi_code(false, ACT_LEAKY))
+    EDSL_M16_CASE(epi_code(true, ACT_LEAKY))
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef EDSL_M16_CASE
+  return hipGetLastError();
+}
+
+}  // namespace edsl
