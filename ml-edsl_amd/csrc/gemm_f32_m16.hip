@@ -59,25 +59,52 @@ __device__ __forceinline__ int a_slot(int row, int q) {
   else return q ^ ((row / (16 / KCH)) % KCH);
 }
 
-constexpr int kBM = 128;
-constexpr int kBN = 128;
-constexpr int BK = 32;   // K step
 constexpr int PF = 2;    // K steps of global loads in flight
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 
-template <int EPI>
+// Tile layouts, four waves as 2x2 over the tile:
+//  kLarge: 128x128 tile, 64x64 per wave (4x4 MFMA blocks), 32-deep K steps;
+//  kSmall: 64x64 tile, 32x32 per wave (2x2 MFMA blocks), 64-deep K steps,
+//          for shapes whose 128x128 tiles would leave CUs idle (1024^3:
+//          256 tiles of 64x64).
+enum : int { kLarge = 0, kSmall = 1 };
+template <int L> struct Layout;
+template <> struct Layout<kLarge> {
+  static constexpr int BM = 128, BN = 128, BK = 32;
+};
+template <> struct Layout<kSmall> {
+  static constexpr int BM = 64, BN = 64, BK = 64;
+};
+
+template <int N> struct VecT;
+template <> struct VecT<2> { using type = f32x2; };
+template <> struct VecT<4> { using type = f32x4; };
+
+// n items spread over `slices` slices: the count of slice t.
+constexpr int share(int n, int slices, int t) { return n / slices + (t < n % slices ? 1 : 0); }
+
+template <int L, int EPI>
 __global__ void __launch_bounds__(kThreads, 2)
 gemm_f32_m16_kernel(GemmF32Args args) {
+  constexpr int kBM = Layout<L>::BM;
+  constexpr int kBN = Layout<L>::BN;
+  constexpr int BK = Layout<L>::BK;
+  constexpr int RB = kBM / 2 / 16;   // 16-row MFMA blocks of a wave tile
+  constexpr int CB = kBN / 2 / 16;   // 16-column MFMA blocks of a wave tile
   constexpr int KCH = BK / 4;        // 16-byte chunks of an A row
   constexpr int G = BK / 16;         // 16-deep groups of a K step
   constexpr int A_F4 = kBM * KCH;
   constexpr int B_F4 = BK * kBN / 4;
   constexpr int A_LD = A_F4 / kThreads;
   constexpr int B_LD = B_F4 / kThreads;
-  static_assert(BK % 16 == 0 && KCH <= 32, "BK");
+  constexpr int NW = A_LD + B_LD;    // global loads, and LDS stores, of one K step per lane
+  constexpr int NR = RB + 4;         // fragment reads of one group
+  constexpr int NM = 4 * RB * CB;    // MFMAs of one group
+  using bvec = typename VecT<CB>::type;
+  static_assert(BK % 16 == 0 && KCH <= 32 && G % 2 == 0, "BK");
   static_assert(A_F4 % kThreads == 0 && B_F4 % kThreads == 0, "tile loads must divide evenly");
-  static_assert(PF >= 2 && PF <= 4, "global prefetch depth");
+  static_assert(PF == 2, "prefetch depth");
   __shared__ f32x4 sA[2][A_F4];
   __shared__ float sB[2][BK * kBN];
 
@@ -86,8 +113,8 @@ gemm_f32_m16_kernel(GemmF32Args args) {
   const int wave = tid >> 6;
   const int g = lane >> 4;
   const int r16 = lane & 15;
-  const int wm0 = (wave >> 1) * 64;
-  const int wn0 = (wave & 1) * 64;
+  const int wm0 = (wave >> 1) * (kBM / 2);
+  const int wn0 = (wave & 1) * (kBN / 2);
   int tm, tn;
   tile_coords(blockIdx.x, args.tiles_m, args.tiles_n, tm, tn);
   const int m0 = tm * kBM;
@@ -136,60 +163,79 @@ gemm_f32_m16_kernel(GemmF32Args args) {
 
   // The epilogue's bias values, loaded before the first K step's tile so
   // that their latency hides behind it.
-  const int col0 = n0 + wn0 + 4 * r16;
-  f32x4 bias4 = {0.0f, 0.0f, 0.0f, 0.0f};
-  if constexpr (epi_has_bias(EPI)) bias4 = *reinterpret_cast<const f32x4*>(args.bias + col0);
+  const int col0 = n0 + wn0 + CB * r16;
+  bvec biasv = {};
+  if constexpr (epi_has_bias(EPI)) biasv = *reinterpret_cast<const bvec*>(args.bias + col0);
 
-  f32x4 acc[4][4];
+  f32x4 acc[RB][CB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < RB; ++i)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[i][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < CB; ++c) acc[i][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   struct Frag {
-    f32x4 a[4];  // row block i: A[wm0 + 16i + r16][16j + 4g .. +3]
-    f32x4 b[4];  // step s: B[16j + 4g + s][wn0 + 4*r16 .. +3]
+    f32x4 a[RB];  // row block i: A[wm0 + 16i + r16][16j + 4g .. +3]
+    bvec b[4];    // step s: B[16j + 4g + s][wn0 + CB*r16 .. +CB-1]
   };
   auto read_frag = [&](int buf, int j, Frag& f) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < RB; ++i) {
       const int row = wm0 + 16 * i + r16;
       f.a[i] = sA[buf][row * KCH + a_slot<KCH>(row, 4 * j + g)];
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      f.b[s] = *reinterpret_cast<const f32x4*>(&sB[buf][(16 * j + 4 * g + s) * kBN + wn0 + 4 * r16]);
+      f.b[s] = *reinterpret_cast<const bvec*>(&sB[buf][(16 * j + 4 * g + s) * kBN + wn0 + CB * r16]);
   };
   auto mfmas = [&](const Frag& f) __attribute__((always_inline)) {
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < CB; ++c)
           acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[i][s], f.b[s][c], acc[i][c], 0, 0, 0);
   };
 
-  // Fragment registers: even groups in f0, odd groups in f1 (G is even, so
-  // a step's last group is in f1). The last group's MFMAs of each K step are
-  // issued after the barrier that ends the step, behind the next step's
-  // global loads and first fragment reads, so the matrix core has work while
-  // those are in flight. f1 starts at zero: the first step's deferred MFMAs
-  // add exact zeros.
+  // The instruction order inside each group's MFMAs is pinned with
+  // scheduling group barriers: the next group's fragment reads spread over
+  // the MFMAs (the compiler otherwise sinks the reads to just before their
+  // first use, and every group starts with an LDS wait), with the global
+  // loads or the LDS stores of the step between them. Same box, 4096^3:
+  // 965 us, against 981 us with each group's reads issued as one burst and
+  // 986 us for the 256x256 tile of gemm_f32.hip; the same reads and stores
+  // in the first half of the group measured 980 us.
+  constexpr int kSlices = NM < 8 ? NM : 8;
+  auto pin = [&](auto vmem, auto stores) __attribute__((always_inline)) {
+    constexpr int V = decltype(vmem)::value, W = decltype(stores)::value;
+    static_for<kSlices>([&](auto tc) __attribute__((always_inline)) {
+      constexpr int t = decltype(tc)::value;
+      if constexpr (share(V, kSlices, t) > 0) __builtin_amdgcn_sched_group_barrier(0x020, share(V, kSlices, t), 0);
+      if constexpr (share(NR, kSlices, t) > 0) __builtin_amdgcn_sched_group_barrier(0x100, share(NR, kSlices, t), 0);
+      constexpr int m = share(NM, kSlices, t);
+      if constexpr (share(W, kSlices, t) > 0) {
+        __builtin_amdgcn_sched_group_barrier(0x008, m / 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, share(W, kSlices, t), 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, m - m / 2, 0);
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x008, m, 0);
+      }
+    });
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Each K step's last group of MFMAs is issued after the barrier that ends
+  // the step, behind the next step's global loads and first fragment reads,
+  // so the matrix core has work while those are in flight. Groups alternate
+  // between the fragment sets f0 and f1 (G is even, so a step's last group
+  // is in f1); f1 starts at zero, so the first step's deferred MFMAs add
+  // exact zeros.
   Frag f0, f1;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) f1.a[i] = f1.b[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  constexpr int NW = A_LD + B_LD;  // global loads, and LDS stores, of one K step per lane
-  static_assert(G % 2 == 0 && NW % 8 == 0, "schedule");
+  for (int i = 0; i < RB; ++i) f1.a[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) f1.b[s] = bvec{};
 
-  // The instruction order inside each group of 64 MFMAs is pinned with
-  // scheduling group barriers: one fragment read per 8 MFMAs (the compiler
-  // otherwise sinks the reads to just before their first use, and every
-  // group starts with an LDS wait), with the global loads or the LDS stores
-  // of the step between them. Same box, 4096^3: 965 us, against 981 us with
-  // each group's reads issued as one burst and 986 us for the 256x256 tile
-  // of gemm_f32.hip; the same reads and stores in the first half of the
-  // group measured 980 us.
   if (nk > 0) {
     // PF K steps of global loads in flight, in a ring of PF register sets
     // (step s lives in set s % PF). While step kt is computed from LDS buffer
@@ -205,12 +251,7 @@ gemm_f32_m16_kernel(GemmF32Args args) {
       load_global(Ic<C>{}, min(kt + PF, nk - 1));
       read_frag(buf, 0, f0);
       mfmas(f1);  // the previous step's last group
-      static_for<8>([&](auto) __attribute__((always_inline)) {
-        __builtin_amdgcn_sched_group_barrier(0x020, NW / 8, 0);  // global loads
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // LDS read
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);       // MFMA
-      });
-      __builtin_amdgcn_sched_barrier(0);
+      pin(Ic<NW>{}, Ic<0>{});
       static_for<G - 1>([&](auto jc) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
         if constexpr (j % 2 == 0) {
@@ -222,18 +263,12 @@ gemm_f32_m16_kernel(GemmF32Args args) {
         }
         // The next step's LDS stores go with the first group (LDS buffer
         // buf ^ 1 was last read before the previous barrier).
-        if constexpr (j == 0) store_lds(Ic<(C + 1) % PF>{}, buf ^ 1);
-        static_for<8>([&](auto) __attribute__((always_inline)) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-          if constexpr (j == 0) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-            __builtin_amdgcn_sched_group_barrier(0x200, NW / 8, 0);  // LDS store
-            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-          } else {
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-          }
-        });
-        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (j == 0) {
+          store_lds(Ic<(C + 1) % PF>{}, buf ^ 1);
+          pin(Ic<0>{}, Ic<NW>{});
+        } else {
+          pin(Ic<0>{}, Ic<0>{});
+        }
       });
       __syncthreads();
     };
@@ -245,31 +280,34 @@ gemm_f32_m16_kernel(GemmF32Args args) {
     mfmas(f1);
   }
 
-  // Epilogue: lane holds rows wm0 + 16i + 4g + e and columns col0 .. col0+3.
+  // Epilogue: lane holds rows wm0 + 16i + 4g + e and columns col0 .. col0+CB-1.
   const float alpha = args.alpha;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < RB; ++i) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = m0 + wm0 + 16 * i + 4 * g + e;
-      f32x4 v;
+      bvec v;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) v[c] = apply_epilogue_f32<EPI>(acc[i][c][e], bias4[c], alpha);
-      __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(args.C + (int64_t)row * args.ldc + col0));
+      for (int c = 0; c < CB; ++c) v[c] = apply_epilogue_f32<EPI>(acc[i][c][e], biasv[c], alpha);
+      __builtin_nontemporal_store(v, reinterpret_cast<bvec*>(args.C + (int64_t)row * args.ldc + col0));
     }
   }
 }
 
 }  // namespace
 
-hipError_t launch_gemm_f32_m16(int epi, GemmF32Args a, hipStream_t stream) {
-  if (a.M % kBM || a.N % kBN || a.K <= 0 || a.K % BK || a.tiles_m != a.M / kBM || a.tiles_n != a.N / kBN)
+namespace {
+template <int L>
+hipError_t launch_layout(int epi, const GemmF32Args& a, hipStream_t stream) {
+  constexpr int BM = Layout<L>::BM, BN = Layout<L>::BN, BK = Layout<L>::BK;
+  if (a.M % BM || a.N % BN || a.K <= 0 || a.K % BK || a.tiles_m != a.M / BM || a.tiles_n != a.N / BN)
     return hipErrorInvalidValue;
   const dim3 grid(a.tiles_m * a.tiles_n);
   const dim3 block(kThreads);
 #define EDSL_M16_CASE(E)                                                         \
   case E:                                                                        \
-    hipLaunchKernelGGL((gemm_f32_m16_kernel<E>), grid, block, 0, stream, a);     \
+    hipLaunchKernelGGL((gemm_f32_m16_kernel<L, E>), grid, block, 0, stream, a);  \
     break;
   switch (epi) {
     EDSL_M16_CASE(epi_code(false, ACT_NONE))
@@ -283,6 +321,11 @@ hipError_t launch_gemm_f32_m16(int epi, GemmF32Args a, hipStream_t stream) {
   }
 #undef EDSL_M16_CASE
   return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_gemm_f32_m16(int small, int epi, GemmF32Args a, hipStream_t stream) {
+  return small ? launch_layout<kSmall>(epi, a, stream) : launch_layout<kLarge>(epi, a, stream);
 }
 
 }  // namespace edsl

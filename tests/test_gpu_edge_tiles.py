@@ -98,7 +98,8 @@ def test_auto_plan_takes_edge_tiles(shape, tile, torch_cuda):
 
 def test_aligned_shapes_keep_their_tiles(torch_cuda):
     """Shapes the tiles divide still take the unguarded configurations."""
-    for (M, K, N), tile in (((1024, 1024, 1024), "f32_64x64x32_w2x2_k2_pf4"),
+    for (M, K, N), tile in (((1024, 1024, 1024), "f32_64x64x64_mfma16"),
+                            ((2048, 2048, 2048), "f32_128x128x32_mfma16"),
                             ((256, 256, 256), "f32_32x32x64_w1x1_k4_pf4")):
         X, W, b = _inputs(M, K, N, 7)
         got, plan = _run(torch_cuda, X, W, b)
