@@ -547,6 +547,7 @@ gemm_f32_kernel(GemmF32Args args) {
 //      2048^3 141 vs 165 us for 2, 4096x512x4096 143 vs 144-150 us for 23
 //  37: its 64x64x64 twin (32x32 per wave): 1024^3 21.6 vs 23.3 us for 24,
 //      4096x4096x512 149 vs 157 us for 22
+//  38-39: edge-tile twins of 36 and 37 (kGuardEdge)
 const GemmF32Config kConfigs[] = {
     {256, 256, 16, 2, 2, kGuardNone, "f32_256x256x16_w2x2"},
     {256, 256, 16, 4, 2, kGuardNone, "f32_256x256x16_w4x2"},
@@ -586,6 +587,8 @@ const GemmF32Config kConfigs[] = {
     {32, 32, 64, 1, 1, kGuardScalar, "f32_32x32x64_w1x1_k4_pf4_anyshape"},
     {128, 128, 32, 2, 2, kGuardNone, "f32_128x128x32_mfma16"},
     {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_mfma16"},
+    {128, 128, 32, 2, 2, kGuardEdge, "f32_128x128x32_mfma16_edge"},
+    {64, 64, 64, 2, 2, kGuardEdge, "f32_64x64x64_mfma16_edge"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -655,8 +658,10 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case 33: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardScalar, 4, 1>(epi, a, stream);
     case 34: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardScalar, 2>(epi, a, stream);
     case 35: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardScalar, 4>(epi, a, stream);
-    case 36: return launch_gemm_f32_m16(0, epi, a, stream);
-    case 37: return launch_gemm_f32_m16(1, epi, a, stream);
+    case 36: return launch_gemm_f32_m16(0, kGuardNone, epi, a, stream);
+    case 37: return launch_gemm_f32_m16(1, kGuardNone, epi, a, stream);
+    case 38: return launch_gemm_f32_m16(0, kGuardEdge, epi, a, stream);
+    case 39: return launch_gemm_f32_m16(1, kGuardEdge, epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -84,9 +84,17 @@ template <> struct VecT<4> { using type = f32x4; };
 // n items spread over `slices` slices: the count of slice t.
 constexpr int share(int n, int slices, int t) { return n / slices + (t < n % slices ? 1 : 0); }
 
-template <int L, int EPI>
+// GUARD: kGuardNone (M, N multiples of the tile, K of BK) or kGuardEdge (partial
+// tiles and a partial last K step; 16-byte aligned rows, N and K multiples of
+// 4). The edge twin clamps the tile's rows past M to row M-1 and its columns
+// past N to N-4 (loop-invariant; those outputs are never stored), runs the
+// whole K steps through the same pipeline, then the partial step once with
+// loads past K skipped and zero, and stores only inside M x N.
+template <int L, int GUARD, int EPI>
 __global__ void __launch_bounds__(kThreads, 2)
 gemm_f32_m16_kernel(GemmF32Args args) {
+  constexpr bool kEdge = GUARD == kGuardEdge;
+  static_assert(GUARD == kGuardNone || GUARD == kGuardEdge, "guard");
   constexpr int kBM = Layout<L>::BM;
   constexpr int kBN = Layout<L>::BN;
   constexpr int BK = Layout<L>::BK;
@@ -128,7 +136,7 @@ gemm_f32_m16_kernel(GemmF32Args args) {
     const int idx = tid + i * kThreads;
     const int r = idx / KCH;
     const int q = idx % KCH;
-    a_src[i] = args.A + (int64_t)(m0 + r) * args.lda + 4 * q;
+    a_src[i] = args.A + (int64_t)(kEdge ? min(m0 + r, args.M - 1) : m0 + r) * args.lda + 4 * q;
     a_dst[i] = r * KCH + a_slot<KCH>(r, q);
   }
   const float* b_src[B_LD];
@@ -138,7 +146,7 @@ gemm_f32_m16_kernel(GemmF32Args args) {
     const int idx = tid + i * kThreads;
     const int r = idx / (kBN / 4);
     const int c = 4 * (idx % (kBN / 4));
-    b_src[i] = args.B + (int64_t)r * args.ldb + n0 + c;
+    b_src[i] = args.B + (int64_t)r * args.ldb + (kEdge ? min(n0 + c, args.N - 4) : n0 + c);
     b_dst[i] = r * kBN + c;
   }
 
@@ -165,7 +173,9 @@ gemm_f32_m16_kernel(GemmF32Args args) {
   // that their latency hides behind it.
   const int col0 = n0 + wn0 + CB * r16;
   bvec biasv = {};
-  if constexpr (epi_has_bias(EPI)) biasv = *reinterpret_cast<const bvec*>(args.bias + col0);
+  if constexpr (epi_has_bias(EPI)) {
+    if (!kEdge || col0 < args.N) biasv = *reinterpret_cast<const bvec*>(args.bias + col0);
+  }
 
   f32x4 acc[RB][CB];
 #pragma unroll
@@ -280,6 +290,34 @@ gemm_f32_m16_kernel(GemmF32Args args) {
     mfmas(f1);
   }
 
+  if constexpr (kEdge) {
+    // The partial last K step, zero past K, through LDS buffer 0 (every
+    // wave's last fragment reads came before the loop's last barrier).
+    const int k0 = nk * BK;
+    if (k0 < args.K) {
+#pragma unroll
+      for (int i = 0; i < A_LD; ++i) {
+        const int q = (tid + i * kThreads) % KCH;
+        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (k0 + 4 * q < args.K) v = *reinterpret_cast<const f32x4*>(a_src[i] + k0);
+        ra[0][i] = v;
+      }
+#pragma unroll
+      for (int i = 0; i < B_LD; ++i) {
+        const int r = (tid + i * kThreads) / (kBN / 4);
+        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (k0 + r < args.K) v = *reinterpret_cast<const f32x4*>(b_src[i] + (int64_t)k0 * args.ldb);
+        rb[0][i] = v;
+      }
+      store_lds(Ic<0>{}, 0);
+      __syncthreads();
+      static_for<G>([&](auto jc) __attribute__((always_inline)) {
+        read_frag(0, decltype(jc)::value, f0);
+        mfmas(f0);
+      });
+    }
+  }
+
   // Epilogue: lane holds rows wm0 + 16i + 4g + e and columns col0 .. col0+CB-1.
   const float alpha = args.alpha;
 #pragma unroll
@@ -290,7 +328,8 @@ gemm_f32_m16_kernel(GemmF32Args args) {
       bvec v;
 #pragma unroll
       for (int c = 0; c < CB; ++c) v[c] = apply_epilogue_f32<EPI>(acc[i][c][e], biasv[c], alpha);
-      __builtin_nontemporal_store(v, reinterpret_cast<bvec*>(args.C + (int64_t)row * args.ldc + col0));
+      if (!kEdge || (row < args.M && col0 < args.N))
+        __builtin_nontemporal_store(v, reinterpret_cast<bvec*>(args.C + (int64_t)row * args.ldc + col0));
     }
   }
 }
@@ -298,16 +337,20 @@ gemm_f32_m16_kernel(GemmF32Args args) {
 }  // namespace
 
 namespace {
-template <int L>
+template <int L, int GUARD>
 hipError_t launch_layout(int epi, const GemmF32Args& a, hipStream_t stream) {
   constexpr int BM = Layout<L>::BM, BN = Layout<L>::BN, BK = Layout<L>::BK;
-  if (a.M % BM || a.N % BN || a.K <= 0 || a.K % BK || a.tiles_m != a.M / BM || a.tiles_n != a.N / BN)
+  if (GUARD == kGuardNone) {
+    if (a.M % BM || a.N % BN || a.K <= 0 || a.K % BK) return hipErrorInvalidValue;
+  } else if (a.M < 1 || a.N < 4 || a.K < 4 || a.N % 4 || a.K % 4) {
     return hipErrorInvalidValue;
+  }
+  if (a.tiles_m != (a.M + BM - 1) / BM || a.tiles_n != (a.N + BN - 1) / BN) return hipErrorInvalidValue;
   const dim3 grid(a.tiles_m * a.tiles_n);
   const dim3 block(kThreads);
-#define EDSL_M16_CASE(E)                                                         \
-  case E:                                                                        \
-    hipLaunchKernelGGL((gemm_f32_m16_kernel<L, E>), grid, block, 0, stream, a);  \
+#define EDSL_M16_CASE(E)                                                                \
+  case E:                                                                               \
+    hipLaunchKernelGGL((gemm_f32_m16_kernel<L, GUARD, E>), grid, block, 0, stream, a);  \
     break;
   switch (epi) {
     EDSL_M16_CASE(epi_code(false, ACT_NONE))
@@ -324,8 +367,11 @@ hipError_t launch_layout(int epi, const GemmF32Args& a, hipStream_t stream) {
 }
 }  // namespace
 
-hipError_t launch_gemm_f32_m16(int small, int epi, GemmF32Args a, hipStream_t stream) {
-  return small ? launch_layout<kSmall>(epi, a, stream) : launch_layout<kLarge>(epi, a, stream);
+hipError_t launch_gemm_f32_m16(int small, int guard, int epi, GemmF32Args a, hipStream_t stream) {
+  if (guard == kGuardEdge)
+    return small ? launch_layout<kSmall, kGuardEdge>(epi, a, stream) : launch_layout<kLarge, kGuardEdge>(epi, a, stream);
+  if (guard != kGuardNone) return hipErrorInvalidValue;
+  return small ? launch_layout<kSmall, kGuardNone>(epi, a, stream) : launch_layout<kLarge, kGuardNone>(epi, a, stream);
 }
 
 }  // namespace edsl

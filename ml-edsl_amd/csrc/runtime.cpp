@@ -499,7 +499,7 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     // of any alignment, K and N of any value), or -1. The any-shape twins
     // keep unaligned layers on the same large tiles (2001^3: 57.8 TFLOP/s on
     // the small guarded tile alone).
-    static const int kOrder[][3] = {{36, -1, -1}, {37, -1, -1}, {23, 26, 31}, {5, -1, -1}, {0, -1, -1}, {6, -1, -1}, {2, 27, 32},
+    static const int kOrder[][3] = {{36, 38, -1}, {37, 39, -1}, {23, 26, 31}, {5, -1, -1}, {0, -1, -1}, {6, -1, -1}, {2, 27, 32},
                                     {24, 28, 33}, {22, 29, 34}, {21, -1, -1}, {14, -1, -1}, {15, -1, -1},
                                     {3, -1, -1}, {25, 30, 35}};
     int best = -1, first_rejected = -1;
@@ -525,6 +525,26 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
       const GemmF32Config& g = gemm_f32_config(c);
       const int64_t tiles = (int64_t)((M + g.bm - 1) / g.bm) * ((N + g.bn - 1) / g.bn);
       if (e[0] == 24 && tiles > ds.cus) continue;
+      if (e[0] == 36 && tiles >= ds.cus) {
+        // The 128x128 tile on 16x16 MFMA blocks against its 64x64 twin: two
+        // workgroups share a CU, so a CU with n tiles runs n/2 pairs (each
+        // pair ~0.94x the time of two tiles alone) and one tile alone when n
+        // is odd; a 64x64 tile takes ~0.27x a 128x128 one. 3000^3: 576 tiles
+        // leave 64 CUs a third tile, 533 us against 470 us on 2209 tiles of
+        // 64x64; 4096^3 and 4000^3 stay on 128x128 (952 vs 1013, 938 vs
+        // 1030 us), and so does 2048^3 (one tile per CU, 141 vs 153 us).
+        int c64 = -1;
+        for (int t : {37, 39})
+          if (c64 < 0 && fits(t)) c64 = t;
+        if (c64 >= 0) {
+          auto cu_time = [&](int64_t n_tiles) {
+            const int64_t n = (n_tiles + ds.cus - 1) / ds.cus;
+            return (double)(n / 2) * 2.0 * 0.94 + (double)(n % 2);
+          };
+          const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
+          if (0.27 * cu_time(tiles64) < cu_time(tiles)) continue;
+        }
+      }
       if (tiles >= ds.cus) {
         // Tiles larger than 64x64 that need more than one round of
         // workgroups are taken only when the last round keeps at least

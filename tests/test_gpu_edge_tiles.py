@@ -81,10 +81,10 @@ def test_every_edge_config_on_odd_shapes(torch_cuda):
 
 
 @pytest.mark.parametrize("shape, tile", [
-    ((1000, 1000, 1000), "f32_64x64x32_w2x2_k2_pf4_edge"),
-    ((4000, 256, 4000), "f32_256x256x16_w4x4_edge"),
-    # 17 x 16 tiles of 256x256 would need two rounds of workgroups
-    ((4097, 256, 4096), "f32_128x128x16_w2x2_edge"),
+    ((1000, 1000, 1000), "f32_64x64x64_mfma16_edge"),
+    ((4000, 256, 4000), "f32_128x128x32_mfma16_edge"),
+    # 33 x 32 tiles of 128x128 would give 32 CUs a fifth tile
+    ((4097, 256, 4096), "f32_64x64x64_mfma16_edge"),
     # K = 1000 leaves a partial last K step on every tile
     ((512, 1000, 512), "f32_32x32x64_w1x1_k4_pf4_edge"),
 ], ids=["1000^3", "4000x256x4000", "4097x256x4096", "512x1000x512"])
@@ -456,3 +456,44 @@ def test_int8_path_odd_shapes_strided_and_out_of_range(torch_cuda):
         torch_cuda.cuda.synchronize()
         assert _native.last_plan().startswith(path)
         assert np.array_equal(tY.cpu().numpy(), _exact_i32(Xc, W, b))
+
+
+# The tiles on 16x16 MFMA blocks (gemm_f32_m16.hip): K steps of 32 (128x128)
+# or 64 (64x64) with loads two steps ahead and each step's last group of MFMAs
+# deferred past its barrier. One, two and three K steps cover the ring's
+# remainder paths and the final deferred group in both parities; the long K
+# and the tall and wide shapes cover many steps and tile orders.
+MFMA16_SHAPES = {
+    "f32_128x128x32_mfma16": [(128, 32, 128), (256, 64, 128), (128, 96, 384), (384, 2048, 256),
+                              (1024, 160, 128), (128, 224, 1024)],
+    "f32_64x64x64_mfma16": [(64, 64, 64), (128, 128, 64), (64, 192, 192), (192, 2048, 128),
+                            (1024, 320, 64), (64, 448, 1024)],
+}
+
+
+@pytest.mark.parametrize("tile", sorted(MFMA16_SHAPES))
+def test_mfma16_tiles_across_k_steps_shapes_and_epilogues(tile, torch_cuda):
+    from mlir_edsl_hip.device import dense_launch, set_f32_config
+    torch = torch_cuda
+    names = _native.f32_config_names()
+    cfg = names.index(tile)
+    acts = [(_native.EPI_BIAS_RELU, "relu", True), (_native.EPI_NONE, "none", False),
+            (_native.EPI_BIAS, "none", True), (_native.EPI_RELU, "relu", False),
+            (_native.EPI_BIAS_LEAKY, "leaky", True), (_native.EPI_LEAKY, "leaky", False)]
+    try:
+        set_f32_config(cfg)
+        for i, (M, K, N) in enumerate(MFMA16_SHAPES[tile]):
+            X, W, b = _inputs(M, K, N, 300 + i)
+            epi, act, has_bias = acts[i % len(acts)]
+            ref = oracle.dense_f32(X, W, b if has_bias else None, act, alpha=0.125)
+            # contiguous, then padded rows with an element offset (16-byte aligned)
+            for pad, off in ((0, 0), (4, 8)):
+                tX, tW = _view(torch, X, pad, off), _view(torch, W, pad, off)
+                tb = torch.from_numpy(b).cuda()
+                tY = _view(torch, np.full((M, N), np.nan, dtype=np.float32), pad, off)
+                dense_launch(tX, tW, tb if has_bias else None, tY, epi, 0.125)
+                torch.cuda.synchronize()
+                assert f"cfg={tile} " in _native.last_plan(), _native.last_plan()
+                assert_f32_parity(tY.cpu().numpy(), ref, K)
+    finally:
+        set_f32_config(-1)
