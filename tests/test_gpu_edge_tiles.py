@@ -497,3 +497,30 @@ def test_mfma16_tiles_across_k_steps_shapes_and_epilogues(tile, torch_cuda):
                 assert_f32_parity(tY.cpu().numpy(), ref, K)
     finally:
         set_f32_config(-1)
+
+
+def test_mfma16_edge_tiles_on_random_shapes(torch_cuda):
+    """The edge twins of the 16x16-block tiles on random sizes (M, N up to
+    2600, K up to 900, multiples of 4, so both partial tiles and a partial
+    last K step occur), contiguous and as padded views with an offset, each
+    forced and by the automatic plan, against the oracle on the full output."""
+    from mlir_edsl_hip.device import set_f32_config
+    torch = torch_cuda
+    names = _native.f32_config_names()
+    forced = [names.index("f32_128x128x32_mfma16_edge"), names.index("f32_64x64x64_mfma16_edge")]
+    rng = np.random.default_rng(77)
+    try:
+        for case in range(12):
+            M, N = (int(v) for v in 4 * rng.integers(1, 651, size=2))
+            K = int(4 * rng.integers(1, 226))
+            X, W, b = _inputs(M, K, N, 400 + case)
+            ref = oracle.dense_f32(X, W, b, "relu")
+            pad, off = ((0, 0), (4, 8), (8, 4))[case % 3]
+            for cfg in forced + [-1]:
+                set_f32_config(cfg)
+                got, plan = _run(torch, X, W, b, pad, off)
+                if cfg >= 0:
+                    assert f"cfg={names[cfg]} " in plan, (plan, (M, K, N))
+                assert_f32_parity(got, ref, K)
+    finally:
+        set_f32_config(-1)
