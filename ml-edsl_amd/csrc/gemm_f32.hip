@@ -548,6 +548,8 @@ gemm_f32_kernel(GemmF32Args args) {
 //  37: its 64x64x64 twin (32x32 per wave): 1024^3 21.6 vs 23.3 us for 24,
 //      4096x4096x512 149 vs 157 us for 22
 //  38-39: edge-tile twins of 36 and 37 (kGuardEdge)
+//  40: any-shape twin of 36 (kGuardScalar); the 64x64 one measured slower
+//      than 34 (1025^3: 54.8 vs 49.0 us) and is not built
 const GemmF32Config kConfigs[] = {
     {256, 256, 16, 2, 2, kGuardNone, "f32_256x256x16_w2x2"},
     {256, 256, 16, 4, 2, kGuardNone, "f32_256x256x16_w4x2"},
@@ -589,6 +591,7 @@ const GemmF32Config kConfigs[] = {
     {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_mfma16"},
     {128, 128, 32, 2, 2, kGuardEdge, "f32_128x128x32_mfma16_edge"},
     {64, 64, 64, 2, 2, kGuardEdge, "f32_64x64x64_mfma16_edge"},
+    {128, 128, 32, 2, 2, kGuardScalar, "f32_128x128x32_mfma16_anyshape"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -662,6 +665,7 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case 37: return launch_gemm_f32_m16(1, kGuardNone, epi, a, stream);
     case 38: return launch_gemm_f32_m16(0, kGuardEdge, epi, a, stream);
     case 39: return launch_gemm_f32_m16(1, kGuardEdge, epi, a, stream);
+    case 40: return launch_gemm_f32_m16(0, kGuardScalar, epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

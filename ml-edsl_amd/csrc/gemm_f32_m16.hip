@@ -84,17 +84,22 @@ template <> struct VecT<4> { using type = f32x4; };
 // n items spread over `slices` slices: the count of slice t.
 constexpr int share(int n, int slices, int t) { return n / slices + (t < n % slices ? 1 : 0); }
 
-// GUARD: kGuardNone (M, N multiples of the tile, K of BK) or kGuardEdge (partial
+// GUARD: kGuardNone (M, N multiples of the tile, K of BK), kGuardEdge (partial
 // tiles and a partial last K step; 16-byte aligned rows, N and K multiples of
-// 4). The edge twin clamps the tile's rows past M to row M-1 and its columns
-// past N to N-4 (loop-invariant; those outputs are never stored), runs the
-// whole K steps through the same pipeline, then the partial step once with
-// loads past K skipped and zero, and stores only inside M x N.
+// 4) or kGuardScalar (any shape and alignment). The edge twin clamps the
+// tile's rows past M to row M-1 and its columns past N to N-4
+// (loop-invariant; those outputs are never stored), runs the whole K steps
+// through the same pipeline, then the partial step once with loads past K
+// skipped and zero, and stores only inside M x N. The any-shape twin does the
+// same with 4-byte loads and stores: a 16-byte chunk of an A row is four
+// loads at one address with immediate offsets, B columns past N read column
+// N-1, and the partial step zeroes each element past K.
 template <int L, int GUARD, int EPI>
 __global__ void __launch_bounds__(kThreads, 2)
 gemm_f32_m16_kernel(GemmF32Args args) {
-  constexpr bool kEdge = GUARD == kGuardEdge;
-  static_assert(GUARD == kGuardNone || GUARD == kGuardEdge, "guard");
+  constexpr bool kScalar = GUARD == kGuardScalar;
+  constexpr bool kEdge = GUARD == kGuardEdge || kScalar;  // partial tiles and K step
+  static_assert(GUARD == kGuardNone || GUARD == kGuardEdge || kScalar, "guard");
   constexpr int kBM = Layout<L>::BM;
   constexpr int kBN = Layout<L>::BN;
   constexpr int BK = Layout<L>::BK;
@@ -141,25 +146,44 @@ gemm_f32_m16_kernel(GemmF32Args args) {
   }
   const float* b_src[B_LD];
   int b_dst[B_LD];
+  // A lane's B chunks all start at the same column (kThreads is a multiple of
+  // the kBN/4 lanes that cover a row).
+  static_assert(kThreads % (kBN / 4) == 0, "B chunk columns");
+  const int b_col = n0 + 4 * (tid % (kBN / 4));
 #pragma unroll
   for (int i = 0; i < B_LD; ++i) {
     const int idx = tid + i * kThreads;
     const int r = idx / (kBN / 4);
     const int c = 4 * (idx % (kBN / 4));
-    b_src[i] = args.B + (int64_t)r * args.ldb + (kEdge ? min(n0 + c, args.N - 4) : n0 + c);
+    b_src[i] = args.B + (int64_t)r * args.ldb + (kScalar ? 0 : kEdge ? min(n0 + c, args.N - 4) : n0 + c);
     b_dst[i] = r * kBN + c;
   }
+  // Any-shape twin: element e of a lane's B chunk, column min(b_col + e, N-1).
+  auto b_elem = [&](int i, int64_t row_off, int e) -> float {
+    return b_src[i][row_off + min(b_col + e, args.N - 1)];
+  };
 
   f32x4 ra[PF][A_LD];
   f32x4 rb[PF][B_LD];
   auto load_global = [&](auto set, int kt) __attribute__((always_inline)) {
     constexpr int S = decltype(set)::value;
     const int k0 = kt * BK;
+    if constexpr (kScalar) {
 #pragma unroll
-    for (int i = 0; i < A_LD; ++i) ra[S][i] = *reinterpret_cast<const f32x4*>(a_src[i] + k0);
+      for (int i = 0; i < A_LD; ++i)
 #pragma unroll
-    for (int i = 0; i < B_LD; ++i)
-      rb[S][i] = *reinterpret_cast<const f32x4*>(b_src[i] + (int64_t)k0 * args.ldb);
+        for (int e = 0; e < 4; ++e) ra[S][i][e] = a_src[i][k0 + e];
+#pragma unroll
+      for (int i = 0; i < B_LD; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rb[S][i][e] = b_elem(i, (int64_t)k0 * args.ldb, e);
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_LD; ++i) ra[S][i] = *reinterpret_cast<const f32x4*>(a_src[i] + k0);
+#pragma unroll
+      for (int i = 0; i < B_LD; ++i)
+        rb[S][i] = *reinterpret_cast<const f32x4*>(b_src[i] + (int64_t)k0 * args.ldb);
+    }
   };
   auto store_lds = [&](auto set, int buf) __attribute__((always_inline)) {
     constexpr int S = decltype(set)::value;
@@ -174,7 +198,12 @@ gemm_f32_m16_kernel(GemmF32Args args) {
   const int col0 = n0 + wn0 + CB * r16;
   bvec biasv = {};
   if constexpr (epi_has_bias(EPI)) {
-    if (!kEdge || col0 < args.N) biasv = *reinterpret_cast<const bvec*>(args.bias + col0);
+    if constexpr (kScalar) {
+#pragma unroll
+      for (int c = 0; c < CB; ++c) biasv[c] = col0 + c < args.N ? args.bias[col0 + c] : 0.0f;
+    } else if (!kEdge || col0 < args.N) {
+      biasv = *reinterpret_cast<const bvec*>(args.bias + col0);
+    }
   }
 
   f32x4 acc[RB][CB];
@@ -261,7 +290,7 @@ gemm_f32_m16_kernel(GemmF32Args args) {
       load_global(Ic<C>{}, min(kt + PF, nk - 1));
       read_frag(buf, 0, f0);
       mfmas(f1);  // the previous step's last group
-      pin(Ic<NW>{}, Ic<0>{});
+      pin(Ic<(kScalar ? 4 : 1) * NW>{}, Ic<0>{});
       static_for<G - 1>([&](auto jc) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
         if constexpr (j % 2 == 0) {
@@ -299,14 +328,27 @@ gemm_f32_m16_kernel(GemmF32Args args) {
       for (int i = 0; i < A_LD; ++i) {
         const int q = (tid + i * kThreads) % KCH;
         f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (k0 + 4 * q < args.K) v = *reinterpret_cast<const f32x4*>(a_src[i] + k0);
+        if constexpr (kScalar) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (k0 + 4 * q + e < args.K) v[e] = a_src[i][k0 + e];
+        } else if (k0 + 4 * q < args.K) {
+          v = *reinterpret_cast<const f32x4*>(a_src[i] + k0);
+        }
         ra[0][i] = v;
       }
 #pragma unroll
       for (int i = 0; i < B_LD; ++i) {
         const int r = (tid + i * kThreads) / (kBN / 4);
         f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (k0 + r < args.K) v = *reinterpret_cast<const f32x4*>(b_src[i] + (int64_t)k0 * args.ldb);
+        if (k0 + r < args.K) {
+          if constexpr (kScalar) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = b_elem(i, (int64_t)k0 * args.ldb, e);
+          } else {
+            v = *reinterpret_cast<const f32x4*>(b_src[i] + (int64_t)k0 * args.ldb);
+          }
+        }
         rb[0][i] = v;
       }
       store_lds(Ic<0>{}, 0);
@@ -328,8 +370,16 @@ gemm_f32_m16_kernel(GemmF32Args args) {
       bvec v;
 #pragma unroll
       for (int c = 0; c < CB; ++c) v[c] = apply_epilogue_f32<EPI>(acc[i][c][e], biasv[c], alpha);
-      if (!kEdge || (row < args.M && col0 < args.N))
-        __builtin_nontemporal_store(v, reinterpret_cast<bvec*>(args.C + (int64_t)row * args.ldc + col0));
+      float* dst = args.C + (int64_t)row * args.ldc + col0;
+      if constexpr (kScalar) {
+        if (row < args.M) {
+#pragma unroll
+          for (int c = 0; c < CB; ++c)
+            if (col0 + c < args.N) __builtin_nontemporal_store(v[c], dst + c);
+        }
+      } else if (!kEdge || (row < args.M && col0 < args.N)) {
+        __builtin_nontemporal_store(v, reinterpret_cast<bvec*>(dst));
+      }
     }
   }
 }
@@ -342,7 +392,9 @@ hipError_t launch_layout(int epi, const GemmF32Args& a, hipStream_t stream) {
   constexpr int BM = Layout<L>::BM, BN = Layout<L>::BN, BK = Layout<L>::BK;
   if (GUARD == kGuardNone) {
     if (a.M % BM || a.N % BN || a.K <= 0 || a.K % BK) return hipErrorInvalidValue;
-  } else if (a.M < 1 || a.N < 4 || a.K < 4 || a.N % 4 || a.K % 4) {
+  } else if (GUARD == kGuardEdge) {
+    if (a.M < 1 || a.N < 4 || a.K < 4 || a.N % 4 || a.K % 4) return hipErrorInvalidValue;
+  } else if (a.M < 1 || a.N < 1 || a.K < 1) {
     return hipErrorInvalidValue;
   }
   if (a.tiles_m != (a.M + BM - 1) / BM || a.tiles_n != (a.N + BN - 1) / BN) return hipErrorInvalidValue;
@@ -370,6 +422,7 @@ hipError_t launch_layout(int epi, const GemmF32Args& a, hipStream_t stream) {
 hipError_t launch_gemm_f32_m16(int small, int guard, int epi, GemmF32Args a, hipStream_t stream) {
   if (guard == kGuardEdge)
     return small ? launch_layout<kSmall, kGuardEdge>(epi, a, stream) : launch_layout<kLarge, kGuardEdge>(epi, a, stream);
+  if (guard == kGuardScalar) return small ? hipErrorInvalidValue : launch_layout<kLarge, kGuardScalar>(epi, a, stream);
   if (guard != kGuardNone) return hipErrorInvalidValue;
   return small ? launch_layout<kSmall, kGuardNone>(epi, a, stream) : launch_layout<kLarge, kGuardNone>(epi, a, stream);
 }

@@ -479,7 +479,11 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     // first wherever it fits with a workgroup per CU (4096^3: 965 us against 986 us for
     // 256x256x16 with 16 waves on the same box; 2048^3: 141 against 165 us for 128x128x16);
     // then its 64x64x64 twin (1024^3: 21.6 against 23.3 us for 64x64x32 with four K steps of
-    // loads ahead; 4096x512 outputs with K = 4096: 149 against 157 us for 64x64x64 two ahead);
+    // loads ahead; 4096x512 outputs with K = 4096: 149 against 157 us for 64x64x64 two ahead).
+    // Its any-shape (4-byte access) twin comes after the 256x256 tiles: 2001^3 175 us against
+    // 233 us for 128x128x16 and 194 us for 64x64x64, 2048^3 with every row misaligned 174 against
+    // 179 us; at 4001^3 and misaligned 4096^3 the 256x256 any-shape tile stays ahead (1116 and
+    // 1059 us against 1153 and 1151 us).
     // then 256x256x16 with 16 waves at 4096^3 (992 us; 256x256x32 with 8 waves
     // 1012 us, the next in line); at 1024^3 the 64x64x64 tile with two
     // waves per output block splitting K and global loads two K steps ahead (24.9 us) beats
@@ -499,7 +503,7 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     // of any alignment, K and N of any value), or -1. The any-shape twins
     // keep unaligned layers on the same large tiles (2001^3: 57.8 TFLOP/s on
     // the small guarded tile alone).
-    static const int kOrder[][3] = {{36, 38, -1}, {37, 39, -1}, {23, 26, 31}, {5, -1, -1}, {0, -1, -1}, {6, -1, -1}, {2, 27, 32},
+    static const int kOrder[][3] = {{36, 38, -1}, {37, 39, -1}, {23, 26, 31}, {5, -1, -1}, {0, -1, -1}, {6, -1, -1}, {-1, -1, 40}, {2, 27, 32},
                                     {24, 28, 33}, {22, 29, 34}, {21, -1, -1}, {14, -1, -1}, {15, -1, -1},
                                     {3, -1, -1}, {25, 30, 35}};
     int best = -1, first_rejected = -1;

@@ -124,7 +124,7 @@ def test_every_any_shape_config_on_odd_shapes(torch_cuda):
     from mlir_edsl_hip.device import set_f32_config
     names = _native.f32_config_names()
     anyshape = [(c, n) for c, n in enumerate(names) if n.endswith("_anyshape")]
-    assert len(anyshape) == 5
+    assert len(anyshape) == 6
     try:
         for cfg, name in anyshape:
             set_f32_config(cfg)
@@ -140,11 +140,12 @@ def test_every_any_shape_config_on_odd_shapes(torch_cuda):
 
 
 @pytest.mark.parametrize("shape, pad_off, tile", [
-    ((2001, 2001, 2001), (0, 0), "f32_128x128x16_w2x2_anyshape"),
+    ((2001, 2001, 2001), (0, 0), "f32_128x128x32_mfma16_anyshape"),
     ((1025, 1025, 1025), (0, 0), "f32_64x64x64_w2x2_k2_pf2_anyshape"),
     # K = N = 2048 but every row misaligned by an element offset
-    ((2048, 2048, 2048), (0, 1), "f32_128x128x16_w2x2_anyshape"),
-], ids=["2001^3", "1025^3", "2048^3-offset"])
+    ((2048, 2048, 2048), (0, 1), "f32_128x128x32_mfma16_anyshape"),
+    ((4001, 1001, 4001), (0, 0), "f32_256x256x16_w4x4_anyshape"),
+], ids=["2001^3", "1025^3", "2048^3-offset", "4001x1001x4001"])
 def test_auto_plan_takes_any_shape_tiles(shape, pad_off, tile, torch_cuda):
     M, K, N = shape
     X, W, b = _inputs(M, K, N, M + 3 * K + N)
