@@ -60,21 +60,25 @@ __device__ __forceinline__ int a_slot(int row, int q) {
 }
 
 constexpr int PF = 2;    // K steps of global loads in flight
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
 
-// Tile layouts, four waves as 2x2 over the tile:
-//  kLarge: 128x128 tile, 64x64 per wave (4x4 MFMA blocks), 32-deep K steps;
-//  kSmall: 64x64 tile, 32x32 per wave (2x2 MFMA blocks), 64-deep K steps,
+// Tile layouts (WM x WN waves over the tile):
+//  kLarge: 128x128 tile, 2x2 waves of 64x64 (4x4 MFMA blocks), 32-deep K steps,
+//          two workgroups per CU;
+//  kSmall: 64x64 tile, 2x2 waves of 32x32 (2x2 MFMA blocks), 64-deep K steps,
 //          for shapes whose 128x128 tiles would leave CUs idle (1024^3:
-//          256 tiles of 64x64).
-enum : int { kLarge = 0, kSmall = 1 };
+//          256 tiles of 64x64);
+//  kWide:  128x256 tile, 2x4 waves of 64x64, 32-deep K steps, one workgroup
+//          of eight waves per CU (96 KiB of LDS).
+enum : int { kLarge = 0, kSmall = 1, kWide = 2 };
 template <int L> struct Layout;
 template <> struct Layout<kLarge> {
-  static constexpr int BM = 128, BN = 128, BK = 32;
+  static constexpr int BM = 128, BN = 128, BK = 32, WM = 2, WN = 2;
 };
 template <> struct Layout<kSmall> {
-  static constexpr int BM = 64, BN = 64, BK = 64;
+  static constexpr int BM = 64, BN = 64, BK = 64, WM = 2, WN = 2;
+};
+template <> struct Layout<kWide> {
+  static constexpr int BM = 128, BN = 256, BK = 32, WM = 2, WN = 4;
 };
 
 template <int N> struct VecT;
@@ -95,16 +99,17 @@ constexpr int share(int n, int slices, int t) { return n / slices + (t < n % sli
 // loads at one address with immediate offsets, B columns past N read column
 // N-1, and the partial step zeroes each element past K.
 template <int L, int GUARD, int EPI>
-__global__ void __launch_bounds__(kThreads, 2)
+__global__ void __launch_bounds__(Layout<L>::WM * Layout<L>::WN * 64, 2)
 gemm_f32_m16_kernel(GemmF32Args args) {
+  constexpr int kThreads = Layout<L>::WM * Layout<L>::WN * 64;
   constexpr bool kScalar = GUARD == kGuardScalar;
   constexpr bool kEdge = GUARD == kGuardEdge || kScalar;  // partial tiles and K step
   static_assert(GUARD == kGuardNone || GUARD == kGuardEdge || kScalar, "guard");
   constexpr int kBM = Layout<L>::BM;
   constexpr int kBN = Layout<L>::BN;
   constexpr int BK = Layout<L>::BK;
-  constexpr int RB = kBM / 2 / 16;   // 16-row MFMA blocks of a wave tile
-  constexpr int CB = kBN / 2 / 16;   // 16-column MFMA blocks of a wave tile
+  constexpr int RB = kBM / Layout<L>::WM / 16;  // 16-row MFMA blocks of a wave tile
+  constexpr int CB = kBN / Layout<L>::WN / 16;  // 16-column MFMA blocks of a wave tile
   constexpr int KCH = BK / 4;        // 16-byte chunks of an A row
   constexpr int G = BK / 16;         // 16-deep groups of a K step
   constexpr int A_F4 = kBM * KCH;
@@ -126,8 +131,8 @@ gemm_f32_m16_kernel(GemmF32Args args) {
   const int wave = tid >> 6;
   const int g = lane >> 4;
   const int r16 = lane & 15;
-  const int wm0 = (wave >> 1) * (kBM / 2);
-  const int wn0 = (wave & 1) * (kBN / 2);
+  const int wm0 = (wave / Layout<L>::WN) * (kBM / Layout<L>::WM);
+  const int wn0 = (wave % Layout<L>::WN) * (kBN / Layout<L>::WN);
   int tm, tn;
   tile_coords(blockIdx.x, args.tiles_m, args.tiles_n, tm, tn);
   const int m0 = tm * kBM;
@@ -399,7 +404,7 @@ hipError_t launch_layout(int epi, const GemmF32Args& a, hipStream_t stream) {
   }
   if (a.tiles_m != (a.M + BM - 1) / BM || a.tiles_n != (a.N + BN - 1) / BN) return hipErrorInvalidValue;
   const dim3 grid(a.tiles_m * a.tiles_n);
-  const dim3 block(kThreads);
+  const dim3 block(Layout<L>::WM * Layout<L>::WN * 64);
 #define EDSL_M16_CASE(E)                                                                \
   case E:                                                                               \
     hipLaunchKernelGGL((gemm_f32_m16_kernel<L, GUARD, E>), grid, block, 0, stream, a);  \
@@ -419,12 +424,17 @@ hipError_t launch_layout(int epi, const GemmF32Args& a, hipStream_t stream) {
 }
 }  // namespace
 
-hipError_t launch_gemm_f32_m16(int small, int guard, int epi, GemmF32Args a, hipStream_t stream) {
-  if (guard == kGuardEdge)
-    return small ? launch_layout<kSmall, kGuardEdge>(epi, a, stream) : launch_layout<kLarge, kGuardEdge>(epi, a, stream);
-  if (guard == kGuardScalar) return small ? hipErrorInvalidValue : launch_layout<kLarge, kGuardScalar>(epi, a, stream);
-  if (guard != kGuardNone) return hipErrorInvalidValue;
-  return small ? launch_layout<kSmall, kGuardNone>(epi, a, stream) : launch_layout<kLarge, kGuardNone>(epi, a, stream);
+hipError_t launch_gemm_f32_m16(int layout, int guard, int epi, GemmF32Args a, hipStream_t stream) {
+  switch (layout * 4 + guard) {
+    case kLarge * 4 + kGuardNone: return launch_layout<kLarge, kGuardNone>(epi, a, stream);
+    case kLarge * 4 + kGuardEdge: return launch_layout<kLarge, kGuardEdge>(epi, a, stream);
+    case kLarge * 4 + kGuardScalar: return launch_layout<kLarge, kGuardScalar>(epi, a, stream);
+    case kSmall * 4 + kGuardNone: return launch_layout<kSmall, kGuardNone>(epi, a, stream);
+    case kSmall * 4 + kGuardEdge: return launch_layout<kSmall, kGuardEdge>(epi, a, stream);
+    case kWide * 4 + kGuardNone: return launch_layout<kWide, kGuardNone>(epi, a, stream);
+    case kWide * 4 + kGuardEdge: return launch_layout<kWide, kGuardEdge>(epi, a, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace edsl

@@ -530,24 +530,39 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
       const int64_t tiles = (int64_t)((M + g.bm - 1) / g.bm) * ((N + g.bn - 1) / g.bn);
       if (e[0] == 24 && tiles > ds.cus) continue;
       if (e[0] == 36 && tiles >= ds.cus) {
-        // The 128x128 tile on 16x16 MFMA blocks against its 64x64 twin: two
+        // The 128x128 tile on 16x16 MFMA blocks against its 64x64 and 128x256
+        // twins, by how the tiles fall on the CUs. Two 128x128 (or 64x64)
         // workgroups share a CU, so a CU with n tiles runs n/2 pairs (each
         // pair ~0.94x the time of two tiles alone) and one tile alone when n
-        // is odd; a 64x64 tile takes ~0.27x a 128x128 one. 3000^3: 576 tiles
-        // leave 64 CUs a third tile, 533 us against 470 us on 2209 tiles of
-        // 64x64; 4096^3 and 4000^3 stay on 128x128 (952 vs 1013, 938 vs
-        // 1030 us), and so does 2048^3 (one tile per CU, 141 vs 153 us).
-        int c64 = -1;
+        // is odd; a 64x64 tile takes ~0.27x a 128x128 one, and a 128x256
+        // workgroup (eight waves, one per CU) ~0.98x a pair. 3000^3: 576
+        // tiles of 128x128 leave 64 CUs a third tile, 533 us against 470 us
+        // on 2209 tiles of 64x64. 4096^3: 939-940 us on 512 tiles of 128x256
+        // against 952-960 us on 1024 of 128x128 (8192^3 7411 against 7519
+        // us); 6000^3 stays on 128x128 (3157 us against 3437 us for 1128
+        // tiles of 128x256, five rounds of one per CU), and so does 2048^3
+        // (one tile per CU, 141 us against 153 us on 64x64).
+        auto cu_time = [&](int64_t n_tiles) {
+          const int64_t n = (n_tiles + ds.cus - 1) / ds.cus;
+          return (double)(n / 2) * 2.0 * 0.94 + (double)(n % 2);
+        };
+        const double t128 = cu_time(tiles);
+        int c64 = -1, cwide = -1;
         for (int t : {37, 39})
           if (c64 < 0 && fits(t)) c64 = t;
-        if (c64 >= 0) {
-          auto cu_time = [&](int64_t n_tiles) {
-            const int64_t n = (n_tiles + ds.cus - 1) / ds.cus;
-            return (double)(n / 2) * 2.0 * 0.94 + (double)(n % 2);
-          };
-          const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
-          if (0.27 * cu_time(tiles64) < cu_time(tiles)) continue;
+        for (int t : {41, 42})
+          if (cwide < 0 && fits(t)) cwide = t;
+        double t64 = 1e30, twide = 1e30;
+        if (c64 >= 0) t64 = 0.27 * cu_time((int64_t)((M + 63) / 64) * ((N + 63) / 64));
+        if (cwide >= 0) {
+          const int64_t tw = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
+          if (tw >= ds.cus) twide = (double)((tw + ds.cus - 1) / ds.cus) * 2.0 * 0.94 * 0.98;
         }
+        if (twide <= t128 && twide <= t64) {
+          cfg = cwide;
+          break;
+        }
+        if (t64 < t128) continue;
       }
       if (tiles >= ds.cus) {
         // Tiles larger than 64x64 that need more than one round of

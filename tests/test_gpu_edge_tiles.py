@@ -82,7 +82,7 @@ def test_every_edge_config_on_odd_shapes(torch_cuda):
 
 @pytest.mark.parametrize("shape, tile", [
     ((1000, 1000, 1000), "f32_64x64x64_mfma16_edge"),
-    ((4000, 256, 4000), "f32_128x128x32_mfma16_edge"),
+    ((4000, 256, 4000), "f32_128x256x32_mfma16_edge"),
     # 33 x 32 tiles of 128x128 would give 32 CUs a fifth tile
     ((4097, 256, 4096), "f32_64x64x64_mfma16_edge"),
     # K = 1000 leaves a partial last K step on every tile
