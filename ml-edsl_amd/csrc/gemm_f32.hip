@@ -553,6 +553,9 @@ gemm_f32_kernel(GemmF32Args args) {
 //  41-42: 128x256x32 on 16x16 MFMA blocks, 2x4 waves of 64x64, one
 //      workgroup per CU, and its edge twin: 4096^3 938-941 vs 959-962 us for
 //      36, 8192^3 7411 vs 7519 us, 4000^3 922-924 vs 949 us for 38
+//  43-44: 128x128x32 with 2x4 waves of 64x32 (eight waves, one workgroup
+//      per CU) and its edge twin, for exactly one tile per CU: 2048^3 137
+//      vs 139-141 us for 36, 2000^3 137 vs 141 us for 38
 const GemmF32Config kConfigs[] = {
     {256, 256, 16, 2, 2, kGuardNone, "f32_256x256x16_w2x2"},
     {256, 256, 16, 4, 2, kGuardNone, "f32_256x256x16_w4x2"},
@@ -597,6 +600,8 @@ const GemmF32Config kConfigs[] = {
     {128, 128, 32, 2, 2, kGuardScalar, "f32_128x128x32_mfma16_anyshape"},
     {128, 256, 32, 2, 4, kGuardNone, "f32_128x256x32_mfma16"},
     {128, 256, 32, 2, 4, kGuardEdge, "f32_128x256x32_mfma16_edge"},
+    {128, 128, 32, 2, 4, kGuardNone, "f32_128x128x32_mfma16_w8"},
+    {128, 128, 32, 2, 4, kGuardEdge, "f32_128x128x32_mfma16_w8_edge"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -673,6 +678,8 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case 40: return launch_gemm_f32_m16(0, kGuardScalar, epi, a, stream);
     case 41: return launch_gemm_f32_m16(2, kGuardNone, epi, a, stream);
     case 42: return launch_gemm_f32_m16(2, kGuardEdge, epi, a, stream);
+    case 43: return launch_gemm_f32_m16(3, kGuardNone, epi, a, stream);
+    case 44: return launch_gemm_f32_m16(3, kGuardEdge, epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -68,8 +68,10 @@ constexpr int PF = 2;    // K steps of global loads in flight
 //          for shapes whose 128x128 tiles would leave CUs idle (1024^3:
 //          256 tiles of 64x64);
 //  kWide:  128x256 tile, 2x4 waves of 64x64, 32-deep K steps, one workgroup
-//          of eight waves per CU (96 KiB of LDS).
-enum : int { kLarge = 0, kSmall = 1, kWide = 2 };
+//          of eight waves per CU (96 KiB of LDS);
+//  kLarge8: 128x128 tile, 2x4 waves of 64x32, 32-deep K steps, for exactly
+//          one tile per CU (two waves per SIMD).
+enum : int { kLarge = 0, kSmall = 1, kWide = 2, kLarge8 = 3 };
 template <int L> struct Layout;
 template <> struct Layout<kLarge> {
   static constexpr int BM = 128, BN = 128, BK = 32, WM = 2, WN = 2;
@@ -79,6 +81,9 @@ template <> struct Layout<kSmall> {
 };
 template <> struct Layout<kWide> {
   static constexpr int BM = 128, BN = 256, BK = 32, WM = 2, WN = 4;
+};
+template <> struct Layout<kLarge8> {
+  static constexpr int BM = 128, BN = 128, BK = 32, WM = 2, WN = 4;
 };
 
 template <int N> struct VecT;
@@ -433,6 +438,8 @@ hipError_t launch_gemm_f32_m16(int layout, int guard, int epi, GemmF32Args a, hi
     case kSmall * 4 + kGuardEdge: return launch_layout<kSmall, kGuardEdge>(epi, a, stream);
     case kWide * 4 + kGuardNone: return launch_layout<kWide, kGuardNone>(epi, a, stream);
     case kWide * 4 + kGuardEdge: return launch_layout<kWide, kGuardEdge>(epi, a, stream);
+    case kLarge8 * 4 + kGuardNone: return launch_layout<kLarge8, kGuardNone>(epi, a, stream);
+    case kLarge8 * 4 + kGuardEdge: return launch_layout<kLarge8, kGuardEdge>(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

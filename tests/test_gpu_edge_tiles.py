@@ -99,7 +99,9 @@ def test_auto_plan_takes_edge_tiles(shape, tile, torch_cuda):
 def test_aligned_shapes_keep_their_tiles(torch_cuda):
     """Shapes the tiles divide still take the unguarded configurations."""
     for (M, K, N), tile in (((1024, 1024, 1024), "f32_64x64x64_mfma16"),
-                            ((2048, 2048, 2048), "f32_128x128x32_mfma16"),
+                            ((2048, 2048, 2048), "f32_128x128x32_mfma16_w8"),
+                            ((4096, 1024, 4096), "f32_128x256x32_mfma16"),
+                            ((3072, 512, 3072), "f32_64x64x64_mfma16"),
                             ((256, 256, 256), "f32_32x32x64_w1x1_k4_pf4")):
         X, W, b = _inputs(M, K, N, 7)
         got, plan = _run(torch_cuda, X, W, b)
@@ -467,6 +469,8 @@ def test_int8_path_odd_shapes_strided_and_out_of_range(torch_cuda):
 MFMA16_SHAPES = {
     "f32_128x128x32_mfma16": [(128, 32, 128), (256, 64, 128), (128, 96, 384), (384, 2048, 256),
                               (1024, 160, 128), (128, 224, 1024)],
+    "f32_128x128x32_mfma16_w8": [(128, 32, 128), (256, 64, 256), (384, 96, 128), (128, 1056, 384)],
+    "f32_128x256x32_mfma16": [(128, 32, 256), (256, 64, 512), (128, 96, 768), (384, 1056, 256)],
     "f32_64x64x64_mfma16": [(64, 64, 64), (128, 128, 64), (64, 192, 192), (192, 2048, 128),
                             (1024, 320, 64), (64, 448, 1024)],
 }
