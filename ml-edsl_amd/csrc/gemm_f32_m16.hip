@@ -1,29 +1,28 @@
-// fp32 dense layer / matmul for large shapes: one wave per SIMD, 16x16 MFMA
-// blocks.
+// fp32 dense layer / matmul on 16x16 MFMA blocks, one or two waves per SIMD.
 //
 // C[M,N] = epilogue(A[M,K] x B[K,N] (+ bias[N])) -- the same op as the
 // 32x32-block tiles of gemm_f32.hip (reference
-// cpp/src/builders/LinalgBuilder.cpp:106-139, 180-239, 301-339), for shapes
-// the 128x128 tile divides, 16-byte aligned operands.
+// cpp/src/builders/LinalgBuilder.cpp:106-139, 180-239, 301-339), for
+// 16-byte aligned operands (edge twins for partial tiles, and an any-shape
+// twin of the 128x128 tile with 4-byte accesses).
 //
-// Design (per workgroup, one 128x128 output tile, four waves of 64x64):
+// Design (per workgroup, one output tile; the layouts are listed below):
 //  * v_mfma_f32_16x16x4_f32: lane l supplies A[row l%16][k-slot l/16] and
 //    B[k-slot l/16][col l%16] and receives rows 4*(l/16)..+3 of column l%16.
-//    A wave tile is 4x4 such blocks: 16 independent accumulators, so the
+//    A 64x64 wave tile is 4x4 such blocks: 16 independent accumulators, so the
 //    matrix core never waits on a result and the wave has room to issue its
 //    LDS reads, global loads and LDS stores between MFMAs.
 //  * Lane group g = l/16 owns k = 16j + 4g .. 16j + 4g + 3 of each 16-deep
 //    group j: one ds_read_b128 of its A row per row block gives the four
-//    k-slots of four MFMA steps, and for each of those k one ds_read_b128 of
-//    four consecutive B columns gives the B operand of the four column
-//    blocks. Column block c therefore holds output columns wn0 + 4*(l%16) + c:
-//    each lane ends with four consecutive columns of a row, one 16-byte store.
-//  * One workgroup of four waves per CU (two with 32-deep K steps): each SIMD
-//    runs one or two waves, which keep their MFMAs back to back. LDS is double
-//    buffered; the global loads run PF K steps ahead in a ring of register
-//    sets, and each step's LDS stores are issued right after the first group's
-//    fragment reads, ahead of the MFMAs. Fragments of group j+1 are read while
-//    group j's MFMAs run.
+//    k-slots of four MFMA steps, and for each of those k one ds_read_b128 (or
+//    b64) of CB consecutive B columns gives the B operand of the CB column
+//    blocks. Column block c therefore holds output columns wn0 + CB*(l%16) + c:
+//    each lane ends with CB consecutive columns of a row, one vector store.
+//  * LDS is double buffered; the global loads run PF K steps ahead in a ring
+//    of register sets; each step's last group of MFMAs is issued after the
+//    barrier that ends the step, behind the next step's loads and first
+//    fragment reads; scheduling group barriers spread each group's fragment
+//    reads, the global loads and the LDS stores over the MFMAs.
 //  * A rows are stored with the 16-byte chunk index XOR-ed by a row hash so
 //    that the 16 lanes of a ds_read_b128 phase hit distinct banks; B rows are
 //    read 256 contiguous bytes per phase.
