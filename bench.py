@@ -71,6 +71,7 @@ SECONDARY_PLAN = {"c4": (200, 20, 3), "c5": (200, 20, 10), "c2": (100, 20, 1), "
 ROTATE_X = {"c5"}           # workloads whose X is rotated together with W
 RESIDENT_TOO = {"c5"}       # also measured without rotation (inputs cache-resident)
 UNFUSED_TOO = {"c2", "c3"}  # also timed as the reference's unfused three-launch sequence
+LIBRARY_TOO = {"c2", "c3"}  # the vendor library's fp32 GEMM on the same operands, for reference
 
 
 def log(msg: str) -> None:
@@ -196,6 +197,31 @@ def measure(p: Prepared, steps: int, warmup: int, rotate: int | None = None, unf
         "rotate_w": rotate,
         "rotate_x": nx,
     }
+
+
+def measure_library(p: Prepared, steps: int, warmup: int) -> float:
+    """Device ms per launch of torch.mm (hipBLASLt) on the workload's own device
+    operands, no bias or activation, timed like kernel_ms_mean (launches
+    queued behind a spin kernel). A reference point beside the fused kernel;
+    nothing of the product path runs through it."""
+    import torch
+    X, W, Y = p.Xs[0], p.Ws[0], p.Y
+    for _ in range(warmup):
+        torch.mm(X, W, out=Y)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        torch.mm(X, W, out=Y)
+    enqueue_s = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(sleep_cycles_per_s() * (enqueue_s * 1.5 + 2e-4)))
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(steps):
+        torch.mm(X, W, out=Y)
+    ev[1].record()
+    torch.cuda.synchronize()
+    return ev[0].elapsed_time(ev[1]) / steps
 
 
 def step_value(wname: str, step_s: float) -> float:
@@ -491,6 +517,15 @@ def main() -> int:
                 "what": "fill + GEMM without epilogue + separate bias/ReLU kernel: the reference GPU "
                         "lowering's three launches (reference cpp/src/MLIRLowering.cpp:495-518), on this "
                         "library's kernels"}
+        if n in LIBRARY_TOO and p.w.dtype == "f32":
+            steps = args.steps if n == head_name else SECONDARY_PLAN[n][0]
+            lib_ms = measure_library(p, steps, SECONDARY_PLAN[n][1])
+            r["vendor_library"] = {
+                "kernel_ms_mean": round(lib_ms, 5),
+                "tflops": round(p.w.flops / (lib_ms * 1e-3) / 1e12, 2),
+                "fused_kernel_vs_library": round(lib_ms / r["kernel_ms_mean"], 3),
+                "what": "torch.mm (hipBLASLt) on the same device operands, no bias or ReLU, timed like "
+                        "kernel_ms_mean; a reference point, not part of the product path"}
         log(f"[bench] {n} done: {val:.2f} {UNITS[n]}, kernel {r['kernel_ms_mean'] * 1e3:.1f} us, region "
             f"{r['region_ms_per_step'] * 1e3:.1f} us/step [{r['plan']}]")
         results[n] = r
@@ -559,7 +594,7 @@ def main() -> int:
         "cpu_baseline": cpu.get(head_name),
         "secondary": secondary,
     }
-    for k in ("unfused_reference_sequence", "inputs_cache_resident"):
+    for k in ("unfused_reference_sequence", "inputs_cache_resident", "vendor_library"):
         if k in head:
             line[k] = head[k]
     if head_name in host:
