@@ -6,7 +6,8 @@ views, the shapes the edge tiles and padded int8 tiles serve), a dtype, a
 pattern, host or device operands, and for device operands a padded row stride
 and an element offset (a third set: small M with X misaligned on its own and K
 often not a multiple of 16; a fourth: small M with W and Y misaligned on their
-own, N often not a multiple of 4), then compares the HIP result with the
+own, N often not a multiple of 4; a fifth: sizes 2048..4096, aligned or
+not), then compares the HIP result with the
 oracle: i32 bit-exact (int8-range values take the int8 MFMA path, wider ones
 the exact i32 fallback), f32 within relative Frobenius 1e-5 and max|delta| <=
 1e-4*sqrt(K).
@@ -88,6 +89,21 @@ def test_random_case(seed, torch_cuda):
 @pytest.mark.parametrize("seed", range(1000, 1040))
 def test_random_edge_case(seed, torch_cuda):
     _check_case(seed, _case(seed, _EDGE_DIMS, pads=(0, 4, 8), offs=(0, 4), k_zero=False), torch_cuda)
+
+
+# Layers of at least one 128x128 tile per CU, some 16-byte aligned, some not
+# (odd pads and offsets). These seeds reach the 16x16-block tiles (64x64 edge,
+# eight-wave 128x128 and the 128x128 any-shape twin), the 256x256 and 64x64
+# any-shape tiles, the host pipeline's row chunks, and the padded int8 tiles
+# with some tiles out of int8 range; the 128x256 and four-wave 128x128
+# layouts are checked on fixed shapes in test_gpu_edge_tiles.py.
+_LARGE_DIMS = [2048, 2052, 2100, 2176, 2500, 3000, 3072, 4000, 4096]
+
+
+@pytest.mark.parametrize("seed", range(4000, 4016))
+def test_random_large_case(seed, torch_cuda):
+    _check_case(seed, _case(seed, _LARGE_DIMS, pads=(0, 0, 4, 1, 3), offs=(0, 0, 4, 1), k_zero=False),
+                torch_cuda)
 
 
 def _check_case(seed, case, torch):
