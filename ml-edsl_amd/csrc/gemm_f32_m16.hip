@@ -276,13 +276,8 @@ gemm_f32_m16_kernel(GemmF32Args args) {
   // the step, behind the next step's global loads and first fragment reads,
   // so the matrix core has work while those are in flight. Groups alternate
   // between the fragment sets f0 and f1 (G is even, so a step's last group
-  // is in f1); f1 starts at zero, so the first step's deferred MFMAs add
-  // exact zeros.
+  // is in f1). The first step is peeled: it has no earlier group to finish.
   Frag f0, f1;
-#pragma unroll
-  for (int i = 0; i < RB; ++i) f1.a[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int s = 0; s < 4; ++s) f1.b[s] = bvec{};
 
   if (nk > 0) {
     // PF K steps of global loads in flight, in a ring of PF register sets
@@ -293,12 +288,12 @@ gemm_f32_m16_kernel(GemmF32Args args) {
     static_for<PF>([&](auto s) { load_global(s, min((int)decltype(s)::value, nk - 1)); });
     store_lds(Ic<0>{}, 0);
     __syncthreads();
-    auto step = [&](auto cur, int kt) __attribute__((always_inline)) {
+    auto step = [&](auto cur, int kt, auto first) __attribute__((always_inline)) {
       constexpr int C = decltype(cur)::value;
       const int buf = kt & 1;
       load_global(Ic<C>{}, min(kt + PF, nk - 1));
       read_frag(buf, 0, f0);
-      mfmas(f1);  // the previous step's last group
+      if constexpr (!decltype(first)::value) mfmas(f1);  // the previous step's last group
       pin(Ic<(kScalar ? 4 : 1) * NW>{}, Ic<0>{});
       static_for<G - 1>([&](auto jc) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
@@ -320,10 +315,14 @@ gemm_f32_m16_kernel(GemmF32Args args) {
       });
       __syncthreads();
     };
-    int kt = 0;
-    for (; kt + PF <= nk; kt += PF) static_for<PF>([&](auto s) { step(s, kt + decltype(s)::value); });
+    // Step kt uses register set kt % PF; after the peeled step 0 every
+    // block of PF steps starts at kt = 1 (mod PF).
+    step(Ic<0>{}, 0, Ic<1>{});
+    int kt = 1;
+    for (; kt + PF <= nk; kt += PF)
+      static_for<PF>([&](auto s) { step(Ic<(decltype(s)::value + 1) % PF>{}, kt + decltype(s)::value, Ic<0>{}); });
     static_for<PF>([&](auto s) {
-      if (kt + decltype(s)::value < nk) step(s, kt + decltype(s)::value);
+      if (kt + decltype(s)::value < nk) step(Ic<(decltype(s)::value + 1) % PF>{}, kt + decltype(s)::value, Ic<0>{});
     });
     mfmas(f1);
   }
