@@ -308,6 +308,7 @@ def measure_resident_host_path(wname: str, arrays, calls: int) -> dict:
     from mlir_edsl_hip.inputs import WORKLOADS
     w = WORKLOADS[wname]
     comp = MLIRCompiler()
+    comp.set_target("gpu")
     name = f"bench_{wname}_resident"
     comp.compile_function(wire.dense_layer(name, w.M, w.K, w.N, dtype=w.dtype))
     shape = (w.M, w.N)
@@ -336,6 +337,7 @@ def reference_gpu_points() -> list:
     from mlir_edsl_hip import wire
     from mlir_edsl_hip._mlir_backend import MLIRCompiler
     comp = MLIRCompiler()
+    comp.set_target("gpu")
     points = []
     for kind in ("matmul", "dense"):
         for n in (256, 512, 1024):

@@ -95,7 +95,12 @@ int edsl_hip_module_execute_gpu_function(edsl_hip_module *m, const char *name, i
  * until it is bound again. Any other address runs as before (copied in).
  * Binding again replaces the snapshot; unbind (index -1: every parameter of
  * the function), clear() and destroy release it. index is the parameter's
- * position in the FunctionDef (param_index maps a name to it). */
+ * position in the FunctionDef (param_index maps a name to it).
+ * The caller must keep the memory at `data` allocated (and not reuse it for
+ * other values) for as long as the parameter stays bound: calls are matched
+ * by address, so memory freed and handed to a new array of the same shape
+ * would be read from the stale snapshot. The Python facade holds the bound
+ * object until unbind, rebind or clear for this reason. */
 int edsl_hip_module_bind_parameter(edsl_hip_module *m, const char *name, int index, const void *data,
                                    const int64_t *shape, int rank);
 int edsl_hip_module_unbind_parameter(edsl_hip_module *m, const char *name, int index);

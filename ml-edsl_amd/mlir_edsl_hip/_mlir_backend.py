@@ -21,21 +21,25 @@ the rest of the DSL) without a compiler. When the reference's own compiled
 module is importable -- kept under another name, ``mlir_edsl._mlir_backend_ref``
 or ``_mlir_backend_ref`` by default, or the module named by
 ``EDSL_HIP_REFERENCE_BACKEND`` -- this class owns one of its
-``MLIRCompiler`` objects and hands it
-
-* every function compiled while the target is ``"cpu"`` (the front end sets
-  the target before each compile, reference
-  mlir_edsl/functions/compilation.py:67): the caller asked for the CPU JIT;
-* every ``"gpu"`` function that is not a dense-path program.
-
-Dense ``"gpu"`` functions run on the HIP kernels. Later calls are routed by
-function name. Without a reference module, every dense function runs on the
-HIP kernels whatever the target, and anything else raises RuntimeError
-naming what was found.
+``MLIRCompiler`` objects and hands it every function compiled while the
+target is ``"cpu"`` (the front end sets the target before each compile,
+reference mlir_edsl/functions/compilation.py:67): the caller asked for the CPU
+JIT. Routing is by target only. A ``"gpu"`` function always compiles here,
+and one that is not a dense-path program raises RuntimeError with the
+decoder's message: the reference module built for this host has no GPU
+support (its executeGPUFunction throws "GPU support not compiled in",
+reference cpp/src/MLIRCompiler.cpp:456-461), so handing it a GPU program would
+only defer the failure and hide its cause. Later calls are routed by function
+name. Without a reference module, every dense function runs on the HIP
+kernels whatever the target, and anything else raises RuntimeError naming
+what was found.
 
 Device-resident parameters (no reference counterpart): ``bind_parameter``
 keeps a snapshot of a weight or bias in HBM, so calls that pass that same
-array skip its host-to-device copy (include/edsl_hip_program.h).
+array skip its host-to-device copy (include/edsl_hip_program.h). The bound
+object is kept alive until it is unbound, rebound or the module is cleared,
+so its memory cannot be freed and handed to another array while calls still
+match the snapshot by address.
 """
 from __future__ import annotations
 
@@ -169,6 +173,9 @@ class MLIRCompiler:
         self._snapshots: list[tuple[str, str]] = []
         self._failure = ""
         self._injected = False
+        # (function, parameter index) -> the bound object: held so that its
+        # address stays its own while the snapshot is matched by address.
+        self._bound: dict[tuple[str, int], object] = {}
 
     def __del__(self):
         m, self._m = getattr(self, "_m", None), None
@@ -200,12 +207,7 @@ class MLIRCompiler:
                 self._routes.setdefault(n, "hip")
             return
         code, msg = _native.last_error()
-        hip_failure = _text(_L().edsl_hip_module_last_failure, self._m)
-        if self._ref is not None and code == ERR_PROGRAM:
-            # Not a dense-path program: the reference compiler takes it.
-            self._compile_on_reference(data)
-            return
-        self._failure = hip_failure
+        self._failure = _text(_L().edsl_hip_module_last_failure, self._m)
         raise RuntimeError(msg if msg else f"compile_function failed (code {code})")
 
     def _compile_on_reference(self, data: bytes) -> None:
@@ -279,6 +281,7 @@ class MLIRCompiler:
         if self._ref is not None:
             self._ref.clear()
         self._routes.clear()
+        self._bound.clear()
         self._failure = ""
         self._injected = False
         self._snapshots = []
@@ -372,7 +375,10 @@ class MLIRCompiler:
         is taken now: writes to `array` after this call are not seen until
         it is bound again. `array` must be C-contiguous with the parameter's
         compiled shape and element type (float32 or int32) -- a numpy array,
-        or anything exposing ``__array_interface__`` or a GPU torch tensor."""
+        or anything exposing ``__array_interface__`` or a GPU torch tensor.
+        This object keeps a reference to `array` until the parameter is
+        unbound or rebound or the module is cleared, so no other array can be
+        given its address (and be mistaken for it) in the meantime."""
         if self._on_reference(name):
             raise RuntimeError(f"function '{name}' runs on the reference compiler: only HIP-compiled "
                                "functions have device-resident parameters")
@@ -401,6 +407,8 @@ class MLIRCompiler:
         idx = -1 if param is None else self._param_index(name, param)
         if _L().edsl_hip_module_unbind_parameter(self._m, name.encode(), idx) != 0:
             _raise("unbind_parameter")
+        for key in [k for k in self._bound if k[0] == name and idx in (-1, k[1])]:
+            del self._bound[key]
 
     def function_form(self, name: str) -> dict:
         """How a compiled function was matched (no reference counterpart):

@@ -5,10 +5,17 @@ lowering of the dense path (file:line citations in oracle.h). Only the test
 suite, ``__graft_entry__.smoke()`` (as the checker) and the ``cpu_baseline``
 leg of ``bench.py`` may import this package; the product path never does.
 
-Parity pinning of each function is documented in the test modules that check
-it (tests/test_oracle_*.py): reference known answers, exact rational
-brute force of the fma / mulf+addf chains, fp64 error bounds, exact integer
-arithmetic, IEEE special values, and planted-mistake checks.
+Every function is pinned in tests/test_oracle.py: reference known answers,
+exact rational brute force of both f32 rounding chains (fma and mulf+addf),
+fp64 error bounds, exact integer arithmetic, IEEE special values, and
+planted-mistake checks.
+
+f32 rounding chains. The reference sums each output element in ascending k
+from +0.0, either as a vector.fma chain (static 8x8x8 tiles) or as mulf then
+addf (dynamic tiles). Which one it takes for a shape is decided inside MLIR,
+so ``dense_f32`` takes the chain explicitly and ``dense_f32_chains`` returns
+both; the parity tests hold a result to the bar against both, element by
+element.
 """
 from __future__ import annotations
 
@@ -16,13 +23,26 @@ import contextlib
 import ctypes
 import os
 import subprocess
+from typing import NamedTuple
 
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-EPI_NONE, EPI_BIAS, EPI_RELU, EPI_BIAS_RELU, EPI_LEAKY, EPI_BIAS_LEAKY = range(6)
+EPI_NONE, EPI_BIAS, EPI_RELU, EPI_BIAS_RELU, EPI_LEAKY, EPI_BIAS_LEAKY, EPI_IF_RELU, EPI_BIAS_IF_RELU = range(8)
+CHAIN_FMA, CHAIN_MULADD = 0, 1
+_CHAINS = {"fma": CHAIN_FMA, "muladd": CHAIN_MULADD}
+# Activations: "relu" is arith.maximumf(v, 0) (NaN propagates); "if_relu" is
+# the tensor_map body If(v > 0.0, v, 0.0) (cmpf ogt: NaN -> +0, -0 -> +0).
+ACTS = {"none": 0, "relu": 1, "leaky": 2, "if_relu": 3}
+
+
+class F32Chains(NamedTuple):
+    """One f32 result on each rounding chain the reference can take."""
+    fma: np.ndarray
+    muladd: np.ndarray
+
 
 _lib = None
 
@@ -46,15 +66,14 @@ def lib() -> ctypes.CDLL:
         i32p = ctypes.POINTER(ctypes.c_int32)
         i64 = ctypes.c_int64
         L.oracle_dense_f32.argtypes = [f32p, f32p, f32p, f32p, i64, i64, i64, ctypes.c_int,
-                                       ctypes.c_float, ctypes.c_int]
+                                       ctypes.c_float, ctypes.c_int, ctypes.c_int]
         L.oracle_dense_f32.restype = ctypes.c_int
         L.oracle_dense_i32.argtypes = [i32p, i32p, i32p, i32p, i64, i64, i64, ctypes.c_int,
                                        ctypes.c_int]
         L.oracle_dense_i32.restype = ctypes.c_int
-        L.oracle_dense_f32_vec.argtypes = L.oracle_dense_f32.argtypes
+        L.oracle_dense_f32_vec.argtypes = [f32p, f32p, f32p, f32p, i64, i64, i64, ctypes.c_int,
+                                           ctypes.c_float, ctypes.c_int]
         L.oracle_dense_f32_vec.restype = ctypes.c_int
-        L.oracle_static_tiles.argtypes = [i64, i64, i64]
-        L.oracle_static_tiles.restype = ctypes.c_int
         L.oracle_set_mutation.argtypes = [ctypes.c_int]
         L.oracle_set_mutation.restype = None
         _lib = L
@@ -66,11 +85,13 @@ def _ptr(a: np.ndarray, ctype):
 
 
 def epilogue_code(bias: bool, act: str) -> int:
-    return (1 if bias else 0) | ({"none": 0, "relu": 1, "leaky": 2}[act] << 1)
+    return (1 if bias else 0) | (ACTS[act] << 1)
 
 
-def dense_f32(X, W, b=None, act: str = "none", alpha: float = 0.0, threads: int = 0) -> np.ndarray:
-    """Y = act(X @ W (+ b)) with the reference CPU-JIT arithmetic (fp32)."""
+def dense_f32(X, W, b=None, act: str = "none", alpha: float = 0.0, *, chain: str,
+              threads: int = 0) -> np.ndarray:
+    """Y = act(X @ W (+ b)) with the reference CPU-JIT arithmetic (fp32), the
+    sums on the given rounding chain ("fma" or "muladd")."""
     X = np.ascontiguousarray(X, dtype=np.float32)
     W = np.ascontiguousarray(W, dtype=np.float32)
     M, K = X.shape
@@ -81,15 +102,22 @@ def dense_f32(X, W, b=None, act: str = "none", alpha: float = 0.0, threads: int 
     Y = np.empty((M, N), dtype=np.float32)
     rc = lib().oracle_dense_f32(_ptr(X, ctypes.c_float), _ptr(W, ctypes.c_float),
                                 _ptr(bb, ctypes.c_float), _ptr(Y, ctypes.c_float), M, N, K,
-                                epilogue_code(bias, act), alpha, threads)
+                                epilogue_code(bias, act), alpha, _CHAINS[chain], threads)
     if rc != 0:
-        raise ValueError(f"oracle_dense_f32 rejected epilogue {act!r}")
+        raise ValueError(f"oracle_dense_f32 rejected epilogue {act!r} / chain {chain!r}")
     return Y
 
 
+def dense_f32_chains(X, W, b=None, act: str = "none", alpha: float = 0.0,
+                     threads: int = 0) -> F32Chains:
+    """dense_f32 on both rounding chains."""
+    return F32Chains(dense_f32(X, W, b, act, alpha, chain="fma", threads=threads),
+                     dense_f32(X, W, b, act, alpha, chain="muladd", threads=threads))
+
+
 def dense_f32_vec(X, W, b=None, act: str = "none", alpha: float = 0.0, threads: int = 0) -> np.ndarray:
-    """dense_f32 with the reference JIT's 8-wide vector FMAs (bit-identical;
-    static-tile shapes only). For timing the CPU baseline."""
+    """dense_f32 on the fma chain with the reference JIT's 8-wide vector FMAs
+    (bit-identical; M, N, K multiples of 8 only). For timing the CPU baseline."""
     X = np.ascontiguousarray(X, dtype=np.float32)
     W = np.ascontiguousarray(W, dtype=np.float32)
     M, K = X.shape
@@ -103,7 +131,7 @@ def dense_f32_vec(X, W, b=None, act: str = "none", alpha: float = 0.0, threads: 
                                     epilogue_code(bias, act), alpha, threads)
     if rc != 0:
         raise ValueError(f"oracle_dense_f32_vec rejected the call (code {rc}): shape {M}x{K}x{N} "
-                         f"needs static 8x8x8 tiles")
+                         f"needs whole 8x8x8 tiles")
     return Y
 
 
@@ -123,18 +151,6 @@ def dense_i32(X, W, b=None, act: str = "none", threads: int = 0) -> np.ndarray:
     if rc != 0:
         raise ValueError(f"oracle_dense_i32 rejected epilogue {act!r}")
     return Y
-
-
-def matmul_f32(A, B, threads: int = 0) -> np.ndarray:
-    return dense_f32(A, B, None, "none", threads=threads)
-
-
-def matmul_i32(A, B, threads: int = 0) -> np.ndarray:
-    return dense_i32(A, B, None, "none", threads=threads)
-
-
-def static_tiles(M: int, N: int, K: int) -> bool:
-    return bool(lib().oracle_static_tiles(M, N, K))
 
 
 @contextlib.contextmanager

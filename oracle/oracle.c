@@ -26,62 +26,64 @@
  *  3  ReLU as fmaxf (NaN -> 0 instead of NaN)
  *  4  bias subtracted
  *  5  last k term dropped
- *  6  fma path replaced by mulf+addf rounding
+ *  6  fma chain replaced by mulf+addf rounding
  *  7  leaky slope applied to the positive side
  *  8  i32 accumulated in f32
+ *  9  mulf+addf chain contracted to fma
+ * 10  If-ReLU as maximumf (NaN -> NaN instead of +0)
+ * 11  If-ReLU keeps -0 (v >= 0 instead of v > 0)
  */
 static int g_mutation = 0;
 
 void oracle_set_mutation(int mutation) { g_mutation = mutation; }
 
-enum { ACT_NONE = 0, ACT_RELU = 1, ACT_LEAKY = 2 };
-
-int oracle_static_tiles(int64_t M, int64_t N, int64_t K) {
-  /* Outer 64x64 forall tiles have static sizes when the dimension divides by
-   * 64 or fits in one tile (the single-iteration forall folds away); the
-   * inner 8x8x8 tiles are static only when the enclosing size is static and
-   * divisible by 8. LinalgMatmulToContractPass needs all three operands as
-   * static 8x8 (reference cpp/src/MLIRLoweringPasses.cpp:135-143). */
-  const int m_ok = (M <= 64 || M % 64 == 0) && M % 8 == 0;
-  const int n_ok = (N <= 64 || N % 64 == 0) && N % 8 == 0;
-  const int k_ok = K % 8 == 0;
-  return m_ok && n_ok && k_ok;
-}
+enum { ACT_NONE = 0, ACT_RELU = 1, ACT_LEAKY = 2, ACT_IF_RELU = 3 };
 
 static inline float w_at(const float *W, int64_t k, int64_t n, int64_t N, int64_t K) {
   if (g_mutation == 1) return W[n * K + k];
   return W[k * N + n];
 }
 
-/* 8x8x8 micro-kernel: vector.contract lowered to outer products, each a
- * vector.fma over a row of C (reference MLIRLoweringPasses.cpp:242-260). */
-static void micro_fma_8x8x8(const float *A, const float *W, float *C, int64_t m0, int64_t n0,
-                            int64_t k0, int64_t N, int64_t K) {
+/* One 8x8x8 tile of the m, n, k tile loops (reference
+ * MLIRLoweringPasses.cpp:270-319), clipped at the matrix edges to mc x nc x kc.
+ * Each element of the C tile continues its ascending-k chain: on the fma
+ * chain one fused multiply-add per k (vector.contract -> outer products ->
+ * vector.fma, MLIRLoweringPasses.cpp:103-185, 242-260), on the mulf+addf chain
+ * a rounded product then a rounded sum (convert-linalg-to-loops,
+ * MLIRLowering.cpp:410). The k loop is outermost, as in the outer-product
+ * form; every element still sees its own k terms in ascending order. */
+static void micro_8x8x8(const float *A, const float *W, float *C, int64_t m0, int64_t n0,
+                        int64_t k0, int64_t mc, int64_t nc, int64_t kc, int64_t N, int64_t K,
+                        int use_fma) {
   float c[8][8];
   for (int m = 0; m < 8; ++m)
-    for (int n = 0; n < 8; ++n) c[m][n] = C[(m0 + m) * N + n0 + n];
-  for (int k = 0; k < 8; ++k) {
+    for (int n = 0; n < 8; ++n) c[m][n] = (m < mc && n < nc) ? C[(m0 + m) * N + n0 + n] : 0.0f;
+  for (int64_t k = 0; k < kc; ++k) {
     if (g_mutation == 5 && k0 + k == K - 1) continue;
-    for (int m = 0; m < 8; ++m) {
+    float w[8];
+    for (int n = 0; n < 8; ++n) w[n] = n < nc ? w_at(W, k0 + k, n0 + n, N, K) : 0.0f;
+    for (int m = 0; m < mc; ++m) {
       const float a = A[(m0 + m) * K + k0 + k];
-      for (int n = 0; n < 8; ++n) {
-        const float w = w_at(W, k0 + k, n0 + n, N, K);
-        if (g_mutation == 6)
-          c[m][n] = c[m][n] + a * w;
-        else
-          c[m][n] = fmaf(a, w, c[m][n]);
+      if (use_fma) {
+        for (int n = 0; n < 8; ++n) c[m][n] = fmaf(a, w[n], c[m][n]);
+      } else {
+        for (int n = 0; n < 8; ++n) {
+          const float p = a * w[n];
+          c[m][n] = c[m][n] + p;
+        }
       }
     }
   }
-  for (int m = 0; m < 8; ++m)
-    for (int n = 0; n < 8; ++n) C[(m0 + m) * N + n0 + n] = c[m][n];
+  for (int m = 0; m < mc; ++m)
+    for (int n = 0; n < nc; ++n) C[(m0 + m) * N + n0 + n] = c[m][n];
 }
 
 static void matmul_f32(const float *A, const float *W, float *C, int64_t M, int64_t N, int64_t K,
-                       int threads) {
+                       int chain, int threads) {
   /* linalg.fill: runs serially before the parallel matmul. */
   for (int64_t i = 0; i < M * N; ++i) C[i] = 0.0f;
-  const int fma_path = oracle_static_tiles(M, N, K);
+  int use_fma = chain == ORACLE_CHAIN_FMA;
+  if ((use_fma && g_mutation == 6) || (!use_fma && g_mutation == 9)) use_fma = !use_fma;
   const int64_t tiles_m = (M + 63) / 64, tiles_n = (N + 63) / 64;
   const int64_t tiles = tiles_m * tiles_n;
 #pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : omp_get_max_threads())
@@ -91,26 +93,9 @@ static void matmul_f32(const float *A, const float *W, float *C, int64_t M, int6
     const int64_t nh = N - n0 < 64 ? N - n0 : 64;
     for (int64_t mi = 0; mi < mh; mi += 8)
       for (int64_t ni = 0; ni < nh; ni += 8)
-        for (int64_t ki = 0; ki < K; ki += 8) {
-          if (fma_path) {
-            micro_fma_8x8x8(A, W, C, m0 + mi, n0 + ni, ki, N, K);
-            continue;
-          }
-          /* Dynamic tile: convert-linalg-to-loops, scalar mulf then addf. */
-          const int64_t me = mi + 8 < mh ? mi + 8 : mh;
-          const int64_t ne = ni + 8 < nh ? ni + 8 : nh;
-          const int64_t ke = ki + 8 < K ? ki + 8 : K;
-          for (int64_t m = m0 + mi; m < m0 + me; ++m)
-            for (int64_t n = n0 + ni; n < n0 + ne; ++n) {
-              float c = C[m * N + n];
-              for (int64_t k = ki; k < ke; ++k) {
-                if (g_mutation == 5 && k == K - 1) continue;
-                const float p = A[m * K + k] * w_at(W, k, n, N, K);
-                c = c + p;
-              }
-              C[m * N + n] = c;
-            }
-        }
+        for (int64_t ki = 0; ki < K; ki += 8)
+          micro_8x8x8(A, W, C, m0 + mi, n0 + ni, ki, mh - mi < 8 ? mh - mi : 8,
+                      nh - ni < 8 ? nh - ni : 8, K - ki < 8 ? K - ki : 8, N, K, use_fma);
   }
 }
 
@@ -123,12 +108,22 @@ static inline float minimumf0(float x) {
   return (x < 0.0f || x != x || x == 0.0f) ? x : 0.0f; /* NaN -> NaN, -0 -> -0 */
 }
 
+/* If(v > 0.0, v, 0.0) on f32: arith.cmpf ogt (false for NaN) selecting v or
+ * the constant +0.0 (reference LinalgBuilder.cpp:141-178, the comparison
+ * predicate at ArithBuilder.cpp:122-126). NaN -> +0, -0 -> +0. */
+static inline float if_relu0(float x) {
+  if (g_mutation == 10) return maximumf0(x);
+  if (g_mutation == 11) return x >= 0.0f ? x : 0.0f;
+  return x > 0.0f ? x : 0.0f;
+}
+
 int oracle_dense_f32(const float *X, const float *W, const float *b, float *Y, int64_t M,
-                     int64_t N, int64_t K, int epilogue, float alpha, int threads) {
-  if (epilogue < 0 || epilogue > 5) return -1;
+                     int64_t N, int64_t K, int epilogue, float alpha, int chain, int threads) {
+  if (epilogue < 0 || epilogue > 7) return -1;
+  if (chain != ORACLE_CHAIN_FMA && chain != ORACLE_CHAIN_MULADD) return -4;
   const int has_bias = epilogue & 1;
   const int act = (epilogue >> 1) & 3;
-  matmul_f32(X, W, Y, M, N, K, threads);
+  matmul_f32(X, W, Y, M, N, K, chain, threads);
   if (!has_bias && act == ACT_NONE) return 0;
   /* The merged bias + activation generic: one serial elementwise pass. */
   for (int64_t m = 0; m < M; ++m)
@@ -137,6 +132,8 @@ int oracle_dense_f32(const float *X, const float *W, const float *b, float *Y, i
       if (has_bias && g_mutation != 2) y = (g_mutation == 4) ? y - b[n] : y + b[n];
       if (act == ACT_RELU) {
         y = maximumf0(y);
+      } else if (act == ACT_IF_RELU) {
+        y = if_relu0(y);
       } else if (act == ACT_LEAKY) {
         const float pos = maximumf0(y), neg = minimumf0(y);
         if (g_mutation == 7) {
@@ -152,19 +149,20 @@ int oracle_dense_f32(const float *X, const float *W, const float *b, float *Y, i
   return 0;
 }
 
-/* The same lowering, with the 8x8x8 micro-kernel on 8-wide vectors as the
- * reference JIT emits it: each outer product is one vector.fma over a row of
- * the C tile (reference MLIRLoweringPasses.cpp:242-260; x86Vector lowering,
- * MLIRLowering.cpp:422-424), here one 256-bit FMA per row and k. Every C
- * element sees the same fmaf chain in the same k order as micro_fma_8x8x8,
- * so the results are bit-identical; it exists to time the reference's CPU
- * schedule at its own vector width (the benchmark's CPU baseline). Static
- * tiles only (oracle_static_tiles true); no planted-mistake hooks. */
+/* The same lowering on the fma chain, with the 8x8x8 micro-kernel on 8-wide
+ * vectors as the reference JIT emits it: each outer product is one vector.fma
+ * over a row of the C tile (reference MLIRLoweringPasses.cpp:242-260;
+ * x86Vector lowering, MLIRLowering.cpp:422-424), here one 256-bit FMA per row
+ * and k. Every C element sees the same fmaf chain in the same k order as
+ * micro_8x8x8 on the fma chain, so the results are bit-identical; it exists
+ * to time the reference's CPU schedule at its own vector width (the
+ * benchmark's CPU baseline). M, N and K multiples of 8 only (whole 8x8x8
+ * tiles); no planted-mistake hooks. */
 int oracle_dense_f32_vec(const float *X, const float *W, const float *b, float *Y, int64_t M,
                          int64_t N, int64_t K, int epilogue, float alpha, int threads) {
 #if defined(__AVX2__) && defined(__FMA__)
-  if (epilogue < 0 || epilogue > 5) return -1;
-  if (!oracle_static_tiles(M, N, K)) return -2;
+  if (epilogue < 0 || epilogue > 7) return -1;
+  if (M % 8 != 0 || N % 8 != 0 || K % 8 != 0) return -2;
   const int has_bias = epilogue & 1;
   const int act = (epilogue >> 1) & 3;
   for (int64_t i = 0; i < M * N; ++i) Y[i] = 0.0f; /* linalg.fill */
@@ -196,6 +194,8 @@ int oracle_dense_f32_vec(const float *X, const float *W, const float *b, float *
       if (has_bias) y = y + b[n];
       if (act == ACT_RELU) {
         y = (y > 0.0f || y != y) ? y : 0.0f;
+      } else if (act == ACT_IF_RELU) {
+        y = y > 0.0f ? y : 0.0f;
       } else if (act == ACT_LEAKY) {
         const float pos = (y > 0.0f || y != y) ? y : 0.0f;
         const float neg = (y < 0.0f || y != y || y == 0.0f) ? y : 0.0f;

@@ -23,20 +23,29 @@
  *     y = addf(c, b[n]); relu = maximumf(y, 0); leaky = maximumf(y,0) +
  *     alpha * minimumf(y,0);
  *   - i32: arith.muli / arith.addi, two's complement wrapping; ReLU written
- *     tensor_map(v -> If(v > 0, v, 0)) (LinalgBuilder.cpp:141-178).
+ *     tensor_map(v -> If(v > 0, v, 0)) (LinalgBuilder.cpp:141-178);
+ *   - the f32 ReLU written as a tensor_map with an If body
+ *     (LinalgBuilder.cpp:141-178): y = cmpf ogt(y, 0) ? y : 0, so NaN -> +0
+ *     and -0 -> +0, unlike maximumf.
+ *
+ * Rounding chains. Per output element the reference sums in ascending k from
+ * +0.0. A static 8x8x8 tile becomes vector.fma (one rounding per step); a
+ * dynamic tile falls to scalar mulf then addf (two roundings per step). Which
+ * tiles the MLIR vectorizer sees as static is decided inside MLIR, which is
+ * absent here, so the oracle takes the chain as an argument and computes
+ * either one; the parity tests hold a result to the bar against both chains
+ * element by element, which covers the reference whichever chain (or per-tile
+ * mix of chains) it takes.
  *
  * Pinning (tests/test_oracle.py): the reference's known answers, exact
- * rational golden vectors (tests/golden/make_golden.py), the fp64 forward-error
- * bound, exact wrapping i32 arithmetic, IEEE special values, and eight planted
- * mistakes that those checks must catch.
- * Parity unpinned: oracle_static_tiles, i.e. WHICH rounding chain (fma or
- * mulf+addf) the reference JIT takes for a given shape. Deciding it needs the
- * MLIR vectorizer itself, which is absent here. Both chains are pinned bit for
- * bit by the golden vectors and by value through the fp64 bound, and they
- * differ by a few ulp, far inside the fp32 parity tolerance.
+ * rational golden vectors of both chains (tests/golden/make_golden.py), the
+ * fp64 forward-error bound, exact wrapping i32 arithmetic, IEEE special values
+ * through every epilogue, and planted mistakes that those checks must catch.
+ * No function of this library is left unpinned.
  *
  * Operands are contiguous row-major: X[M][K], W[K][N], b[N], Y[M][N].
- * epilogue: bit 0 = add bias; bits 1-2 = activation (0 none, 1 relu, 2 leaky).
+ * epilogue: bit 0 = add bias; bits 1-2 = activation (0 none, 1 relu as
+ * maximumf, 2 leaky, 3 relu as If(v > 0, v, 0); f32 only for 2 and 3).
  */
 #ifndef EDSL_ORACLE_H
 #define EDSL_ORACLE_H
@@ -47,21 +56,23 @@
 extern "C" {
 #endif
 
-/* 1 when every 8x8x8 block of an MxNxK matmul is a static tile in the
- * reference CPU lowering (so every element is an fma chain), 0 when the tiles
- * are dynamic (every element is a mulf+addf chain). */
-int oracle_static_tiles(int64_t M, int64_t N, int64_t K);
+/* Rounding chain of the f32 sums: vector.fma per k step (static tiles), or
+ * mulf then addf per k step (dynamic tiles, convert-linalg-to-loops). */
+#define ORACLE_CHAIN_FMA 0
+#define ORACLE_CHAIN_MULADD 1
 
-/* Returns 0, or -1 on a bad epilogue code. threads <= 0: OpenMP default. */
+/* Returns 0, -1 on a bad epilogue code, -4 on a bad chain. threads <= 0:
+ * OpenMP default. */
 int oracle_dense_f32(const float *X, const float *W, const float *b, float *Y, int64_t M,
-                     int64_t N, int64_t K, int epilogue, float alpha, int threads);
+                     int64_t N, int64_t K, int epilogue, float alpha, int chain, int threads);
 int oracle_dense_i32(const int32_t *X, const int32_t *W, const int32_t *b, int32_t *Y,
                      int64_t M, int64_t N, int64_t K, int epilogue, int threads);
 
-/* oracle_dense_f32 with the 8x8x8 micro-kernel on 8-wide FMA vectors, as the
- * reference JIT emits it (bit-identical results; static-tile shapes only:
- * returns -2 otherwise, -3 when built without AVX2/FMA). For timing the
- * reference's CPU schedule at its own vector width. */
+/* oracle_dense_f32 on the fma chain with the 8x8x8 micro-kernel on 8-wide FMA
+ * vectors, as the reference JIT emits it for static tiles (bit-identical
+ * results; M, N and K multiples of 8 only: returns -2 otherwise, -3 when built
+ * without AVX2/FMA). For timing the reference's CPU schedule at its own vector
+ * width. */
 int oracle_dense_f32_vec(const float *X, const float *W, const float *b, float *Y, int64_t M,
                          int64_t N, int64_t K, int epilogue, float alpha, int threads);
 

@@ -84,6 +84,12 @@ def minimumf0(x: float) -> float:
     return 0.0
 
 
+def if_relu0(x: float) -> float:
+    """If(v > 0.0, v, 0.0): cmpf ogt is false for NaN and for -0, so both
+    give the constant +0."""
+    return x if x > 0 else 0.0
+
+
 def dense_f32_exact(X, W, b, act: str, alpha: float, fma_path: bool) -> np.ndarray:
     """Per element: +0, then an ascending-k chain of fma (fma_path) or of
     mulf-then-addf; then addf bias, then the activation."""
@@ -105,6 +111,8 @@ def dense_f32_exact(X, W, b, act: str, alpha: float, fma_path: bool) -> np.ndarr
                 y = f32_add(y, float(np.float32(b[n])))
             if act == "relu":
                 y = maximumf0(y)
+            elif act == "if_relu":
+                y = if_relu0(y)
             elif act == "leaky":
                 y = f32_add(maximumf0(y), f32_mul(minimumf0(y), alpha32))
             Y[m, n] = y

@@ -4,10 +4,11 @@ Golden vectors for the dense path: seeded small inputs and the outputs
 computed by exact rational arithmetic (tests/exact.py) -- neither the C
 oracle nor the HIP kernels are involved, so these pin both.
 
-Each f32 case follows the reference CPU-JIT arithmetic for its shape: an
-ascending-k fma chain when every 8x8x8 tile is static, else a mulf+addf
-chain (rule restated in oracle/oracle.c: oracle_static_tiles). i32 cases
-include values far outside int8 so that products and sums wrap modulo 2^32.
+Each f32 case holds the reference CPU-JIT result on both rounding chains it
+can take: the ascending-k fma chain (static 8x8x8 tiles) under key
+`Y_<epilogue>_fma` and the mulf+addf chain (dynamic tiles) under
+`Y_<epilogue>_muladd`. i32 cases include values far outside int8 so that
+products and sums wrap modulo 2^32.
 
 Run from the repository root:  python tests/golden/make_golden.py
 """
@@ -41,14 +42,11 @@ I32_CASES = [
     ("i32_wrap_9x13x11", 9, 13, 11, 23, 2**31 - 1),
     ("i32_big_12x20x16", 12, 20, 16, 24, 2**20),
 ]
-ACTS = [("none", False), ("bias", True), ("relu", True), ("leaky", True), ("relu_nobias", False)]
+ACTS = [("none", False), ("bias", True), ("relu", True), ("leaky", True), ("relu_nobias", False),
+        ("if_relu", True), ("if_relu_nobias", False)]
+F32_ACT = {"none": "none", "bias": "none", "relu": "relu", "leaky": "leaky", "relu_nobias": "relu",
+           "if_relu": "if_relu", "if_relu_nobias": "if_relu"}
 ALPHA = 0.01
-
-
-def static_tiles(M, N, K):
-    m_ok = (M <= 64 or M % 64 == 0) and M % 8 == 0
-    n_ok = (N <= 64 or N % 64 == 0) and N % 8 == 0
-    return m_ok and n_ok and K % 8 == 0
 
 
 def main():
@@ -59,15 +57,14 @@ def main():
         X = rng.standard_normal((M, K), dtype=np.float32)
         W = (rng.standard_normal((K, N), dtype=np.float32) / np.float32(np.sqrt(K))).astype(np.float32)
         b = (rng.random(N, dtype=np.float32) * np.float32(0.2) - np.float32(0.1)).astype(np.float32)
-        fma = static_tiles(M, N, K)
         arrays[f"{name}/X"], arrays[f"{name}/W"], arrays[f"{name}/b"] = X, W, b
         for tag, use_b in ACTS:
-            act = {"none": "none", "bias": "none", "relu": "relu", "leaky": "leaky",
-                   "relu_nobias": "relu"}[tag]
-            arrays[f"{name}/Y_{tag}"] = exact.dense_f32_exact(X, W, b if use_b else None, act, ALPHA, fma)
+            for chain, fma in (("fma", True), ("muladd", False)):
+                arrays[f"{name}/Y_{tag}_{chain}"] = exact.dense_f32_exact(
+                    X, W, b if use_b else None, F32_ACT[tag], ALPHA, fma)
         index.append({"name": name, "dtype": "f32", "M": M, "K": K, "N": N, "seed": seed,
-                      "fma_path": fma, "alpha": ALPHA, "epilogues": [t for t, _ in ACTS]})
-        print(name, "fma" if fma else "mulf+addf", flush=True)
+                      "chains": ["fma", "muladd"], "alpha": ALPHA, "epilogues": [t for t, _ in ACTS]})
+        print(name, flush=True)
     for name, M, K, N, seed, vr in I32_CASES:
         rng = np.random.default_rng(seed)
         lo, hi = (-vr, vr) if vr < 2**31 - 1 else (-(2**31), 2**31 - 1)
@@ -77,7 +74,7 @@ def main():
         arrays[f"{name}/X"], arrays[f"{name}/W"], arrays[f"{name}/b"] = X, W, b
         tags = []
         for tag, use_b in ACTS:
-            if tag == "leaky":
+            if tag == "leaky" or tag.startswith("if_relu"):
                 continue
             act = "relu" if tag.startswith("relu") else "none"
             arrays[f"{name}/Y_{tag}"] = exact.dense_i32_exact(X, W, b if use_b else None, act)

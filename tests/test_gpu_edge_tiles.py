@@ -69,7 +69,7 @@ def test_every_edge_config_on_odd_shapes(torch_cuda):
             set_f32_config(cfg)
             for i, (M, K, N) in enumerate(EDGE_SHAPES):
                 X, W, b = _inputs(M, K, N, 100 + i)
-                ref = oracle.dense_f32(X, W, b, "relu")
+                ref = oracle.dense_f32_chains(X, W, b, "relu")
                 # contiguous, then a padded row pitch with an element offset
                 # (both keep 16-byte aligned rows)
                 for pad, off in ((0, 0), (8, 4)):
@@ -93,7 +93,7 @@ def test_auto_plan_takes_edge_tiles(shape, tile, torch_cuda):
     X, W, b = _inputs(M, K, N, M + K + N)
     got, plan = _run(torch_cuda, X, W, b)
     assert f"cfg={tile} " in plan, plan
-    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+    assert_f32_parity(got, oracle.dense_f32_chains(X, W, b, "relu"), K)
 
 
 def test_aligned_shapes_keep_their_tiles(torch_cuda):
@@ -106,7 +106,7 @@ def test_aligned_shapes_keep_their_tiles(torch_cuda):
         X, W, b = _inputs(M, K, N, 7)
         got, plan = _run(torch_cuda, X, W, b)
         assert f"cfg={tile} " in plan, plan
-        assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+        assert_f32_parity(got, oracle.dense_f32_chains(X, W, b, "relu"), K)
 
 
 def test_unaligned_k_takes_an_any_shape_tile(torch_cuda):
@@ -114,7 +114,7 @@ def test_unaligned_k_takes_an_any_shape_tile(torch_cuda):
     X, W, b = _inputs(70, 37, 50, 9)
     got, plan = _run(torch_cuda, X, W, b)
     assert "anyshape" in plan, plan
-    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), 37)
+    assert_f32_parity(got, oracle.dense_f32_chains(X, W, b, "relu"), 37)
 
 
 # K and N of every residue mod 4, M past and below the tiles; with an odd row
@@ -132,7 +132,7 @@ def test_every_any_shape_config_on_odd_shapes(torch_cuda):
             set_f32_config(cfg)
             for i, (M, K, N) in enumerate(ODD_SHAPES):
                 X, W, b = _inputs(M, K, N, 200 + i)
-                ref = oracle.dense_f32(X, W, b, "relu")
+                ref = oracle.dense_f32_chains(X, W, b, "relu")
                 for pad, off in ((0, 0), (3, 1)):
                     got, plan = _run(torch_cuda, X, W, b, pad, off)
                     assert name in plan, (name, plan, (M, K, N))
@@ -153,7 +153,7 @@ def test_auto_plan_takes_any_shape_tiles(shape, pad_off, tile, torch_cuda):
     X, W, b = _inputs(M, K, N, M + 3 * K + N)
     got, plan = _run(torch_cuda, X, W, b, *pad_off)
     assert f"cfg={tile} " in plan, plan
-    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+    assert_f32_parity(got, oracle.dense_f32_chains(X, W, b, "relu"), K)
 
 
 def _run_small_m(torch, X, W, b, pad=0, off=0):
@@ -172,7 +172,7 @@ def test_small_m_uneven_k_slices(M, K, N, torch_cuda):
     X, W, b = _inputs(M, K, N, M * 3 + K)
     got, plan = _run_small_m(torch_cuda, X, W, b)
     assert plan.startswith("gemv_f32"), plan
-    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+    assert_f32_parity(got, oracle.dense_f32_chains(X, W, b, "relu"), K)
 
 
 # Small M with W, Y and bias rows that are not 16-byte aligned or N not a
@@ -190,7 +190,7 @@ def test_small_m_unaligned_w(M, K, N, torch_cuda):
     under a forced split of 2."""
     from mlir_edsl_hip.device import set_gemv_ksplit
     X, W, b = _inputs(M, K, N, M * 7 + K + N)
-    ref = oracle.dense_f32(X, W, b, "relu")
+    ref = oracle.dense_f32_chains(X, W, b, "relu")
     for pad, off in ((0, 0), (3, 1)):
         got, plan = _run(torch_cuda, X, W, b, pad, off)
         assert "+wunaligned" in plan or "+wrealigned" in plan or "32x32x64" in plan, plan
@@ -220,7 +220,7 @@ def test_realigned_w_rows(M, cols, torch_cuda):
     checked = 0
     for N in (5, 61, 62, 63, 64 + 58, 64 + 60, 128 + 1, 128 + 63, 256 + 2, 256 + 62, 511):
         X, W, b = _inputs(M, K, N, M * 1000 + N)
-        ref = oracle.dense_f32(X, W, b, "relu")
+        ref = oracle.dense_f32_chains(X, W, b, "relu")
         for pad, off in ((0, 0), (1, 0), (2, 1), (3, 3), (0, 2)):
             try:
                 set_gemv_cols(cols)
@@ -254,14 +254,14 @@ def test_auto_choice_small_m_or_tile(M, K, N, kernel, torch_cuda):
     X, W, b = _inputs(M, K, N, M + 5 * K + N)
     got, plan = _run(torch_cuda, X, W, b)
     assert plan.startswith(kernel), plan
-    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+    assert_f32_parity(got, oracle.dense_f32_chains(X, W, b, "relu"), K)
 
 
 def test_small_m_forced_splits_on_uneven_k(torch_cuda):
     from mlir_edsl_hip.device import set_gemv_cols, set_gemv_ksplit
     M, K, N = 16, 8000, 1024
     X, W, b = _inputs(M, K, N, 5)
-    ref = oracle.dense_f32(X, W, b, "relu")
+    ref = oracle.dense_f32_chains(X, W, b, "relu")
     try:
         set_gemv_cols(128)
         for ks in (1, 2, 3, 5, 16):
@@ -282,14 +282,14 @@ def test_small_m_partial_column_blocks(M, K, N, torch_cuda):
     X, W, b = _inputs(M, K, N, M + K + N)
     got, plan = _run_small_m(torch_cuda, X, W, b)
     assert plan.startswith("gemv_f32"), plan
-    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+    assert_f32_parity(got, oracle.dense_f32_chains(X, W, b, "relu"), K)
 
 
 def test_small_m_every_width_on_a_partial_block(torch_cuda):
     from mlir_edsl_hip.device import set_gemv_cols, set_gemv_ksplit
     M, K, N = 16, 8000, 1000
     X, W, b = _inputs(M, K, N, 11)
-    ref = oracle.dense_f32(X, W, b, "relu")
+    ref = oracle.dense_f32_chains(X, W, b, "relu")
     try:
         for cols in (32, 64, 128, 256):
             for ks in (1, 3):
@@ -337,7 +337,7 @@ def test_small_m_k_tail_and_unaligned_x(M, K, N, x_pad, x_off, tags, torch_cuda)
         assert t in plan, plan
     if "+ktail" not in tags:
         assert "+ktail" not in plan, plan
-    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), K)
+    assert_f32_parity(got, oracle.dense_f32_chains(X, W, b, "relu"), K)
 
 
 _TAIL_EPIS = {"none": (_native.EPI_NONE, None, "none"), "bias": (_native.EPI_BIAS, "b", "none"),
@@ -358,7 +358,7 @@ def test_small_m_tail_and_unaligned_x_per_row_block_and_epilogue(M, K, x_pad, x_
     got, plan = _run_x_view(torch_cuda, X, W, b, x_pad, x_off, epi=epi, alpha=0.05)
     assert plan.startswith(f"gemv_f32 mb={(M + 15) // 16}"), plan
     assert "+ktail" in plan and "+xunaligned" in plan, plan
-    ref = oracle.dense_f32(X, W, b if use_b else None, act, 0.05)
+    ref = oracle.dense_f32_chains(X, W, b if use_b else None, act, 0.05)
     assert_f32_parity(got, ref, K)
 
 
@@ -376,7 +376,7 @@ def test_single_row_x_with_any_row_stride(K, torch_cuda):
     dense_launch(tX, tW, tb, tY, _native.EPI_BIAS_RELU)
     torch_cuda.cuda.synchronize()
     assert _native.last_plan().startswith("gemv_f32"), _native.last_plan()
-    assert_f32_parity(tY.cpu().numpy(), oracle.dense_f32(X, W, b, "relu"), K)
+    assert_f32_parity(tY.cpu().numpy(), oracle.dense_f32_chains(X, W, b, "relu"), K)
     # Row stride 0 through the C ABI directly (torch reports the view's own
     # stride; a broadcast (1, K) row from expand() has stride 0 on dim 0).
     tY2 = torch_cuda.full((1, N), float("nan"), device="cuda")
@@ -394,7 +394,7 @@ def test_small_m_k_tail_forces_the_reduce(torch_cuda):
     X, W, b = _inputs(16, 4100, 1024, 3)
     got, plan = _run_x_view(torch_cuda, X, W, b, 0, 0, ksplit=1)
     assert "ksplit=2" in plan and "+ktail" in plan, plan
-    assert_f32_parity(got, oracle.dense_f32(X, W, b, "relu"), 4100)
+    assert_f32_parity(got, oracle.dense_f32_chains(X, W, b, "relu"), 4100)
 
 
 # ------------------------------------------------------------ integer path
@@ -490,7 +490,7 @@ def test_mfma16_tiles_across_k_steps_shapes_and_epilogues(tile, torch_cuda):
         for i, (M, K, N) in enumerate(MFMA16_SHAPES[tile]):
             X, W, b = _inputs(M, K, N, 300 + i)
             epi, act, has_bias = acts[i % len(acts)]
-            ref = oracle.dense_f32(X, W, b if has_bias else None, act, alpha=0.125)
+            ref = oracle.dense_f32_chains(X, W, b if has_bias else None, act, alpha=0.125)
             # contiguous, then padded rows with an element offset (16-byte aligned)
             for pad, off in ((0, 0), (4, 8)):
                 tX, tW = _view(torch, X, pad, off), _view(torch, W, pad, off)
@@ -519,7 +519,7 @@ def test_mfma16_edge_tiles_on_random_shapes(torch_cuda):
             M, N = (int(v) for v in 4 * rng.integers(1, 651, size=2))
             K = int(4 * rng.integers(1, 226))
             X, W, b = _inputs(M, K, N, 400 + case)
-            ref = oracle.dense_f32(X, W, b, "relu")
+            ref = oracle.dense_f32_chains(X, W, b, "relu")
             pad, off = ((0, 0), (4, 8), (8, 4))[case % 3]
             for cfg in forced + [-1]:
                 set_f32_config(cfg)

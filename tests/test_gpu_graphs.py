@@ -114,7 +114,7 @@ def test_graph_replay_matches_eager(name, dtype, M, widths, epis, plans):
     act = "relu" if epi in (2, 3) else "none"
     bias = b.cpu().numpy() if epi in (1, 3) else None
     if dtype == "f32":
-        assert_f32_parity(outs[-1].cpu().numpy(), oracle.dense_f32(prev, W.cpu().numpy(), bias, act), W.shape[0])
+        assert_f32_parity(outs[-1].cpu().numpy(), oracle.dense_f32_chains(prev, W.cpu().numpy(), bias, act), W.shape[0])
     else:
         assert np.array_equal(outs[-1].cpu().numpy(), oracle.dense_i32(prev, W.cpu().numpy(), bias, act))
 

@@ -102,7 +102,7 @@ def test_host_staging(dt, M, K, N, xpo, wpo, ypo, lib):
         ref = oracle.dense_i32(np.ascontiguousarray(X), np.ascontiguousarray(W), b, "relu")
         assert np.array_equal(Y, ref), what
     else:
-        ref = oracle.dense_f32(np.ascontiguousarray(X), np.ascontiguousarray(W), b, "relu")
+        ref = oracle.dense_f32_chains(np.ascontiguousarray(X), np.ascontiguousarray(W), b, "relu")
         assert_f32_parity(np.ascontiguousarray(Y), ref, K)
     # nothing outside the output view was written
     assert np.array_equal(Yb[outside], Yb_before[outside]), what
@@ -131,4 +131,4 @@ def test_pipeline_with_device_weights(lib):
     _native.raise_on_error("edsl_hip_dense_relu_f32")
     plan = _native.last_plan()
     assert plan.startswith("host pipeline"), plan
-    assert_f32_parity(Y, oracle.dense_f32(X, W, b, "relu"), K)
+    assert_f32_parity(Y, oracle.dense_f32_chains(X, W, b, "relu"), K)

@@ -42,7 +42,7 @@ def test_tiled_f32_output_beyond_2_31(torch_cuda):
     plan = _native.last_plan()
     assert plan.startswith("gemm_f32"), plan
     rows = _rows(torch, M)
-    ref = oracle.dense_f32(X.index_select(0, rows).cpu().numpy(), W.cpu().numpy(), b.cpu().numpy(), "relu")
+    ref = oracle.dense_f32_chains(X.index_select(0, rows).cpu().numpy(), W.cpu().numpy(), b.cpu().numpy(), "relu")
     assert_f32_parity(Y.index_select(0, rows).cpu().numpy(), ref, K)
     del X, W, b, Y
     torch.cuda.empty_cache()
@@ -88,7 +88,7 @@ def test_small_m_weights_beyond_2_31(torch_cuda):
     assert plan.startswith("gemv_f32"), plan
     cols = torch.from_numpy(np.unique(np.r_[0, 1, 4096, N // 2, N - 129, N - 4, N - 1])).cuda()
     Wc = W.index_select(1, cols).cpu().numpy()
-    ref = oracle.dense_f32(X.cpu().numpy(), Wc, b.index_select(0, cols).cpu().numpy(), "relu")
+    ref = oracle.dense_f32_chains(X.cpu().numpy(), Wc, b.index_select(0, cols).cpu().numpy(), "relu")
     assert_f32_parity(Y.index_select(1, cols).cpu().numpy(), ref, K)
     del X, W, b, Y
     torch.cuda.empty_cache()

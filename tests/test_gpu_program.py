@@ -43,25 +43,35 @@ def _inputs(case, seed, wide=False):
 
 def _reference(form, args):
     """Layer by layer, as the reference lowering computes a chain: each
-    layer's matmul in full, then its bias + activation, then the next."""
-    h = None
-    for L in form["layers"]:
-        X = args[L["x"]] if L["x"] >= 0 else h
-        W = args[L["w"]]
-        b = args[L["b"]] if L["b"] >= 0 else None
-        act = {0: "none", 1: "relu", 2: "leaky"}[L["epilogue"] >> 1]
-        if form["dtype"] == "i32":
-            h = oracle.dense_i32(X, W, b, act)
-        else:
-            h = oracle.dense_f32(X, W, b, act, L["alpha"])
-    return h
+    layer's matmul in full, then its bias + activation, then the next. f32
+    chains are computed once per rounding chain, every layer on that chain."""
+    def run(chain):
+        h = None
+        for L in form["layers"]:
+            X = args[L["x"]] if L["x"] >= 0 else h
+            W = args[L["w"]]
+            b = args[L["b"]] if L["b"] >= 0 else None
+            act = {0: "none", 1: "relu", 2: "leaky", 3: "if_relu"}[L["epilogue"] >> 1]
+            if form["dtype"] == "i32":
+                h = oracle.dense_i32(X, W, b, act)
+            else:
+                h = oracle.dense_f32(X, W, b, act, L["alpha"], chain=chain)
+        return h
+    if form["dtype"] == "i32":
+        return run(None)
+    return oracle.F32Chains(run("fma"), run("muladd"))
+
+
+def _arr(ref):
+    """The array whose shape and dtype the output has."""
+    return ref.fma if isinstance(ref, oracle.F32Chains) else ref
 
 
 def _check(got, ref, K):
-    if ref.dtype == np.int32:
-        assert got.dtype == np.int32 and np.array_equal(got, ref)
-    else:
+    if isinstance(ref, oracle.F32Chains):
         assert_f32_parity(got, ref, K)
+    else:
+        assert got.dtype == np.int32 and np.array_equal(got, ref)
 
 
 def _descriptor_types_and_values(a):
@@ -85,6 +95,7 @@ def torch_cuda():
 def test_reference_program_runs_three_ways(case, torch_cuda):
     torch = torch_cuda
     comp = MLIRCompiler()
+    comp.set_target("gpu")
     comp.compile_function(open(os.path.join(GOLDEN, case["file"]), "rb").read())
     name = case["function"]
     form = comp.function_form(name)
@@ -93,8 +104,9 @@ def test_reference_program_runs_three_ways(case, torch_cuda):
     for seed, wide in ((1, False), (2, True)):
         args = _inputs(case, seed, wide)
         ref = _reference(form, args)
+        like = _arr(ref)
         # 1) host buffers through the function pointer
-        out = np.empty(ref.shape, dtype=ref.dtype)
+        out = np.empty(like.shape, dtype=like.dtype)
         types, vals = [], []
         for a in args + [out]:
             t, v = _descriptor_types_and_values(a)
@@ -105,7 +117,7 @@ def test_reference_program_runs_three_ways(case, torch_cuda):
         _check(out, ref, K)
         # 2) device tensors through the same pointer
         dargs = [torch.from_numpy(a).cuda() for a in args]
-        dout = torch.empty(ref.shape, dtype=dargs[0].dtype, device="cuda")
+        dout = torch.empty(like.shape, dtype=dargs[0].dtype, device="cuda")
         types, vals = [], []
         for a in dargs + [dout]:
             t, v = _descriptor_types_and_values(a)
@@ -117,13 +129,13 @@ def test_reference_program_runs_three_ways(case, torch_cuda):
         _check(dout.cpu().numpy(), ref, K)
         # 3) execute_gpu_function with (pointer, shape) pairs, element size from the dtype
         raw = comp.execute_gpu_function(name, [(a.ctypes.data, list(a.shape)) for a in args],
-                                        list(ref.shape), ref.dtype.itemsize)
-        assert type(raw) is bytes and len(raw) == ref.nbytes  # the reference returns py::bytes
-        _check(np.frombuffer(raw, dtype=ref.dtype).reshape(ref.shape), ref, K)
+                                        list(like.shape), like.dtype.itemsize)
+        assert type(raw) is bytes and len(raw) == like.nbytes  # the reference returns py::bytes
+        _check(np.frombuffer(raw, dtype=like.dtype).reshape(like.shape), ref, K)
         # a second call returns a new object; the first result is unchanged
         first = bytes(raw)
         raw2 = comp.execute_gpu_function(name, [(a.ctypes.data, list(a.shape)) for a in args],
-                                         list(ref.shape), ref.dtype.itemsize)
+                                         list(like.shape), like.dtype.itemsize)
         assert raw2 is not raw and raw == first and raw2 == first
     if "execute_gpu_function" in case:  # the reference front end's call has the same shapes
         call = case["execute_gpu_function"]
@@ -161,11 +173,12 @@ def test_bound_parameters_match_unbound_calls_and_the_oracle(M, K, N, torch_cuda
     same shape is copied in as usual; unbinding goes back to copying."""
     from mlir_edsl_hip import wire
     comp = MLIRCompiler()
+    comp.set_target("gpu")
     name = "dense_bound"
     comp.compile_function(wire.dense_layer(name, M, K, N))
     ptr = comp.get_function_pointer(name)
     X, W, b = _layer_inputs(M, K, N, M + K)
-    ref = oracle.dense_f32(X, W, b, "relu")
+    ref = oracle.dense_f32_chains(X, W, b, "relu")
     plain = np.empty((M, N), np.float32)
     _call_pointer(ptr, (X, W, b), plain)
     assert "resident" not in _native.last_plan()
@@ -194,7 +207,7 @@ def test_bound_parameters_match_unbound_calls_and_the_oracle(M, K, N, torch_cuda
     comp.bind_parameter(name, "W", W)
     rebound = np.empty((M, N), np.float32)
     _call_pointer(ptr, (X, W, b), rebound)
-    ref2 = oracle.dense_f32(X, W2, b, "relu")
+    ref2 = oracle.dense_f32_chains(X, W2, b, "relu")
     _check(rebound, ref2, K)
     assert not np.array_equal(rebound, plain)
 
@@ -203,7 +216,7 @@ def test_bound_parameters_match_unbound_calls_and_the_oracle(M, K, N, torch_cuda
     other = np.empty((M, N), np.float32)
     _call_pointer(ptr, (X, W3, b), other)
     assert _native.last_plan().endswith("[resident: b]"), _native.last_plan()
-    _check(other, oracle.dense_f32(X, W3, b, "relu"), K)
+    _check(other, oracle.dense_f32_chains(X, W3, b, "relu"), K)
 
     comp.unbind_parameter(name)
     again = np.empty((M, N), np.float32)
@@ -219,6 +232,7 @@ def test_bound_parameters_in_a_chain_and_with_device_operands(torch_cuda):
     from mlir_edsl_hip import wire
     torch = torch_cuda
     comp = MLIRCompiler()
+    comp.set_target("gpu")
     name = "chain_bound"
     comp.compile_function(wire.dense_program(name, ("X", 64, 512), [wire.Layer("W1", 256, "b1", "relu"),
                                                                     wire.Layer("W2", 96, "b2", "leaky", 0.1)]))
@@ -242,4 +256,39 @@ def test_bound_parameters_in_a_chain_and_with_device_operands(torch_cuda):
     torch.cuda.synchronize()
     assert "resident" not in _native.last_plan()
     _check(dout.cpu().numpy(), ref, 512)
+    comp.clear()
+
+
+def test_a_freed_bound_array_cannot_lend_its_address(torch_cuda):
+    """The compiler holds the bound array until it is unbound, so dropping
+    the caller's last reference frees nothing: new arrays of the same shape
+    get other addresses and are copied in, never mistaken for the snapshot
+    (a freed block is otherwise handed to the next array of its size)."""
+    import gc
+    import weakref
+    from mlir_edsl_hip import wire
+    M, K, N = 16, 64, 32
+    comp = MLIRCompiler()
+    comp.set_target("gpu")
+    name = "dense_bound_lifetime"
+    comp.compile_function(wire.dense_layer(name, M, K, N))
+    ptr = comp.get_function_pointer(name)
+    X, W, b = _layer_inputs(M, K, N, 77)
+    comp.bind_parameter(name, "W", W)
+    addr, alive = W.ctypes.data, weakref.ref(W)
+    del W
+    gc.collect()
+    assert alive() is not None, "the bound array was released while bound"
+    rng = np.random.default_rng(78)
+    for trial in range(16):
+        Wn = rng.standard_normal((K, N), dtype=np.float32)
+        assert Wn.ctypes.data != addr, trial
+        out = np.empty((M, N), np.float32)
+        _call_pointer(ptr, (X, Wn, b), out)
+        assert "resident: W" not in _native.last_plan(), _native.last_plan()
+        _check(out, oracle.dense_f32_chains(X, Wn, b, "relu"), K)
+        del Wn
+    comp.unbind_parameter(name, "W")
+    gc.collect()
+    assert alive() is None, "unbinding keeps no reference"
     comp.clear()

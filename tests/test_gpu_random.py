@@ -114,7 +114,7 @@ def _check_case(seed, case, torch):
     b = _draw(rng, (N,), dtype, wide) if bias else None
     alpha = float(np.float32(rng.uniform(0.01, 0.5)))
     if dtype == "f32":
-        ref = oracle.dense_f32(X, W, b, act, alpha)
+        ref = oracle.dense_f32_chains(X, W, b, act, alpha)
     else:
         ref = oracle.dense_i32(X, W, b, act)
     epi = (1 if bias else 0) | (_EPI[act] << 1)
@@ -176,7 +176,7 @@ def _check_small_m(seed, torch):
            f"w_off={w_off} [{plan}]"
     assert plan.startswith("gemv_f32"), what
     try:
-        assert_f32_parity(tY.cpu().numpy(), oracle.dense_f32(X, W, b, act, alpha), K)
+        assert_f32_parity(tY.cpu().numpy(), oracle.dense_f32_chains(X, W, b, act, alpha), K)
     except AssertionError as e:
         raise AssertionError(f"{what}: {e}") from None
 
@@ -215,7 +215,7 @@ def _check_small_m_unaligned_w(seed, torch):
     what = f"seed={seed} {pattern} M={M} K={K} N={N} x_pad={x_pad} x_off={x_off} w_pad={w_pad} " \
            f"w_off={w_off} [{_native.last_plan()}]"
     try:
-        assert_f32_parity(tY.cpu().numpy(), oracle.dense_f32(X, W, b, act, alpha), K)
+        assert_f32_parity(tY.cpu().numpy(), oracle.dense_f32_chains(X, W, b, act, alpha), K)
     except AssertionError as e:
         raise AssertionError(f"{what}: {e}") from None
     return _native.last_plan()

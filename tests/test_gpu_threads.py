@@ -34,7 +34,7 @@ def _worker(tid, iters, errors):
                 X = rng.standard_normal((M, K), dtype=np.float32)
                 W = rng.standard_normal((K, N), dtype=np.float32)
                 b = rng.standard_normal(N, dtype=np.float32)
-                ref = oracle.dense_f32(X, W, b, "relu")
+                ref = oracle.dense_f32_chains(X, W, b, "relu")
             else:
                 X = rng.integers(-128, 128, size=(M, K), dtype=np.int32)
                 W = rng.integers(-128, 128, size=(K, N), dtype=np.int32)

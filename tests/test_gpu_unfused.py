@@ -39,4 +39,4 @@ def test_unfused_sequence_equals_the_fused_launch(M, K, N, epi):
     assert plans[1].startswith("unfused: fill | ") and plans[1].endswith(f"bias_act epi={epi}"), plans[1]
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     bias, act = _ACT[epi]
-    assert_f32_parity(outs[1], oracle.dense_f32(X, W, b if bias else None, act, 0.03), K)
+    assert_f32_parity(outs[1], oracle.dense_f32_chains(X, W, b if bias else None, act, 0.03), K)

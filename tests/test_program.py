@@ -38,6 +38,7 @@ REJECT = [c for c in _cases() if "reject" in c["expected"]]
 @pytest.fixture
 def compiler():
     c = MLIRCompiler()
+    c.set_target("gpu")  # as the front end does for a target="gpu" function
     yield c
     c.clear()
 
@@ -339,19 +340,18 @@ def _case(fixture):
 
 
 def test_scalar_and_dense_functions_in_one_session(with_reference):
-    """Dense target="gpu" programs run on the HIP kernels; programs outside the
-    dense path, and anything compiled for target="cpu", go to the reference
-    compiler; later calls are routed by name."""
+    """Routing is by target: target="gpu" programs compile on the HIP module,
+    anything compiled for target="cpu" goes to the reference compiler (even a
+    dense program); later calls are routed by name."""
     c = with_reference
     dense, scalar, mm = _case("dense_relu_f32"), _case("reject_scalar_function"), _case("matmul_f32")
     c.set_target("gpu")
     c.compile_function(_bytes(dense))
-    c.compile_function(_bytes(scalar))  # rejected by the HIP module -> reference
     assert c.backend_of(dense["function"]) == "hip"
-    assert c.backend_of(scalar["function"]) == "reference"
-    assert c.reference.fns == {scalar["function"]: "gpu"}
     c.set_target("cpu")
+    c.compile_function(_bytes(scalar))  # CPU JIT requested -> reference
     c.compile_function(_bytes(mm))  # CPU JIT requested -> reference, although it is dense
+    assert c.backend_of(scalar["function"]) == "reference" and c.reference.fns[scalar["function"]] == "cpu"
     assert c.backend_of(mm["function"]) == "reference" and c.reference.fns[mm["function"]] == "cpu"
     assert c.list_functions() == sorted([dense["function"], scalar["function"], mm["function"]])
     assert all(c.has_function(n) for n in c.list_functions())
@@ -365,6 +365,23 @@ def test_scalar_and_dense_functions_in_one_session(with_reference):
     assert c.reference.opt == 3
     c.clear()
     assert c.list_functions() == [] and c.reference.fns == {}
+
+
+def test_rejected_gpu_program_raises_the_decoder_message(with_reference):
+    """A target="gpu" program outside the dense path is not handed to the
+    reference module (built without GPU support on this host, reference
+    cpp/src/MLIRCompiler.cpp:456-461): the HIP decoder's own message is
+    raised at compile time and the reference compiler sees nothing."""
+    c = with_reference
+    c.set_target("gpu")
+    for fixture in ("reject_scalar_function", "reject_layer_as_rhs"):
+        case = _case(fixture)
+        with pytest.raises(RuntimeError, match=case["expected"]["reject"]) as e:
+            c.compile_function(_bytes(case))
+        assert "is not a dense-path program" in str(e.value)
+        assert not c.has_function(case["function"])
+    assert c.reference.fns == {}
+    assert c.list_functions() == []
 
 
 def test_dense_errors_are_not_delegated(with_reference):

@@ -78,7 +78,7 @@ def test_noalloc_matches_the_allocating_entry(pair, torch_cuda):
             f"{np.count_nonzero(got.view(np.uint32) != ref.view(np.uint32))} elements differ"
         act = {_native.EPI_BIAS_RELU: "relu", _native.EPI_RELU: "relu", _native.EPI_BIAS_LEAKY: "leaky",
                _native.EPI_BIAS: "none"}[epi]
-        assert_f32_parity(got, oracle.dense_f32(X, W, b if epi & 1 else None, act, 0.02), K)
+        assert_f32_parity(got, oracle.dense_f32_chains(X, W, b if epi & 1 else None, act, 0.02), K)
 
 
 def test_noalloc_rejects_plans_beyond_its_scratch(torch_cuda):
