@@ -40,6 +40,8 @@
  *  - i32 arithmetic: arith.muli / arith.addi (two's complement, wrapping);
  *    results are bit-identical to the reference for every input. ReLU on i32
  *    is v > 0 ? v : 0, the reference's tensor_map(If(v > 0, v, 0)).
+ *  - The f32 ReLU written tensor_map(v -> If(v > 0.0, v, 0.0)) is cmpf ogt
+ *    then a select of v or +0.0: NaN and -0 give +0 (unlike maximumf).
  */
 #ifndef EDSL_HIP_H
 #define EDSL_HIP_H
@@ -99,6 +101,15 @@ void edsl_hip_matmul_relu_f32(EDSL_MEMREF2(float, A), EDSL_MEMREF2(float, B), ED
 void edsl_hip_matmul_relu_i32(EDSL_MEMREF2(int32_t, A), EDSL_MEMREF2(int32_t, B),
                               EDSL_MEMREF2(int32_t, C));
 
+/* Y = tensor_map(X @ W + b, lambda v: If(v > 0.0, v, 0.0)) over f32, one
+ * fused kernel. 26 arguments. Replaces fill + matmul + the bias generic + the
+ * linalg.map whose body is the If (reference cpp/src/builders/LinalgBuilder.cpp:141-178;
+ * the map form of tests/linalg/test_map_execution.py:40-52). */
+void edsl_hip_dense_if_relu_f32(EDSL_MEMREF2(float, X), EDSL_MEMREF2(float, W),
+                                EDSL_MEMREF1(float, b), EDSL_MEMREF2(float, Y));
+/* Y = tensor_map(A @ B, lambda v: If(v > 0.0, v, 0.0)) over f32. 21 arguments. */
+void edsl_hip_matmul_if_relu_f32(EDSL_MEMREF2(float, A), EDSL_MEMREF2(float, B), EDSL_MEMREF2(float, C));
+
 /* Host-buffer entry in the shape of MLIRCompiler::executeGPUFunction
  * (reference cpp/src/MLIRCompiler.cpp:352-461, bound to Python as
  * execute_gpu_function at cpp/src/python_bindings.cpp:69-97): contiguous
@@ -113,6 +124,8 @@ void edsl_hip_matmul_relu_i32(EDSL_MEMREF2(int32_t, A), EDSL_MEMREF2(int32_t, B)
 #define EDSL_PATTERN_DENSE_RELU 2  /* relu(X @ W + b)               */
 #define EDSL_PATTERN_DENSE_LEAKY 3 /* leaky_relu(X @ W + b, alpha)  */
 #define EDSL_PATTERN_MATMUL_RELU 4 /* relu(A @ B)                   */
+#define EDSL_PATTERN_DENSE_IF_RELU 5  /* tensor_map(X @ W + b, v -> If(v > 0, v, 0)) */
+#define EDSL_PATTERN_MATMUL_IF_RELU 6 /* tensor_map(A @ B, v -> If(v > 0, v, 0))     */
 #define EDSL_DTYPE_F32 0
 #define EDSL_DTYPE_I32 1
 int edsl_hip_execute_gpu_function(int pattern, int dtype, int num_inputs,

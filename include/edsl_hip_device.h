@@ -36,13 +36,18 @@
 extern "C" {
 #endif
 
-/* Epilogue codes: bit 0 = add bias[N]; bits 1-2 = activation. */
+/* Epilogue codes: bit 0 = add bias[N]; bits 1-2 = activation: ReLU as
+ * arith.maximumf (NaN propagates), leaky ReLU (f32 only), or ReLU as the
+ * tensor_map body If(v > 0, v, 0) (cmpf ogt: NaN and -0 give +0; on i32 the
+ * same as EDSL_EPI_RELU). */
 #define EDSL_EPI_NONE 0
 #define EDSL_EPI_BIAS 1
 #define EDSL_EPI_RELU 2
 #define EDSL_EPI_BIAS_RELU 3
 #define EDSL_EPI_LEAKY 4
 #define EDSL_EPI_BIAS_LEAKY 5
+#define EDSL_EPI_IF_RELU 6
+#define EDSL_EPI_BIAS_IF_RELU 7
 
 /* Y[M,N] = epilogue(X[M,K] @ W[K,N] (+ bias)), f32. */
 int edsl_hip_dense_f32_launch(const float *X, int64_t ldx, const float *W, int64_t ldw,

@@ -8,6 +8,10 @@
 //          tensor_map(v -> If(v > 0, v, 0)) (LinalgBuilder.cpp:141-178).
 //   leaky: max(x,0) + alpha*min(x,0) with arith.maximumf / arith.minimumf,
 //          mulf, addf (LinalgBuilder.cpp:216-225).
+//   if-relu: the f32 ReLU written tensor_map(v -> If(v > 0.0, v, 0.0))
+//          (LinalgBuilder.cpp:141-178, comparison predicate
+//          ArithBuilder.cpp:122-126): cmpf ogt is false for NaN and -0, so
+//          both give the constant +0.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -27,6 +31,7 @@ enum : int {
   ACT_NONE = 0,
   ACT_RELU = 1,
   ACT_LEAKY = 2,
+  ACT_IF_RELU = 3,
 };
 constexpr int epi_code(bool bias, int act) { return (bias ? 1 : 0) | (act << 1); }
 constexpr bool epi_has_bias(int epi) { return (epi & 1) != 0; }
@@ -47,6 +52,8 @@ __device__ __forceinline__ float apply_epilogue_f32(float acc, float b, float al
   if constexpr (epi_has_bias(EPI)) y = __fadd_rn(y, b);
   if constexpr (epi_act(EPI) == ACT_RELU) {
     y = maximumf_zero(y);
+  } else if constexpr (epi_act(EPI) == ACT_IF_RELU) {
+    y = y > 0.0f ? y : 0.0f;
   } else if constexpr (epi_act(EPI) == ACT_LEAKY) {
     // mulf then addf, each rounded (no contraction), as the reference emits them.
     y = __fadd_rn(maximumf_zero(y), __fmul_rn(minimumf_zero(y), alpha));

@@ -508,102 +508,6 @@ gemm_f32_kernel(GemmF32Args args) {
   }
 }
 
-// Tile configurations. Keep in sync with kConfigs below.
-//  0: 256x256x16, 2x2 waves (wave tile 128x128, 256 accumulators / lane)
-//  1: 256x256x16, 4x2 waves (wave tile  64x128)
-//  2: 128x128x16, 2x2 waves (wave tile  64x64)
-//  3:  64x64x16,  2x2 waves (wave tile  32x32)
-//  4:  64x64x16,  2x2 waves, guarded (any shape / alignment)
-//  5: 256x256x32, 4x2 waves
-//  6: 128x256x16, 2x2 waves (wave tile 64x128)
-//  7-11: 64x64x{32,64}, 128x64x32, 64x128x32, 128x128x32 with 2x2 waves
-//  12-13: 32x32x{32,64}, one wave
-//  14-18: _kN = N waves per output block splitting each K step, partial tiles
-//         summed through LDS: 64x64x64 and 64x64x32 (k2), 32x32x64 (k2, k4),
-//         128x128x32 (k2)
-//  19-21: 64x64x128 (k2, k4) and 64x64x64 (k4): deeper K steps / more waves
-//         per CU for latency-bound mid-size shapes
-//  22: 64x64x64 (k2) with global loads two K steps ahead (_pf2); the same
-//      lead measured slower for the k4 and 256x256 tiles
-//  23: 256x256x16 with 16 waves (4x4, wave tile 64x64): at 4096^3 ~2 % faster
-//      than 8 waves (992 vs 1012 us); 8x2 waves measure the same, 2x8 and
-//      BK = 32 with 16 waves slower, two K steps of prefetch slower
-//  24: 64x64x32 (k2) with global loads four K steps ahead: at 1024^3 (one
-//      workgroup per CU, nothing else on the CU to hide a step's loads)
-//      24.1-24.4 vs 24.6-25.0 us for 22; at 4096x512x4096 (two per CU) 171
-//      vs 163 us. Three steps ahead, and 64-deep steps four ahead, measured
-//      no better than 22. Its LDS stores are issued ahead of the MFMAs
-//      (SCHED 1); the same order on 22 measured 1 % slower at 4096x512x4096.
-//  25: 32x32x64 (k4) with all four 64-deep K steps of a 256-deep K loaded
-//      up front (256^3: 7.54 vs 7.31 TFLOP/s for 17)
-//  26-30: edge-tile twins of 23, 2, 24, 22 and 25 (kGuardEdge) for shapes
-//      the tile does not divide
-//  31-35: any-shape twins of the same five (kGuardScalar: 4-byte loads and
-//      stores at clamped addresses), for operands whose rows are not 16-byte
-//      aligned or whose K or N is not a multiple of 4; these layers stay on
-//      the large MFMA tiles instead of the small guarded 64x64x16 one
-//  36: 128x128x32 on 16x16 MFMA blocks, one wave per SIMD and two
-//      workgroups per CU (gemm_f32_m16.hip): 4096^3 965 vs 986 us for 23,
-//      2048^3 141 vs 165 us for 2, 4096x512x4096 143 vs 144-150 us for 23
-//  37: its 64x64x64 twin (32x32 per wave): 1024^3 21.6 vs 23.3 us for 24,
-//      4096x4096x512 149 vs 157 us for 22
-//  38-39: edge-tile twins of 36 and 37 (kGuardEdge)
-//  40: any-shape twin of 36 (kGuardScalar); the 64x64 one measured slower
-//      than 34 (1025^3: 54.8 vs 49.0 us) and is not built
-//  41-42: 128x256x32 on 16x16 MFMA blocks, 2x4 waves of 64x64, one
-//      workgroup per CU, and its edge twin: 4096^3 938-941 vs 959-962 us for
-//      36, 8192^3 7411 vs 7519 us, 4000^3 922-924 vs 949 us for 38
-//  43-44: 128x128x32 with 2x4 waves of 64x32 (eight waves, one workgroup
-//      per CU) and its edge twin, for exactly one tile per CU: 2048^3 137
-//      vs 139-141 us for 36, 2000^3 137 vs 141 us for 38
-const GemmF32Config kConfigs[] = {
-    {256, 256, 16, 2, 2, kGuardNone, "f32_256x256x16_w2x2"},
-    {256, 256, 16, 4, 2, kGuardNone, "f32_256x256x16_w4x2"},
-    {128, 128, 16, 2, 2, kGuardNone, "f32_128x128x16_w2x2"},
-    {64, 64, 16, 2, 2, kGuardNone, "f32_64x64x16_w2x2"},
-    {64, 64, 16, 2, 2, kGuardAll, "f32_64x64x16_w2x2_guard"},
-    {256, 256, 32, 4, 2, kGuardNone, "f32_256x256x32_w4x2"},
-    {128, 256, 16, 2, 2, kGuardNone, "f32_128x256x16_w2x2"},
-    {64, 64, 32, 2, 2, kGuardNone, "f32_64x64x32_w2x2"},
-    {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_w2x2"},
-    {128, 64, 32, 2, 2, kGuardNone, "f32_128x64x32_w2x2"},
-    {64, 128, 32, 2, 2, kGuardNone, "f32_64x128x32_w2x2"},
-    {128, 128, 32, 2, 2, kGuardNone, "f32_128x128x32_w2x2"},
-    {32, 32, 32, 1, 1, kGuardNone, "f32_32x32x32_w1x1"},
-    {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1"},
-    {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_w2x2_k2"},
-    {64, 64, 32, 2, 2, kGuardNone, "f32_64x64x32_w2x2_k2"},
-    {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k2"},
-    {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k4"},
-    {128, 128, 32, 2, 2, kGuardNone, "f32_128x128x32_w2x2_k2"},
-    {64, 64, 128, 2, 2, kGuardNone, "f32_64x64x128_w2x2_k2"},
-    {64, 64, 128, 2, 2, kGuardNone, "f32_64x64x128_w2x2_k4"},
-    {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_w2x2_k4"},
-    {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_w2x2_k2_pf2"},
-    {256, 256, 16, 4, 4, kGuardNone, "f32_256x256x16_w4x4"},
-    {64, 64, 32, 2, 2, kGuardNone, "f32_64x64x32_w2x2_k2_pf4"},
-    {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k4_pf4"},
-    {256, 256, 16, 4, 4, kGuardEdge, "f32_256x256x16_w4x4_edge"},
-    {128, 128, 16, 2, 2, kGuardEdge, "f32_128x128x16_w2x2_edge"},
-    {64, 64, 32, 2, 2, kGuardEdge, "f32_64x64x32_w2x2_k2_pf4_edge"},
-    {64, 64, 64, 2, 2, kGuardEdge, "f32_64x64x64_w2x2_k2_pf2_edge"},
-    {32, 32, 64, 1, 1, kGuardEdge, "f32_32x32x64_w1x1_k4_pf4_edge"},
-    {256, 256, 16, 4, 4, kGuardScalar, "f32_256x256x16_w4x4_anyshape"},
-    {128, 128, 16, 2, 2, kGuardScalar, "f32_128x128x16_w2x2_anyshape"},
-    {64, 64, 32, 2, 2, kGuardScalar, "f32_64x64x32_w2x2_k2_pf4_anyshape"},
-    {64, 64, 64, 2, 2, kGuardScalar, "f32_64x64x64_w2x2_k2_pf2_anyshape"},
-    {32, 32, 64, 1, 1, kGuardScalar, "f32_32x32x64_w1x1_k4_pf4_anyshape"},
-    {128, 128, 32, 2, 2, kGuardNone, "f32_128x128x32_mfma16"},
-    {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_mfma16"},
-    {128, 128, 32, 2, 2, kGuardEdge, "f32_128x128x32_mfma16_edge"},
-    {64, 64, 64, 2, 2, kGuardEdge, "f32_64x64x64_mfma16_edge"},
-    {128, 128, 32, 2, 2, kGuardScalar, "f32_128x128x32_mfma16_anyshape"},
-    {128, 256, 32, 2, 4, kGuardNone, "f32_128x256x32_mfma16"},
-    {128, 256, 32, 2, 4, kGuardEdge, "f32_128x256x32_mfma16_edge"},
-    {128, 128, 32, 2, 4, kGuardNone, "f32_128x128x32_mfma16_w8"},
-    {128, 128, 32, 2, 4, kGuardEdge, "f32_128x128x32_mfma16_w8_edge"},
-};
-constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
 template <int BM, int BN, int BK, int WMW, int WNW, int WKW, int GUARD, int PF = 1, int SCHED = 0>
 hipError_t launch_cfg(int epi, const GemmF32Args& a, hipStream_t stream) {
@@ -621,6 +525,8 @@ hipError_t launch_cfg(int epi, const GemmF32Args& a, hipStream_t stream) {
     EDSL_F32_CASE(epi_code(true, ACT_RELU))
     EDSL_F32_CASE(epi_code(false, ACT_LEAKY))
     EDSL_F32_CASE(epi_code(true, ACT_LEAKY))
+    EDSL_F32_CASE(epi_code(false, ACT_IF_RELU))
+    EDSL_F32_CASE(epi_code(true, ACT_IF_RELU))
     default:
       return hipErrorInvalidValue;
   }
@@ -630,56 +536,24 @@ hipError_t launch_cfg(int epi, const GemmF32Args& a, hipStream_t stream) {
 
 }  // namespace
 
-int gemm_f32_num_configs() { return kNumConfigs; }
-const GemmF32Config& gemm_f32_config(int cfg) { return kConfigs[cfg]; }
-
 hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) {
   switch (cfg) {
-    case 0: return launch_cfg<256, 256, 16, 2, 2, 1, kGuardNone>(epi, a, stream);
-    case 1: return launch_cfg<256, 256, 16, 4, 2, 1, kGuardNone>(epi, a, stream);
-    case 2: return launch_cfg<128, 128, 16, 2, 2, 1, kGuardNone>(epi, a, stream);
-    case 3: return launch_cfg<64, 64, 16, 2, 2, 1, kGuardNone>(epi, a, stream);
-    case 4: return launch_cfg<64, 64, 16, 2, 2, 1, kGuardAll>(epi, a, stream);
-    case 5: return launch_cfg<256, 256, 32, 4, 2, 1, kGuardNone>(epi, a, stream);
-    case 6: return launch_cfg<128, 256, 16, 2, 2, 1, kGuardNone>(epi, a, stream);
-    case 7: return launch_cfg<64, 64, 32, 2, 2, 1, kGuardNone>(epi, a, stream);
-    case 8: return launch_cfg<64, 64, 64, 2, 2, 1, kGuardNone>(epi, a, stream);
-    case 9: return launch_cfg<128, 64, 32, 2, 2, 1, kGuardNone>(epi, a, stream);
-    case 10: return launch_cfg<64, 128, 32, 2, 2, 1, kGuardNone>(epi, a, stream);
-    case 11: return launch_cfg<128, 128, 32, 2, 2, 1, kGuardNone>(epi, a, stream);
-    case 12: return launch_cfg<32, 32, 32, 1, 1, 1, kGuardNone>(epi, a, stream);
-    case 13: return launch_cfg<32, 32, 64, 1, 1, 1, kGuardNone>(epi, a, stream);
-    case 14: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardNone>(epi, a, stream);
-    case 15: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardNone>(epi, a, stream);
-    case 16: return launch_cfg<32, 32, 64, 1, 1, 2, kGuardNone>(epi, a, stream);
-    case 17: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardNone>(epi, a, stream);
-    case 18: return launch_cfg<128, 128, 32, 2, 2, 2, kGuardNone>(epi, a, stream);
-    case 19: return launch_cfg<64, 64, 128, 2, 2, 2, kGuardNone>(epi, a, stream);
-    case 20: return launch_cfg<64, 64, 128, 2, 2, 4, kGuardNone>(epi, a, stream);
-    case 21: return launch_cfg<64, 64, 64, 2, 2, 4, kGuardNone>(epi, a, stream);
-    case 22: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardNone, 2>(epi, a, stream);
-    case 23: return launch_cfg<256, 256, 16, 4, 4, 1, kGuardNone>(epi, a, stream);
-    case 24: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardNone, 4, 1>(epi, a, stream);
-    case 25: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardNone, 4>(epi, a, stream);
-    case 26: return launch_cfg<256, 256, 16, 4, 4, 1, kGuardEdge>(epi, a, stream);
-    case 27: return launch_cfg<128, 128, 16, 2, 2, 1, kGuardEdge>(epi, a, stream);
-    case 28: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardEdge, 4, 1>(epi, a, stream);
-    case 29: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardEdge, 2>(epi, a, stream);
-    case 30: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardEdge, 4>(epi, a, stream);
-    case 31: return launch_cfg<256, 256, 16, 4, 4, 1, kGuardScalar>(epi, a, stream);
-    case 32: return launch_cfg<128, 128, 16, 2, 2, 1, kGuardScalar>(epi, a, stream);
-    case 33: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardScalar, 4, 1>(epi, a, stream);
-    case 34: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardScalar, 2>(epi, a, stream);
-    case 35: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardScalar, 4>(epi, a, stream);
-    case 36: return launch_gemm_f32_m16(0, kGuardNone, epi, a, stream);
-    case 37: return launch_gemm_f32_m16(1, kGuardNone, epi, a, stream);
-    case 38: return launch_gemm_f32_m16(0, kGuardEdge, epi, a, stream);
-    case 39: return launch_gemm_f32_m16(1, kGuardEdge, epi, a, stream);
-    case 40: return launch_gemm_f32_m16(0, kGuardScalar, epi, a, stream);
-    case 41: return launch_gemm_f32_m16(2, kGuardNone, epi, a, stream);
-    case 42: return launch_gemm_f32_m16(2, kGuardEdge, epi, a, stream);
-    case 43: return launch_gemm_f32_m16(3, kGuardNone, epi, a, stream);
-    case 44: return launch_gemm_f32_m16(3, kGuardEdge, epi, a, stream);
+    case kF32Guard64: return launch_cfg<64, 64, 16, 2, 2, 1, kGuardAll>(epi, a, stream);
+    case kF32T32: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardNone, 4>(epi, a, stream);
+    case kF32T32Edge: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardEdge, 4>(epi, a, stream);
+    case kF32T32Any: return launch_cfg<32, 32, 64, 1, 1, 4, kGuardScalar, 4>(epi, a, stream);
+    case kF32T64Any: return launch_cfg<64, 64, 32, 2, 2, 2, kGuardScalar, 4, 1>(epi, a, stream);
+    case kF32T64K2Any: return launch_cfg<64, 64, 64, 2, 2, 2, kGuardScalar, 2>(epi, a, stream);
+    case kF32T256Any: return launch_cfg<256, 256, 16, 4, 4, 1, kGuardScalar>(epi, a, stream);
+    case kF32M16_128: return launch_gemm_f32_m16(0, kGuardNone, epi, a, stream);
+    case kF32M16_128Edge: return launch_gemm_f32_m16(0, kGuardEdge, epi, a, stream);
+    case kF32M16_128Any: return launch_gemm_f32_m16(0, kGuardScalar, epi, a, stream);
+    case kF32M16_64: return launch_gemm_f32_m16(1, kGuardNone, epi, a, stream);
+    case kF32M16_64Edge: return launch_gemm_f32_m16(1, kGuardEdge, epi, a, stream);
+    case kF32M16_128x256: return launch_gemm_f32_m16(2, kGuardNone, epi, a, stream);
+    case kF32M16_128x256Edge: return launch_gemm_f32_m16(2, kGuardEdge, epi, a, stream);
+    case kF32M16_128W8: return launch_gemm_f32_m16(3, kGuardNone, epi, a, stream);
+    case kF32M16_128W8Edge: return launch_gemm_f32_m16(3, kGuardEdge, epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -419,6 +419,8 @@ hipError_t launch_layout(int epi, const GemmF32Args& a, hipStream_t stream) {
     EDSL_M16_CASE(epi_code(true, ACT_RELU))
     EDSL_M16_CASE(epi_code(false, ACT_LEAKY))
     EDSL_M16_CASE(epi_code(true, ACT_LEAKY))
+    EDSL_M16_CASE(epi_code(false, ACT_IF_RELU))
+    EDSL_M16_CASE(epi_code(true, ACT_IF_RELU))
     default:
       return hipErrorInvalidValue;
   }

@@ -59,7 +59,9 @@ __device__ __forceinline__ float epilogue_rt(float acc, float b, float alpha, in
     case epi_code(false, ACT_RELU): return apply_epilogue_f32<epi_code(false, ACT_RELU)>(acc, b, alpha);
     case epi_code(true, ACT_RELU): return apply_epilogue_f32<epi_code(true, ACT_RELU)>(acc, b, alpha);
     case epi_code(false, ACT_LEAKY): return apply_epilogue_f32<epi_code(false, ACT_LEAKY)>(acc, b, alpha);
-    default: return apply_epilogue_f32<epi_code(true, ACT_LEAKY)>(acc, b, alpha);
+    case epi_code(true, ACT_LEAKY): return apply_epilogue_f32<epi_code(true, ACT_LEAKY)>(acc, b, alpha);
+    case epi_code(false, ACT_IF_RELU): return apply_epilogue_f32<epi_code(false, ACT_IF_RELU)>(acc, b, alpha);
+    default: return apply_epilogue_f32<epi_code(true, ACT_IF_RELU)>(acc, b, alpha);
   }
 }
 

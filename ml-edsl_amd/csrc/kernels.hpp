@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "plan_f32.hpp"
+
 namespace edsl {
 
 // ---------------------------------------------------------------- fp32 tiled
@@ -19,23 +21,6 @@ struct GemmF32Args {
   float alpha;        // leaky-ReLU slope
 };
 
-// Bounds handling of a tile configuration.
-enum : int {
-  kGuardNone = 0,  // M, N, K multiples of the tile; 16-byte aligned operands and row strides
-  kGuardEdge = 1,  // partial edge tiles; 16-byte aligned operands, strides, N and K multiples of 4
-  kGuardAll = 2,   // any shape and alignment (element-wise checks)
-  kGuardScalar = 3,  // partial edge tiles, any alignment, K and N: 4-byte accesses at clamped addresses
-};
-
-struct GemmF32Config {
-  int bm, bn, bk;
-  int waves_m, waves_n;
-  int guard;          // kGuard*
-  const char* name;
-};
-
-int gemm_f32_num_configs();
-const GemmF32Config& gemm_f32_config(int cfg);
 hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args args, hipStream_t stream);
 // The tiles on 16x16 MFMA blocks (gemm_f32_m16.hip), 16-byte aligned operands
 // and row strides: layout 0, a 128x128 tile with 32-deep K steps; 1, a 64x64

@@ -1,0 +1,194 @@
+// The fp32 tile configurations and their planner (plan_f32.hpp).
+#include "plan_f32.hpp"
+
+#include <initializer_list>
+
+namespace edsl {
+namespace {
+
+// The shipped tile configurations, indexed by F32Tile (plan_f32.hpp). Each
+// name spells the tile (BM x BN x BK), its waves and, for the tiles on 32x32
+// MFMA blocks, the waves splitting K (_kN) and the K steps of global loads
+// issued ahead (_pfN); a suffix gives the bounds variant (_edge: kGuardEdge,
+// _anyshape: kGuardScalar, _guard: kGuardAll).
+//  kF32Guard64: 64x64x16, 2x2 waves, element-checked loads and stores: any
+//      shape and alignment; the plan for K = 0.
+//  kF32T32*: 32x32x64 on one output block with four waves splitting each K
+//      step, all four 64-deep K steps of a 256-deep K loaded up front (256^3:
+//      7.54 TFLOP/s against 7.31 one step ahead); layers of at most 64 rows
+//      and many-tile shapes of small outputs.
+//  kF32T64Any: 64x64x32, two waves per output block splitting K, loads four
+//      steps ahead, LDS stores of the next step issued ahead of the MFMAs
+//      (SCHED 1): any-shape layers of at most one tile per CU.
+//  kF32T64K2Any: 64x64x64, two K waves, loads two steps ahead: any-shape
+//      layers of more 64x64 tiles than CUs (1025^3: 49.0 us against 54.8 us
+//      for the 64x64 layout on 16x16 blocks).
+//  kF32T256Any: 256x256x16, 4x4 waves (wave tile 64x64): 4001^3 and
+//      misaligned 4096^3 1116 and 1059 us against 1153 and 1151 us for
+//      kF32M16_128Any.
+//  kF32M16_*: the tiles on 16x16 MFMA blocks (gemm_f32_m16.hip): 128x128x32
+//      with one wave per SIMD and two workgroups per CU (4096^3 965 us
+//      against 986 us for 256x256x16 with 16 waves on 32x32 blocks; 2048^3
+//      141 against 165 us for 128x128x16), its 64x64x64 twin (1024^3 21.6
+//      against 23.3 us), 128x256x32 with 2x4 waves of 64x64 and one
+//      workgroup per CU (4096^3 938-941 against 959-962 us for 128x128,
+//      8192^3 7411 against 7519 us), and 128x128x32 with eight waves for
+//      exactly one tile per CU (2048^3 137 against 139-141 us).
+const GemmF32Config kConfigs[] = {
+    {64, 64, 16, 2, 2, kGuardAll, "f32_64x64x16_w2x2_guard"},
+    {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k4_pf4"},
+    {32, 32, 64, 1, 1, kGuardEdge, "f32_32x32x64_w1x1_k4_pf4_edge"},
+    {32, 32, 64, 1, 1, kGuardScalar, "f32_32x32x64_w1x1_k4_pf4_anyshape"},
+    {64, 64, 32, 2, 2, kGuardScalar, "f32_64x64x32_w2x2_k2_pf4_anyshape"},
+    {64, 64, 64, 2, 2, kGuardScalar, "f32_64x64x64_w2x2_k2_pf2_anyshape"},
+    {256, 256, 16, 4, 4, kGuardScalar, "f32_256x256x16_w4x4_anyshape"},
+    {128, 128, 32, 2, 2, kGuardNone, "f32_128x128x32_mfma16"},
+    {128, 128, 32, 2, 2, kGuardEdge, "f32_128x128x32_mfma16_edge"},
+    {128, 128, 32, 2, 2, kGuardScalar, "f32_128x128x32_mfma16_anyshape"},
+    {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_mfma16"},
+    {64, 64, 64, 2, 2, kGuardEdge, "f32_64x64x64_mfma16_edge"},
+    {128, 256, 32, 2, 4, kGuardNone, "f32_128x256x32_mfma16"},
+    {128, 256, 32, 2, 4, kGuardEdge, "f32_128x256x32_mfma16_edge"},
+    {128, 128, 32, 2, 4, kGuardNone, "f32_128x128x32_mfma16_w8"},
+    {128, 128, 32, 2, 4, kGuardEdge, "f32_128x128x32_mfma16_w8_edge"},
+};
+constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
+static_assert(kNumConfigs == kF32Tiles, "one table entry per F32Tile");
+
+}  // namespace
+
+int gemm_f32_num_configs() { return kNumConfigs; }
+const GemmF32Config& gemm_f32_config(int cfg) { return kConfigs[cfg]; }
+
+int plan_f32_tile(const F32TileQuery& q) {
+  const int64_t M = q.M, N = q.N, K = q.K;
+  const bool aligned = q.aligned;
+  int cfg = -1;
+  // Partial edge tiles need 16-byte vectors that are all in or all out of
+  // range: K and N multiples of 4 (true for every contiguous aligned operand).
+  const bool edge_ok = aligned && K >= 4 && N >= 4 && M >= 1 && K % 4 == 0 && N % 4 == 0;
+  auto fits = [&](int c) {
+    const GemmF32Config& g = gemm_f32_config(c);
+    if (g.guard == kGuardNone) return aligned && K > 0 && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
+    if (g.guard == kGuardEdge) return edge_ok;
+    return K > 0;  // kGuardScalar, kGuardAll: any shape, stride and alignment
+  };
+  // The first of a tile's bounds variants that fits these operands, or -1.
+  auto pick = [&](std::initializer_list<int> variants) {
+    for (int c : variants)
+      if (fits(c)) return c;
+    return -1;
+  };
+  auto tiles_of = [&](int c) {
+    const GemmF32Config& g = gemm_f32_config(c);
+    return (int64_t)((M + g.bm - 1) / g.bm) * ((N + g.bn - 1) / g.bn);
+  };
+  if (q.forced >= 0 && q.forced < gemm_f32_num_configs() && fits(q.forced)) {
+    cfg = q.forced;
+  } else if (K > 0 && M <= kF32SmallM) {
+    // Layers of at most 64 rows that the small-M kernel does not take (W or Y
+    // rows unaligned, N not a multiple of 4, short K) run on the 32x32 tiles:
+    // larger tiles spend most of their MFMAs on rows past M (16x4096x50257:
+    // 287 us on 32x32 against 364-1139 us on 64x64 to 256x256 tiles and 406
+    // us on the element-checked 64x64 tile; the same order at 16, 48 and 64
+    // rows).
+    cfg = pick({kF32T32, kF32T32Edge, kF32T32Any});
+  } else if (K > 0) {
+    // Candidates are tried in order of preference. The first whose tiles give
+    // every CU a workgroup is taken, unless it is larger than 64x64 and needs
+    // more than one round of workgroups with the last round keeping fewer
+    // than three quarters of the CUs busy (4097x4096: 272 tiles of 256x256
+    // would take two rounds of 4096^3-sized work). When none fills the chip,
+    // the candidate with the most tiles.
+    int best = -1, first_rejected = -1;
+    int64_t best_tiles = 0;
+    auto consider = [&](int c) {  // true when c is taken
+      if (c < 0) return false;
+      const GemmF32Config& g = gemm_f32_config(c);
+      const int64_t tiles = tiles_of(c);
+      if (tiles >= q.cus) {
+        const int64_t rounds = (tiles + q.cus - 1) / q.cus;
+        if (g.bm * g.bn > 64 * 64 && 4 * tiles < 3 * rounds * q.cus) {
+          if (first_rejected < 0) first_rejected = c;
+          return false;
+        }
+        cfg = c;
+        return true;
+      }
+      if (tiles > best_tiles) {
+        best_tiles = tiles;
+        best = c;
+      }
+      return false;
+    };
+    if (edge_ok) {
+      // 16-byte vector tiles (exact where the tile divides the layer, else
+      // their edge-tile twins): the 128x128 tile on 16x16 MFMA blocks, then
+      // its 64x64 twin, then 32x32 tiles.
+      const int c128 = pick({kF32M16_128, kF32M16_128Edge});
+      const int c64 = pick({kF32M16_64, kF32M16_64Edge});
+      bool skip128 = false;
+      if (tiles_of(c128) >= q.cus) {
+        // The 128x128 tile against its 64x64 and 128x256 twins, by how the
+        // tiles fall on the CUs. Two 128x128 (or 64x64) workgroups share a
+        // CU, so a CU with n tiles runs n/2 pairs (each pair ~0.94x the time
+        // of two tiles alone) and one tile alone when n is odd; a 64x64 tile
+        // takes ~0.27x a 128x128 one, and a 128x256 workgroup (eight waves,
+        // one per CU) ~0.98x a pair. 3000^3: 576 tiles of 128x128 leave 64
+        // CUs a third tile, 533 us against 470 us on 2209 tiles of 64x64.
+        // 4096^3: 939-940 us on 512 tiles of 128x256 against 952-960 us on
+        // 1024 of 128x128 (8192^3 7411 against 7519 us); 6000^3 stays on
+        // 128x128 (3157 us against 3437 us for 1128 tiles of 128x256, five
+        // rounds of one per CU), and so does 2048^3 (one tile per CU, 141 us
+        // against 153 us on 64x64). The constants were fitted on those
+        // shapes on MI355X.
+        auto cu_time = [&](int64_t n_tiles) {
+          const int64_t n = (n_tiles + q.cus - 1) / q.cus;
+          return (double)(n / 2) * 2.0 * 0.94 + (double)(n % 2);
+        };
+        const double t128 = cu_time(tiles_of(c128));
+        const double t64 = 0.27 * cu_time(tiles_of(c64));
+        const int cwide = pick({kF32M16_128x256, kF32M16_128x256Edge});
+        const int64_t tw = tiles_of(cwide);
+        const double twide =
+            tw >= q.cus ? (double)((tw + q.cus - 1) / q.cus) * 2.0 * 0.94 * 0.98 : 1e30;
+        if (twide <= t128 && twide <= t64) {
+          cfg = cwide;
+        } else if (t64 < t128) {
+          skip128 = true;
+        } else if (tiles_of(c128) == q.cus) {
+          // Exactly one 128x128 tile per CU: its eight-wave layout (two waves
+          // per SIMD to cover each other's waits; 2048^3 137 against 139-141
+          // us, 2000^3 137 against 141 us).
+          cfg = pick({kF32M16_128W8, kF32M16_128W8Edge});
+        }
+      }
+      if (cfg < 0 && !skip128) consider(c128);
+      if (cfg < 0) consider(c64);
+      if (cfg < 0) consider(pick({kF32T32, kF32T32Edge}));
+    } else {
+      // Rows not 16-byte aligned, or K or N not a multiple of 4: the
+      // any-shape tiles (4-byte accesses at clamped addresses) keep such
+      // layers on large MFMA tiles (2001^3: 57.8 TFLOP/s on the small
+      // element-checked tile alone). Measured order: 256x256 first (4001^3
+      // and misaligned 4096^3: 1116 and 1059 us against 1153 and 1151 us for
+      // 128x128 on 16x16 blocks), then 128x128 on 16x16 blocks (2001^3 175 us
+      // against 233 us for 128x128 on 32x32 blocks, which is therefore not
+      // built, and 194 us for 64x64;
+      // 2048^3 with every row misaligned 174 against 179 us), then the 64x64
+      // tiles: with loads four K steps ahead while there is one workgroup per
+      // CU at most (at two per CU the other workgroup hides the loads and the
+      // two-step twin wins), then 32x32.
+      for (int c : {kF32T256Any, kF32M16_128Any})
+        if (consider(c)) break;
+      if (cfg < 0 && tiles_of(kF32T64Any) <= q.cus) consider(kF32T64Any);
+      if (cfg < 0) consider(kF32T64K2Any);
+      if (cfg < 0) consider(kF32T32Any);
+    }
+    if (cfg < 0) cfg = best >= 0 ? best : first_rejected;
+  }
+  if (cfg < 0) cfg = kF32Guard64;  // K = 0: any shape and alignment
+  return cfg;
+}
+
+}  // namespace edsl

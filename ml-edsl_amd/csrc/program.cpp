@@ -38,6 +38,7 @@
 
 #include <algorithm>
 #include <array>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -572,7 +573,7 @@ struct Program {
 
 const char* kDenseForms =
     "matmul(A, B), relu(A @ B), X @ W + b, relu(X @ W + b), leaky_relu(X @ W + b, alpha), "
-    "tensor_map(X @ W [+ b], lambda v: If(v > 0, v, 0)) over i32, and chains of these layers "
+    "tensor_map(X @ W [+ b], lambda v: If(v > 0, v, 0)) over i32 or f32, and chains of these layers "
     "(h @ W2 + b2 with h a previous layer), with A, B, X, W, b parameters";
 
 struct Matcher {
@@ -675,30 +676,54 @@ struct Matcher {
     return n.k == K::Constant &&
            ((n.cvalue == 1 && n.ival == 0) || (n.cvalue == 2 && n.fval == 0.0f) || n.cvalue == 0);
   }
+  bool is_negative_zero(const Node& n) const { return n.k == K::Constant && n.cvalue == 2 && std::signbit(n.fval); }
 
-  // tensor_map body If(cmp, t, e) that is max(v, 0) exactly on i32.
-  bool relu_body(const Node& body, int64_t id) const {
-    if (body.k != K::If) return false;
+  // The activation a tensor_map body If(cmp, t, e) computes, as its epilogue
+  // bits: EDSL_EPI_RELU (on i32 every spelling of max(v, 0); on f32 the one
+  // with arith.maximumf's semantics), EDSL_EPI_IF_RELU (f32 v > 0 ? v : +0),
+  // or a rejection.
+  int map_activation(const Node& body, int64_t id, bool f32) {
+    const char* not_relu = "tensor_map body is not If(v > 0, v, 0) (or an equivalent ReLU)";
+    if (body.k != K::If) reject("%s", not_relu);
     const Node& c = res(body.a);
     const Node& t = res(body.b);
     const Node& e = res(body.c);
-    if (c.k != K::Compare) return false;
+    if (c.k != K::Compare) reject("%s", not_relu);
     const Node& l = res(c.a);
     const Node& r = res(c.b);
-    // v > 0, v >= 0 (then v else 0); v < 0, v <= 0 (then 0 else v); and the mirrored forms.
-    const bool gt = c.op == kGT || c.op == kSGT || c.op == kGE || c.op == kSGE || c.op == kOGT || c.op == kOGE;
-    const bool lt = c.op == kLT || c.op == kSLT || c.op == kLE || c.op == kSLE || c.op == kOLT || c.op == kOLE;
-    bool v_pos_selects_v;  // true when "cond true" means v is (weakly) positive
-    if (is_elem(l, id) && is_zero(r)) {
-      if (!gt && !lt) return false;
-      v_pos_selects_v = gt;
-    } else if (is_zero(l) && is_elem(r, id)) {
-      if (!gt && !lt) return false;
-      v_pos_selects_v = lt;  // 0 < v
-    } else {
-      return false;
+    // The comparison as "v OP 0": strict or weak, greater or less.
+    enum { kStrictGt, kWeakGt, kStrictLt, kWeakLt };
+    int dir;
+    switch (c.op) {
+      case kGT: case kSGT: case kOGT: dir = kStrictGt; break;
+      case kGE: case kSGE: case kOGE: dir = kWeakGt; break;
+      case kLT: case kSLT: case kOLT: dir = kStrictLt; break;
+      case kLE: case kSLE: case kOLE: dir = kWeakLt; break;
+      default: reject("%s", not_relu);
     }
-    return v_pos_selects_v ? (is_elem(t, id) && is_zero(e)) : (is_zero(t) && is_elem(e, id));
+    if (is_zero(l) && is_elem(r, id)) {
+      dir = dir == kStrictGt ? kStrictLt : dir == kWeakGt ? kWeakLt : dir == kStrictLt ? kStrictGt : kWeakGt;  // 0 < v is v > 0
+    } else if (!(is_elem(l, id) && is_zero(r))) {
+      reject("%s", not_relu);
+    }
+    // "v is positive" selects v, the other branch selects the zero.
+    const bool then_is_v = dir == kStrictGt || dir == kWeakGt;
+    const Node& v_branch = then_is_v ? t : e;
+    const Node& zero_branch = then_is_v ? e : t;
+    if (!is_elem(v_branch, id) || !is_zero(zero_branch)) reject("%s", not_relu);
+    if (!f32) return EDSL_EPI_RELU;
+    // f32: the reference builds arith.cmpf with ordered predicates only
+    // (ArithBuilder.cpp:122-138), false whenever v is NaN; and -0 compares
+    // equal to 0. Of the four spellings, v > 0 ? v : 0 maps NaN and -0 to +0,
+    // and v <= 0 ? 0 : v is arith.maximumf exactly (NaN propagates, -0 -> +0).
+    if (c.op != kOGT && c.op != kOGE && c.op != kOLT && c.op != kOLE)
+      reject("float comparison predicate %d is not one the reference lowers", c.op);
+    if (is_negative_zero(zero_branch))
+      reject("tensor_map body selects -0.0, which no fused epilogue writes; select 0.0");
+    if (dir == kStrictGt) return EDSL_EPI_IF_RELU;
+    if (dir == kWeakLt) return EDSL_EPI_RELU;
+    reject("tensor_map body If(v >= 0, v, 0) / If(v < 0, 0, v) over f32 keeps -0 (and the latter NaN), which no "
+           "fused epilogue computes; write If(v > 0.0, v, 0.0) or relu()");
   }
 
   // One layer rooted at n (activation / tensor_map ReLU / affine); its
@@ -722,12 +747,7 @@ struct Matcher {
       }
       affine(res(n.a), L, depth);
     } else if (n.k == K::Map) {
-      if (!relu_body(res(n.b), n.id))
-        reject("tensor_map body is not If(v > 0, v, 0) (or an equivalent integer ReLU)");
-      if (prog.dtype != EDSL_DTYPE_I32)
-        reject("tensor_map If-ReLU over f32 maps NaN to 0, which the fused maximumf epilogue does not; "
-               "use relu()");
-      L.epi |= EDSL_EPI_RELU;
+      L.epi |= map_activation(res(n.b), n.id, prog.dtype == EDSL_DTYPE_F32);
       affine(res(n.a), L, depth);
     } else {
       affine(n, L, depth);
@@ -790,6 +810,7 @@ std::string form_of(const Program& p) {
     if (L.b >= 0) aff += " + " + p.params[L.b].name;
     switch (L.epi >> 1) {
       case 1: h = "relu(" + aff + ")"; break;
+      case 3: h = "tensor_map(" + aff + ", lambda v: If(v > 0.0, v, 0.0))"; break;
       case 2: {
         char a[32];
         snprintf(a, sizeof(a), "%g", (double)L.alpha);
@@ -1133,7 +1154,7 @@ int edsl_hip_module_describe(edsl_hip_module* m, char* buf, size_t len) {
       std::string h;
       for (size_t li = 0; li < p.layers.size(); ++li) {
         const Layer& L = p.layers[li];
-        static const char* kAct[] = {"", "relu", "leaky_relu"};
+        static const char* kAct[4] = {"", "relu", "leaky_relu", "tensor_map If(v > 0.0, v, 0.0)"};
         char line[256];
         snprintf(line, sizeof(line), "  // layer %zu: %s @ %s%s%s%s -> one fused launch (epilogue %d%s)\n", li,
                  L.x >= 0 ? p.params[L.x].name.c_str() : h.c_str(), p.params[L.w].name.c_str(),

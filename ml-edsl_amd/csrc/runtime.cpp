@@ -285,6 +285,10 @@ struct DenseLaunch {
   void* y;
   int64_t ldy;
   int64_t M, N, K;
+  // A bias whose alignment the kernel choice takes into account although
+  // this launch does not add it (the GEMM of the unfused sequence, so that it
+  // runs the kernel the fused launch with that bias runs); null: none.
+  const void* plan_bias = nullptr;
 };
 
 void check_dims(int64_t M, int64_t N, int64_t K) {
@@ -352,7 +356,10 @@ bool plan_gemv(const DeviceState& ds, int64_t M, int64_t N, int64_t K, bool real
 
 void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const FixedScratch* fixed) {
   const bool has_bias = epi_has_bias(L.epi);
-  const bool aligned = al16(L.x) && al16(L.w) && al16(L.y) && (!has_bias || al16(L.bias)) &&
+  // The bias whose alignment constrains the kernels: the one added, or the
+  // plan's stand-in.
+  const void* bias_al = has_bias ? L.bias : L.plan_bias;
+  const bool aligned = al16(L.x) && al16(L.w) && al16(L.y) && (!bias_al || al16(bias_al)) &&
                        L.ldx % 4 == 0 && L.ldw % 4 == 0 && L.ldy % 4 == 0;
   const int M = (int)L.M, N = (int)L.N, K = (int)L.K;
 
@@ -362,7 +369,7 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   // not a multiple of 4) are realigned from 16-byte chunks or read per column,
   // with Y and the bias written and read per element.
   int gemv_cols = 0, gemv_ks = 0;
-  const bool w_vec = al16(L.w) && al16(L.y) && (!has_bias || al16(L.bias)) && L.ldw % 4 == 0 &&
+  const bool w_vec = al16(L.w) && al16(L.y) && (!bias_al || al16(bias_al)) && L.ldw % 4 == 0 &&
                      L.ldy % 4 == 0 && N % 4 == 0;
   // Realigned W rows (two aligned 16-byte chunks per lane and row) leave the
   // last row of W to the reduce kernel's K tail.
@@ -440,7 +447,10 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     if (!has_bias) a.bias = nullptr;
     // Two columns per lane (32-column blocks) read unaligned rows per column.
     a.w_mode = w_vec ? kWVector : (realigned_plan ? kWRealign : kWScalar);
-    if (gemv_f32_w_mode(a) == kWVector && a.w_mode != kWVector) fail(kErrInternal, "small-M W mode mismatch");
+    // Vector rows only where the operands allow them; the other modes are
+    // correct on any rows (a bias the epilogue does not add may still have
+    // ruled vector rows out, see DenseLaunch::plan_bias).
+    if (a.w_mode == kWVector && !gemv_f32_vector_rows(a)) fail(kErrInternal, "small-M W mode mismatch");
     if (fixed) {
       // Caller-fixed scratch: nothing is allocated and no cross-stream
       // ordering is added.
@@ -462,141 +472,8 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
     return;
   }
 
-  int cfg = -1;
-  // Partial edge tiles need 16-byte vectors that are all in or all out of
-  // range: K and N multiples of 4 (true for every contiguous aligned operand).
-  const bool edge_ok = aligned && K >= 4 && N >= 4 && M >= 1 && K % 4 == 0 && N % 4 == 0;
-  auto fits = [&](int c) {
-    const GemmF32Config& g = gemm_f32_config(c);
-    if (g.guard == kGuardNone) return aligned && K > 0 && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
-    if (g.guard == kGuardEdge) return edge_ok;
-    return K > 0;  // kGuardScalar, kGuardAll: any shape, stride and alignment
-  };
-  if (g_force_cfg >= 0 && g_force_cfg < gemm_f32_num_configs() && fits(g_force_cfg)) {
-    cfg = g_force_cfg;
-  } else if (K > 0) {
-    // Measured on MI355X: the 128x128x32 tile on 16x16 MFMA blocks with two workgroups per CU
-    // first wherever it fits with a workgroup per CU (4096^3: 965 us against 986 us for
-    // 256x256x16 with 16 waves on the same box; 2048^3: 141 against 165 us for 128x128x16);
-    // then its 64x64x64 twin (1024^3: 21.6 against 23.3 us for 64x64x32 with four K steps of
-    // loads ahead; 4096x512 outputs with K = 4096: 149 against 157 us for 64x64x64 two ahead).
-    // Its any-shape (4-byte access) twin comes after the 256x256 tiles: 2001^3 175 us against
-    // 233 us for 128x128x16 and 194 us for 64x64x64, 2048^3 with every row misaligned 174 against
-    // 179 us; at 4001^3 and misaligned 4096^3 the 256x256 any-shape tile stays ahead (1116 and
-    // 1059 us against 1153 and 1151 us).
-    // then 256x256x16 with 16 waves at 4096^3 (992 us; 256x256x32 with 8 waves
-    // 1012 us, the next in line); at 1024^3 the 64x64x64 tile with two
-    // waves per output block splitting K and global loads two K steps ahead (24.9 us) beats
-    // four K waves (25.6 us), two with one step ahead (26.1 us) and the plain 64x64x16 tile
-    // (29.6 us); at 256^3 the 32x32x64 tile with four K waves (64 workgroups, 3.5 us inside
-    // the kernel) beats every 64x64 tile (16 workgroups, 7 us).
-    // The 64x64 tile with four 32-deep K steps of loads ahead (24) only
-    // pays when there is one workgroup per CU at most (1024^3: 24.1-24.4 us
-    // against 24.6-25.0 for 22); with two per CU the other workgroup hides
-    // the loads and the deeper steps of 22 win (4096x512x4096: 163 vs 171 us).
-    // At 256^3 the 32x32x64 tile with four K waves loads all four K steps
-    // up front (25: 7.54-7.56 TFLOP/s against 7.31 for 17, one step ahead;
-    // 2 steps ahead, 8 K waves, or 128-deep steps measured lower).
-    // Each entry: the configuration for shapes the tile divides, its
-    // edge-tile twin (partial tiles at the M, N, K edges, 16-byte aligned
-    // rows) and its any-shape twin (element-checked loads and stores: rows
-    // of any alignment, K and N of any value), or -1. The any-shape twins
-    // keep unaligned layers on the same large tiles (2001^3: 57.8 TFLOP/s on
-    // the small guarded tile alone).
-    static const int kOrder[][3] = {{36, 38, -1}, {37, 39, -1}, {23, 26, 31}, {5, -1, -1}, {0, -1, -1}, {6, -1, -1}, {-1, -1, 40}, {2, 27, 32},
-                                    {24, 28, 33}, {22, 29, 34}, {21, -1, -1}, {14, -1, -1}, {15, -1, -1},
-                                    {3, -1, -1}, {25, 30, 35}};
-    int best = -1, first_rejected = -1;
-    int64_t best_tiles = 0;
-    // Layers of at most 64 rows that the small-M kernel cannot take (W or Y
-    // rows unaligned, N not a multiple of 4) run on the 32x32 tiles: larger
-    // tiles spend most of their MFMAs on rows past M (16x4096x50257: 287 us
-    // on 32x32 against 364-1139 us on 64x64 to 256x256 tiles and 406 us on
-    // the element-checked 64x64 tile; the same order at 16, 48 and 64 rows).
-    if (M <= kGemvMaxM) {
-      for (int c : {25, 30, 35})
-        if (fits(c)) {
-          cfg = c;
-          break;
-        }
-    }
-    for (const auto& e : kOrder) {
-      if (cfg >= 0) break;
-      int c = -1;
-      for (int t = 0; t < 3 && c < 0; ++t)
-        if (e[t] >= 0 && fits(e[t])) c = e[t];
-      if (c < 0) continue;
-      const GemmF32Config& g = gemm_f32_config(c);
-      const int64_t tiles = (int64_t)((M + g.bm - 1) / g.bm) * ((N + g.bn - 1) / g.bn);
-      if (e[0] == 24 && tiles > ds.cus) continue;
-      if (e[0] == 36 && tiles >= ds.cus) {
-        // The 128x128 tile on 16x16 MFMA blocks against its 64x64 and 128x256
-        // twins, by how the tiles fall on the CUs. Two 128x128 (or 64x64)
-        // workgroups share a CU, so a CU with n tiles runs n/2 pairs (each
-        // pair ~0.94x the time of two tiles alone) and one tile alone when n
-        // is odd; a 64x64 tile takes ~0.27x a 128x128 one, and a 128x256
-        // workgroup (eight waves, one per CU) ~0.98x a pair. 3000^3: 576
-        // tiles of 128x128 leave 64 CUs a third tile, 533 us against 470 us
-        // on 2209 tiles of 64x64. 4096^3: 939-940 us on 512 tiles of 128x256
-        // against 952-960 us on 1024 of 128x128 (8192^3 7411 against 7519
-        // us); 6000^3 stays on 128x128 (3157 us against 3437 us for 1128
-        // tiles of 128x256, five rounds of one per CU), and so does 2048^3
-        // (one tile per CU, 141 us against 153 us on 64x64).
-        auto cu_time = [&](int64_t n_tiles) {
-          const int64_t n = (n_tiles + ds.cus - 1) / ds.cus;
-          return (double)(n / 2) * 2.0 * 0.94 + (double)(n % 2);
-        };
-        const double t128 = cu_time(tiles);
-        int c64 = -1, cwide = -1;
-        for (int t : {37, 39})
-          if (c64 < 0 && fits(t)) c64 = t;
-        for (int t : {41, 42})
-          if (cwide < 0 && fits(t)) cwide = t;
-        double t64 = 1e30, twide = 1e30;
-        if (c64 >= 0) t64 = 0.27 * cu_time((int64_t)((M + 63) / 64) * ((N + 63) / 64));
-        if (cwide >= 0) {
-          const int64_t tw = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
-          if (tw >= ds.cus) twide = (double)((tw + ds.cus - 1) / ds.cus) * 2.0 * 0.94 * 0.98;
-        }
-        if (twide <= t128 && twide <= t64) {
-          cfg = cwide;
-          break;
-        }
-        if (t64 < t128) continue;
-        // Exactly one 128x128 tile per CU: its eight-wave layout (two waves
-        // per SIMD to cover each other's waits; 2048^3 137 against 139-141
-        // us, 2000^3 137 against 141 us).
-        if (tiles == ds.cus) {
-          int c8 = -1;
-          for (int t : {43, 44})
-            if (c8 < 0 && fits(t)) c8 = t;
-          if (c8 >= 0) {
-            cfg = c8;
-            break;
-          }
-        }
-      }
-      if (tiles >= ds.cus) {
-        // Tiles larger than 64x64 that need more than one round of
-        // workgroups are taken only when the last round keeps at least
-        // three quarters of the CUs busy (4097x4096: 272 tiles of 256x256
-        // would take two rounds of 4096^3-sized work).
-        const int64_t rounds = (tiles + ds.cus - 1) / ds.cus;
-        if (g.bm * g.bn > 64 * 64 && 4 * tiles < 3 * rounds * ds.cus) {
-          if (first_rejected < 0) first_rejected = c;
-          continue;
-        }
-        cfg = c;
-        break;
-      }
-      if (tiles > best_tiles) {
-        best_tiles = tiles;
-        best = c;
-      }
-    }
-    if (cfg < 0) cfg = best >= 0 ? best : first_rejected;
-  }
-  if (cfg < 0) cfg = 4;  // guarded: any shape and alignment
+  static_assert(kF32SmallM == kGemvMaxM, "the tile planner's small-M rule covers the small-M kernel's rows");
+  const int cfg = plan_f32_tile(F32TileQuery{M, N, K, aligned, ds.cus, g_force_cfg});
   const GemmF32Config& g = gemm_f32_config(cfg);
   GemmF32Args a{};
   a.A = static_cast<const float*>(L.x);
@@ -618,6 +495,8 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
 
 void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
   if (epi_act(L.epi) == ACT_LEAKY) fail(kErrDtype, "leaky_relu is float-only");
+  // On integers If(v > 0, v, 0) is the ReLU: the select codes run as it.
+  const int epi = epi_act(L.epi) == ACT_IF_RELU ? epi_code(epi_has_bias(L.epi), ACT_RELU) : L.epi;
   GemmI32Args a{};
   a.X = static_cast<const int32_t*>(L.x);
   a.W = static_cast<const int32_t*>(L.w);
@@ -666,13 +545,13 @@ void launch_i32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream) {
     a.flags_x = flags;
     a.flags_w = flags + fx;
     const int variant = (g_force_i8 >= 0 && g_force_i8 < kI8Variants) ? g_force_i8 : kI8DefaultVariant;
-    check_hip(launch_gemm_i8(L.epi, a, stream, variant), "gemm_i8 launch");
+    check_hip(launch_gemm_i8(epi, a, stream, variant), "gemm_i8 launch");
     scratch_end(ds, stream);
     set_plan("narrow_i8+gemm_i8 variant=%d waves=%s depth=%d grid=%d", variant, gemm_i8_layout(variant),
              gemm_i8_depth(variant, Kp),
              (Mp / kI8Tile) * (Np / kI8Tile));
   } else {
-    check_hip(launch_gemm_i32_valu(L.epi, a, stream), "gemm_i32_valu launch");
+    check_hip(launch_gemm_i32_valu(epi, a, stream), "gemm_i32_valu launch");
     set_plan("gemm_i32_valu grid=%d", ((a.M + 127) / 128) * ((a.N + 127) / 128));
   }
 }
@@ -683,7 +562,7 @@ void launch_dense(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, con
     set_plan("empty");
     return;
   }
-  if (L.epi < 0 || L.epi > 5) fail(kErrArgument, "bad epilogue code %d", L.epi);
+  if (L.epi < 0 || L.epi > 7) fail(kErrArgument, "bad epilogue code %d", L.epi);
   if (L.dtype == EDSL_DTYPE_F32)
     launch_f32(ds, L, stream, fixed);
   else if (L.dtype == EDSL_DTYPE_I32 && !fixed)
@@ -1000,7 +879,7 @@ std::shared_ptr<ResidentCopy> make_resident_copy(const void* src, int64_t rows, 
 
 void dense_f32_launch(const float* X, int64_t ldx, const float* W, int64_t ldw, const float* bias, float* Y,
                       int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, float alpha, void* stream,
-                      const FixedScratch* fixed) {
+                      const FixedScratch* fixed, const float* plan_bias) {
   if (epi_has_bias(epilogue) && !bias && N > 0) fail(kErrArgument, "epilogue adds a bias but bias is null");
   if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) fail(kErrArgument, "null operand");
   if (K > 0 && M > 1 && ldx < K) fail(kErrStride, "ldx < K");
@@ -1011,6 +890,7 @@ void dense_f32_launch(const float* X, int64_t ldx, const float* W, int64_t ldw, 
   read_env_overrides();
   DeviceState& ds = device_state(nullptr);
   DenseLaunch L{EDSL_DTYPE_F32, epilogue, alpha, X, ldx, W, ldw, bias, Y, ldy, M, N, K};
+  L.plan_bias = plan_bias;
   launch_dense(ds, L, static_cast<hipStream_t>(stream), fixed);
 }
 
@@ -1094,6 +974,19 @@ void edsl_hip_dense_leaky_relu_f32(MEMREF2(float, X), MEMREF2(float, W), MEMREF1
   });
 }
 
+void edsl_hip_dense_if_relu_f32(MEMREF2(float, X), MEMREF2(float, W), MEMREF1(float, b), MEMREF2(float, Y)) {
+  (void)X_allocated; (void)W_allocated; (void)b_allocated; (void)Y_allocated;
+  guarded([&] {
+    const Vec bv = VEC(b, "b");
+    sync_dense(EDSL_DTYPE_F32, EDSL_EPI_BIAS_IF_RELU, 0.f, MAT(X, "X"), MAT(W, "W"), &bv, MAT(Y, "Y"));
+  });
+}
+
+void edsl_hip_matmul_if_relu_f32(MEMREF2(float, A), MEMREF2(float, B), MEMREF2(float, C)) {
+  (void)A_allocated; (void)B_allocated; (void)C_allocated;
+  guarded([&] { sync_dense(EDSL_DTYPE_F32, EDSL_EPI_IF_RELU, 0.f, MAT(A, "A"), MAT(B, "B"), nullptr, MAT(C, "C")); });
+}
+
 int edsl_hip_execute_gpu_function(int pattern, int dtype, int num_inputs, const void* const* input_ptrs,
                                   const int64_t* const* input_shapes, const int* input_ranks, void* output,
                                   const int64_t* output_shape, int output_rank, size_t element_size,
@@ -1109,6 +1002,8 @@ int edsl_hip_execute_gpu_function(int pattern, int dtype, int num_inputs, const 
       case EDSL_PATTERN_MATMUL_BIAS: epi = EDSL_EPI_BIAS; break;
       case EDSL_PATTERN_DENSE_RELU: epi = EDSL_EPI_BIAS_RELU; break;
       case EDSL_PATTERN_DENSE_LEAKY: epi = EDSL_EPI_BIAS_LEAKY; break;
+      case EDSL_PATTERN_DENSE_IF_RELU: epi = EDSL_EPI_BIAS_IF_RELU; break;
+      case EDSL_PATTERN_MATMUL_IF_RELU: epi = EDSL_EPI_IF_RELU; want_inputs = 2; break;
       default: fail(kErrArgument, "unknown pattern %d", pattern);
     }
     if (num_inputs != want_inputs)
@@ -1152,7 +1047,7 @@ int edsl_hip_dense_f32_launch_unfused(const float* X, int64_t ldx, const float* 
                                       int epilogue, float alpha, void* stream) {
   return guarded([&] {
     // The checks of dense_f32_launch, before the fill touches Y.
-    if (epilogue < 0 || epilogue > 5) fail(kErrArgument, "bad epilogue code %d", epilogue);
+    if (epilogue < 0 || epilogue > 7) fail(kErrArgument, "bad epilogue code %d", epilogue);
     check_dims(M, N, K);
     if (epi_has_bias(epilogue) && !bias && N > 0) fail(kErrArgument, "epilogue adds a bias but bias is null");
     if (M > 0 && N > 0 && (!Y || (K > 0 && (!X || !W)))) fail(kErrArgument, "null operand");
@@ -1162,7 +1057,10 @@ int edsl_hip_dense_f32_launch_unfused(const float* X, int64_t ldx, const float* 
     if (M <= 1) ldy = N;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (M > 0 && N > 0) check_hip(launch_fill_zero_f32(Y, ldy, (int)M, (int)N, s), "fill launch");
-    dense_f32_launch(X, ldx, W, ldw, nullptr, Y, ldy, M, N, K, EDSL_EPI_NONE, 0.f, stream, nullptr);
+    // The GEMM plans as the fused launch with this bias would, so that both
+    // run the same kernel (and give the same bits).
+    dense_f32_launch(X, ldx, W, ldw, nullptr, Y, ldy, M, N, K, EDSL_EPI_NONE, 0.f, stream, nullptr,
+                     epi_has_bias(epilogue) ? bias : nullptr);
     const std::string gemm_plan = t_plan;
     if (M > 0 && N > 0) check_hip(launch_bias_act_f32(Y, ldy, bias, (int)M, (int)N, epilogue, alpha, s), "bias_act launch");
     set_plan("unfused: fill | %s | bias_act epi=%d", gemm_plan.c_str(), epilogue);

@@ -126,10 +126,12 @@ struct FixedScratch {
 };
 
 // Body of edsl_hip_dense_f32_launch (argument checks, plan, launch); with
-// `fixed` non-null every scratch buffer comes from it. Throws Failure.
+// `fixed` non-null every scratch buffer comes from it. `plan_bias`, when not
+// null, is a bias the epilogue does not add whose alignment the kernel
+// choice still honours (see DenseLaunch::plan_bias). Throws Failure.
 void dense_f32_launch(const float* X, int64_t ldx, const float* W, int64_t ldw, const float* bias, float* Y,
                       int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, float alpha, void* stream,
-                      const FixedScratch* fixed);
+                      const FixedScratch* fixed, const float* plan_bias = nullptr);
 
 }  // namespace rt
 }  // namespace edsl

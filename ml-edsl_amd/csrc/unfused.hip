@@ -93,6 +93,14 @@ hipError_t launch_bias_act_f32(float* Y, int64_t ldy, const float* bias, int M, 
       hipLaunchKernelGGL(bias_act_f32_kernel<epi_code(true, ACT_LEAKY)>, grid, block, 0, stream, Y, ldy, bias, M,
                          N, alpha, vec);
       break;
+    case epi_code(false, ACT_IF_RELU):
+      hipLaunchKernelGGL(bias_act_f32_kernel<epi_code(false, ACT_IF_RELU)>, grid, block, 0, stream, Y, ldy, bias, M,
+                         N, alpha, vec);
+      break;
+    case epi_code(true, ACT_IF_RELU):
+      hipLaunchKernelGGL(bias_act_f32_kernel<epi_code(true, ACT_IF_RELU)>, grid, block, 0, stream, Y, ldy, bias, M,
+                         N, alpha, vec);
+      break;
     default:
       return hipErrorInvalidValue;
   }

@@ -395,11 +395,13 @@ class MLIRCompiler:
                 raise ValueError("bind_parameter needs a C-contiguous array (calls must pass the same "
                                  "array for the snapshot to be used)")
             ptr, shape, itemsize = a.ctypes.data, list(a.shape), a.itemsize
+            array = (array, a)  # `a` may be a view np.asarray made of `array`
         if itemsize != 4:
             raise TypeError(f"element size {itemsize}: the dense path binds f32 and i32 parameters")
         dims = (ctypes.c_int64 * max(1, len(shape)))(*shape)
         if _L().edsl_hip_module_bind_parameter(self._m, name.encode(), idx, ptr, dims, len(shape)) != 0:
             _raise("bind_parameter")
+        self._bound[(name, idx)] = array
 
     def unbind_parameter(self, name: str, param=None) -> None:
         """Release the snapshot of `param` (name or position), or of every

@@ -11,8 +11,9 @@ import os
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libedsl_hip.so")
 
-EPI_NONE, EPI_BIAS, EPI_RELU, EPI_BIAS_RELU, EPI_LEAKY, EPI_BIAS_LEAKY = range(6)
-PATTERN_MATMUL, PATTERN_MATMUL_BIAS, PATTERN_DENSE_RELU, PATTERN_DENSE_LEAKY, PATTERN_MATMUL_RELU = range(5)
+EPI_NONE, EPI_BIAS, EPI_RELU, EPI_BIAS_RELU, EPI_LEAKY, EPI_BIAS_LEAKY, EPI_IF_RELU, EPI_BIAS_IF_RELU = range(8)
+(PATTERN_MATMUL, PATTERN_MATMUL_BIAS, PATTERN_DENSE_RELU, PATTERN_DENSE_LEAKY, PATTERN_MATMUL_RELU,
+ PATTERN_DENSE_IF_RELU, PATTERN_MATMUL_IF_RELU) = range(7)
 DTYPE_F32, DTYPE_I32 = 0, 1
 NOALLOC_SCRATCH_BYTES = 16 << 20  # EDSL_NOALLOC_SCRATCH_BYTES (include/edsl_hip_device.h)
 
@@ -32,6 +33,8 @@ MEMREF_ENTRY_POINTS = {
     "edsl_hip_dense_relu_f32": MEMREF2 * 2 + MEMREF1 + MEMREF2,
     "edsl_hip_dense_relu_i32": MEMREF2 * 2 + MEMREF1 + MEMREF2,
     "edsl_hip_dense_leaky_relu_f32": MEMREF2 * 2 + MEMREF1 + MEMREF2 + [ctypes.c_float],
+    "edsl_hip_dense_if_relu_f32": MEMREF2 * 2 + MEMREF1 + MEMREF2,
+    "edsl_hip_matmul_if_relu_f32": MEMREF2 * 3,
 }
 
 

@@ -17,7 +17,8 @@ Operands may be numpy arrays (host memory: copied in and out by the library)
 or torch tensors on the GPU (used in place; the output is then a GPU tensor).
 
 A function is bound to one of the dense-path patterns when it is compiled:
-``matmul``, ``matmul_relu``, ``matmul_bias``, ``dense_relu``, ``dense_leaky``.
+``matmul``, ``matmul_relu``, ``matmul_bias``, ``dense_relu``, ``dense_leaky``,
+and the f32 If-ReLU map forms ``dense_if_relu`` and ``matmul_if_relu``.
 """
 from __future__ import annotations
 
@@ -70,6 +71,9 @@ PATTERNS = {
     "matmul_bias": (True, "none", 3),
     "dense_relu": (True, "relu", 3),
     "dense_leaky": (True, "leaky", 3),
+    # tensor_map(... , lambda v: If(v > 0.0, v, 0.0)) over f32: NaN and -0 give +0
+    "dense_if_relu": (True, "if_relu", 3),
+    "matmul_if_relu": (False, "if_relu", 2),
 }
 
 _SYMBOLS = {
@@ -82,6 +86,8 @@ _SYMBOLS = {
     ("dense_relu", f32): "edsl_hip_dense_relu_f32",
     ("dense_relu", i32): "edsl_hip_dense_relu_i32",
     ("dense_leaky", f32): "edsl_hip_dense_leaky_relu_f32",
+    ("dense_if_relu", f32): "edsl_hip_dense_if_relu_f32",
+    ("matmul_if_relu", f32): "edsl_hip_matmul_if_relu_f32",
 }
 
 _PATTERN_CODES = {
@@ -90,12 +96,14 @@ _PATTERN_CODES = {
     "matmul_bias": _native.PATTERN_MATMUL_BIAS,
     "dense_relu": _native.PATTERN_DENSE_RELU,
     "dense_leaky": _native.PATTERN_DENSE_LEAKY,
+    "dense_if_relu": _native.PATTERN_DENSE_IF_RELU,
+    "matmul_if_relu": _native.PATTERN_MATMUL_IF_RELU,
 }
 
 
 def epilogue_code(pattern: str) -> int:
     bias, act, _ = PATTERNS[pattern]
-    return (1 if bias else 0) | ({"none": 0, "relu": 1, "leaky": 2}[act] << 1)
+    return (1 if bias else 0) | ({"none": 0, "relu": 1, "leaky": 2, "if_relu": 3}[act] << 1)
 
 
 @dataclass
@@ -374,12 +382,15 @@ def matmul(A, B):
 
 
 def dense(X, W, b=None, act: str = "relu", alpha: float = 0.01):
-    """act(X @ W (+ b)) with act in {'none', 'relu', 'leaky'}."""
+    """act(X @ W (+ b)) with act in {'none', 'relu', 'leaky', 'if_relu'}
+    ('if_relu': the f32 map body If(v > 0.0, v, 0.0))."""
     if b is None:
         if act == "none":
             return run("matmul", X, W)
         if act == "relu":
             return run("matmul_relu", X, W)
+        if act == "if_relu":
+            return run("matmul_if_relu", X, W)
         raise ValueError("leaky_relu without bias is not a dense-path pattern")
-    pattern = {"none": "matmul_bias", "relu": "dense_relu", "leaky": "dense_leaky"}[act]
+    pattern = {"none": "matmul_bias", "relu": "dense_relu", "leaky": "dense_leaky", "if_relu": "dense_if_relu"}[act]
     return run(pattern, X, W, b, alpha=alpha)

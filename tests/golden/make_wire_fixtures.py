@@ -244,8 +244,14 @@ def load_reference_front_end():
 
 # ---------------------------------------------------------------- programs
 def programs(E):
-    """(fixture name, python function, expected decode or rejection)."""
-    Tensor, f32, i32 = E.Tensor, E.f32, E.i32
+    """(fixture name, python function, expected decode or rejection[, calls]).
+
+    `calls`, for functions declared with DYN dimensions, lists the argument
+    shapes of each call: the front end compiles one specialisation per shape
+    (reference mlir_edsl/functions/decorator.py:79-107) under a name with the
+    shapes appended (mlir_edsl/functions/signature.py:98-104), each written
+    as its own fixture; `expected` then maps the shapes to the decode."""
+    Tensor, f32, i32, DYN = E.Tensor, E.f32, E.i32, E.DYN
     relu, leaky_relu, tensor_map, If, matmul = E.relu, E.leaky_relu, E.tensor_map, E.If, E.matmul
     out = []
 
@@ -306,9 +312,53 @@ def programs(E):
         return tensor_map(X @ W, lambda v: v * 2.0)
     out.append(("reject_map_scale", map_scale, {"reject": "tensor_map body is not If"}))
 
+    # The f32 ReLU as a map with an If body (reference LinalgBuilder.cpp:141-178):
+    # cmpf ogt selects v or +0.0, so NaN and -0 give +0.
     def f32_if_relu(X: Tensor[f32, 4, 4], W: Tensor[f32, 4, 4]) -> Tensor[f32, 4, 4]:
         return tensor_map(X @ W, lambda v: If(v > 0.0, v, 0.0))
-    out.append(("reject_f32_if_relu", f32_if_relu, {"reject": "maps NaN to 0"}))
+    out.append(("matmul_if_relu_f32", f32_if_relu, {"form": "tensor_map(X @ W, lambda v: If(v > 0.0, v, 0.0))",
+                                                    "dtype": "f32", "x": 0, "w": 1, "b": -1, "epilogue": 6}))
+
+    def f32_if_relu_bias(X: Tensor[f32, 24, 40], W: Tensor[f32, 40, 16], b: Tensor[f32, 16]) -> Tensor[f32, 24, 16]:
+        return tensor_map(X @ W + b, lambda v: If(v > 0.0, v, 0.0))
+    out.append(("dense_if_relu_f32", f32_if_relu_bias, {
+        "form": "tensor_map(X @ W + b, lambda v: If(v > 0.0, v, 0.0))", "dtype": "f32", "x": 0, "w": 1, "b": 2,
+        "epilogue": 7}))
+
+    # If(v <= 0, 0, v) over f32 is arith.maximumf exactly (NaN propagates, -0 -> +0)
+    def f32_le_relu(X: Tensor[f32, 8, 16], W: Tensor[f32, 16, 8], b: Tensor[f32, 8]) -> Tensor[f32, 8, 8]:
+        return tensor_map(X @ W + b, lambda v: If(v <= 0.0, 0.0, v))
+    out.append(("dense_relu_f32_tensor_map_le", f32_le_relu, {"form": "relu(X @ W + b)", "dtype": "f32", "x": 0,
+                                                              "w": 1, "b": 2, "epilogue": 3}))
+
+    # If(v >= 0, v, 0) over f32 keeps -0: no fused epilogue computes it
+    def f32_ge_relu(X: Tensor[f32, 4, 4], W: Tensor[f32, 4, 4]) -> Tensor[f32, 4, 4]:
+        return tensor_map(X @ W, lambda v: If(v >= 0.0, v, 0.0))
+    out.append(("reject_f32_if_ge_relu", f32_ge_relu, {"reject": "keeps -0"}))
+
+    # DYN-declared functions: one specialisation per call shape
+    # (reference tests/linalg/test_linalg_dyn.py:86-95)
+    def dyn_dense(X: Tensor[f32, DYN, DYN], W: Tensor[f32, DYN, DYN], b: Tensor[f32, DYN]) -> Tensor[f32, DYN, DYN]:
+        return relu(X @ W + b)
+    dyn_calls = [[(16, 64), (64, 32), (32,)], [(40, 24), (24, 48), (48,)]]
+    out.append(("dyn_dense_relu_f32", dyn_dense, {
+        "16x64x32": {"form": "relu(X @ W + b)", "dtype": "f32", "x": 0, "w": 1, "b": 2, "epilogue": 3},
+        "40x24x48": {"form": "relu(X @ W + b)", "dtype": "f32", "x": 0, "w": 1, "b": 2, "epilogue": 3}},
+        dyn_calls))
+
+    def dyn_matmul(A: Tensor[f32, DYN, DYN], B: Tensor[f32, DYN, DYN]) -> Tensor[f32, DYN, DYN]:
+        return matmul(A, B)
+    out.append(("dyn_matmul_f32", dyn_matmul, {
+        "2x2x2": {"form": "A @ B", "dtype": "f32", "x": 0, "w": 1, "b": -1, "epilogue": 0},
+        "33x17x65": {"form": "A @ B", "dtype": "f32", "x": 0, "w": 1, "b": -1, "epilogue": 0}},
+        [[(2, 2), (2, 2)], [(33, 17), (17, 65)]]))
+
+    def dyn_int_dense(X: Tensor[i32, DYN, DYN], W: Tensor[i32, DYN, DYN], b: Tensor[i32, DYN]) -> Tensor[i32, DYN, DYN]:
+        return tensor_map(X @ W + b, lambda v: If(v > 0, v, 0))
+    out.append(("dyn_dense_relu_i32", dyn_int_dense, {
+        "8x16x24": {"form": "relu(X @ W + b)", "dtype": "i32", "x": 0, "w": 1, "b": 2, "epilogue": 3},
+        "130x64x40": {"form": "relu(X @ W + b)", "dtype": "i32", "x": 0, "w": 1, "b": 2, "epilogue": 3}},
+        [[(8, 16), (16, 24), (24,)], [(130, 64), (64, 40), (40,)]]))
 
     def relu_of_param(X: Tensor[f32, 4, 4]) -> Tensor[f32, 4, 4]:
         return relu(X)
@@ -375,51 +425,83 @@ def programs(E):
     return out
 
 
-def sample_args(fn):
+def sample_args(fn, shapes=None):
     args = []
-    for name, t in list(fn.__annotations__.items()):
-        if name == "return":
-            continue
+    params = [(n, t) for n, t in fn.__annotations__.items() if n != "return"]
+    for i, (name, t) in enumerate(params):
         if t is int:
             args.append(3)
             continue
-        shape = tuple(t.shape)
+        shape = tuple(shapes[i]) if shapes is not None else tuple(t.shape)
         dt = np.float32 if t.element_type.name == "f32" else np.int32
         args.append(np.zeros(shape, dtype=dt))
     return args
+
+
+def front_end_rejections(E):
+    """Calls the front end refuses before serializing anything: the reference
+    raises at specialisation, so no FunctionDef reaches a backend (reference
+    tests/linalg/test_linalg_dyn.py:72-80). Recorded with the message."""
+    Tensor, f32, DYN, matmul = E.Tensor, E.f32, E.DYN, E.matmul
+
+    def dyn_mismatch(A: Tensor[f32, DYN, DYN], B: Tensor[f32, DYN, DYN]) -> Tensor[f32, DYN, DYN]:
+        return matmul(A, B)
+    out = []
+    fn = E.ml_function(target="gpu")(dyn_mismatch)
+    shapes = [(2, 3), (4, 2)]
+    try:
+        fn(*sample_args(dyn_mismatch, shapes))
+        raise RuntimeError("the front end accepted mismatched inner dimensions")
+    except TypeError as e:
+        out.append({"case": "dyn_matmul_inner_mismatch", "source": textwrap.dedent(inspect.getsource(dyn_mismatch)).strip(),
+                    "arg_shapes": [list(s) for s in shapes], "error": "TypeError", "message": str(e),
+                    "serialized": sorted(Recorder.compiled).count(fn.signature.name) > 0})
+    return out
 
 
 def main():
     E = load_reference_front_end()
     os.makedirs(OUT_DIR, exist_ok=True)
     index = []
-    for fixture, pyfn, expected in programs(E):
+    for fixture, pyfn, expected, *calls in programs(E):
         mlfn = E.ml_function(target="gpu")(pyfn)
-        args = sample_args(pyfn)
-        err = None
-        try:
-            mlfn(*args)
-        except Exception as e:  # the recorder still saw compile_function
-            err = f"{type(e).__name__}: {e}"
-        name = mlfn.signature.name
-        data = Recorder.compiled.get(name)
-        if data is None:
-            raise RuntimeError(f"{fixture}: the front end did not serialize {name} ({err})")
-        with open(os.path.join(OUT_DIR, f"{fixture}.pb"), "wb") as f:
-            f.write(data)
-        entry = {"fixture": fixture, "file": f"wire/{fixture}.pb", "function": name,
-                 "source": textwrap.dedent(inspect.getsource(pyfn)).strip(),
-                 "param_shapes": [list(a.shape) if hasattr(a, "shape") else [] for a in args],
-                 "param_dtypes": [str(a.dtype) if hasattr(a, "dtype") else "int" for a in args],
-                 "expected": expected}
-        if name in Recorder.gpu_calls:
-            entry["execute_gpu_function"] = Recorder.gpu_calls[name]
-        index.append(entry)
-        print(f"{fixture}: {name}, {len(data)} bytes", flush=True)
+        variants = [(fixture, None, expected)]
+        if calls:  # DYN: one fixture per specialisation
+            variants = []
+            for shapes in calls[0]:
+                key = "x".join(str(d) for d in (shapes[0][0], shapes[0][1], shapes[1][1]))
+                variants.append((f"{fixture}__{key}", shapes, expected[key]))
+        for name_fx, shapes, exp in variants:
+            args = sample_args(pyfn, shapes)
+            before = set(Recorder.compiled)
+            err = None
+            try:
+                mlfn(*args)
+            except Exception as e:  # the recorder still saw compile_function
+                err = f"{type(e).__name__}: {e}"
+            new = sorted(set(Recorder.compiled) - before)
+            name = new[0] if len(new) == 1 else mlfn.signature.name
+            data = Recorder.compiled.get(name)
+            if data is None:
+                raise RuntimeError(f"{name_fx}: the front end did not serialize {name} ({err})")
+            with open(os.path.join(OUT_DIR, f"{name_fx}.pb"), "wb") as f:
+                f.write(data)
+            entry = {"fixture": name_fx, "file": f"wire/{name_fx}.pb", "function": name,
+                     "source": textwrap.dedent(inspect.getsource(pyfn)).strip(),
+                     "param_shapes": [list(a.shape) if hasattr(a, "shape") else [] for a in args],
+                     "param_dtypes": [str(a.dtype) if hasattr(a, "dtype") else "int" for a in args],
+                     "expected": exp}
+            if shapes is not None:
+                entry["declared_dyn"] = True
+            if name in Recorder.gpu_calls:
+                entry["execute_gpu_function"] = Recorder.gpu_calls[name]
+            index.append(entry)
+            print(f"{name_fx}: {name}, {len(data)} bytes", flush=True)
     with open(os.path.join(HERE, "wire_fixtures.json"), "w") as f:
         json.dump({"generator": "tests/golden/make_wire_fixtures.py (reference front end, "
                                 "mlir_edsl/backend.py serialization)",
-                   "schema": "cpp/schemas/ast.proto", "cases": index}, f, indent=1)
+                   "schema": "cpp/schemas/ast.proto", "cases": index,
+                   "front_end_rejections": front_end_rejections(E)}, f, indent=1)
 
 
 if __name__ == "__main__":

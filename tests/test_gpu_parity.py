@@ -519,6 +519,35 @@ def test_nan_and_inf_propagate_like_maximumf(torch_cuda):
         check(got, ref, K)
 
 
+@pytest.mark.parametrize("shape", [(16, 1024, 512), (256, 256, 256), (300, 101, 259), (1, 64, 8)],
+                         ids=["small-M", "tiles", "any-shape", "one-row"])
+def test_if_relu_maps_nan_and_negative_zero_to_zero(shape, torch_cuda):
+    """The f32 If(v > 0.0, v, 0.0) epilogue on every kernel family: NaN
+    inputs and -0 sums give +0 (cmpf ogt), where maximumf keeps the NaN;
+    every element against the oracle's If epilogue on both chains."""
+    import torch
+    from mlir_edsl_hip.device import dense_launch
+    M, K, N = shape
+    rng = np.random.default_rng(M + K + N)
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.float32(np.sqrt(K))).astype(np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    X[0, K // 2] = np.nan                 # row 0: NaN sums
+    b[N // 2] = np.nan                    # one NaN column
+    b[-1] = -0.0
+    if M > 1:
+        X[M - 1, :] = 0.0                 # last row: +0 + -0 = +0 in the last column
+    tX, tW, tb = to_dev(torch, [X, W, b])
+    for epi, bias in ((_native.EPI_BIAS_IF_RELU, b), (_native.EPI_IF_RELU, None)):
+        Y = torch.full((M, N), 7.0, device="cuda")
+        dense_launch(tX, tW, tb if bias is not None else None, Y, epi)
+        torch.cuda.synchronize()
+        got = Y.cpu().numpy()
+        assert not np.isnan(got).any() and not np.signbit(got).any(), _native.last_plan()
+        assert np.array_equal(got[0], np.zeros(N, np.float32))
+        check(got, oracle.dense_f32_chains(X, W, bias, "if_relu"), K)
+
+
 def test_execute_gpu_function_host_entry(torch_cuda):
     be = backend.get_backend()
     w = WORKLOADS["c2"]

@@ -292,3 +292,54 @@ def test_a_freed_bound_array_cannot_lend_its_address(torch_cuda):
     gc.collect()
     assert alive() is None, "unbinding keeps no reference"
     comp.clear()
+
+
+def test_dyn_specialisations_run_from_one_compiler(torch_cuda):
+    """Every shape variant of the DYN-declared functions (reference
+    tests/linalg/test_linalg_dyn.py:86-95: one compile per call shape, under
+    the shape-mangled name) compiled into one compiler, then each run through
+    its function pointer and through execute_gpu_function against the
+    oracle."""
+    comp = MLIRCompiler()
+    comp.set_target("gpu")
+    cases = [c for c in DENSE if c.get("declared_dyn")]
+    assert len(cases) == 6
+    for c in cases:
+        comp.compile_function(open(os.path.join(GOLDEN, c["file"]), "rb").read())
+    for i, c in enumerate(cases):
+        name = c["function"]
+        form = comp.function_form(name)
+        K = c["param_shapes"][0][1]
+        args = _inputs(c, 40 + i, wide=True)
+        ref = _reference(form, args)
+        like = _arr(ref)
+        print(f"{name}: {form['form']} {like.shape}", flush=True)
+        out = np.empty(like.shape, like.dtype)
+        _call_pointer(comp.get_function_pointer(name), args, out)
+        _check(out, ref, K)
+        raw = comp.execute_gpu_function(name, [(a.ctypes.data, list(a.shape)) for a in args], list(like.shape), 4)
+        _check(np.frombuffer(raw, dtype=like.dtype).reshape(like.shape), ref, K)
+    comp.clear()
+
+
+def test_f32_if_relu_program_maps_nan_and_negative_zero_to_zero(torch_cuda):
+    """tensor_map(X @ W + b, lambda v: If(v > 0.0, v, 0.0)) from the front
+    end's bytes: NaN rows and -0 sums come out +0, bit for bit with the
+    oracle's If epilogue (reference LinalgBuilder.cpp:141-178, cmpf ogt)."""
+    c = next(c for c in DENSE if c["fixture"] == "dense_if_relu_f32")
+    comp = MLIRCompiler()
+    comp.set_target("gpu")
+    comp.compile_function(open(os.path.join(GOLDEN, c["file"]), "rb").read())
+    X, W, b = _inputs(c, 9)
+    X[3, :] = np.nan                    # a NaN row: maximumf would keep NaN
+    X[5, :] = 0.0
+    b[:4] = -0.0                        # row 5: 0 * w sums to +0; +0 + -0 = +0
+    X[7, :] = np.float32(-1e-30)        # tiny negative sums underflow toward -0
+    W[:, 0] = np.float32(1e-30)
+    ref = oracle.dense_f32_chains(X, W, b, "if_relu")
+    out = np.empty(ref.fma.shape, np.float32)
+    _call_pointer(comp.get_function_pointer(c["function"]), (X, W, b), out)
+    assert not np.isnan(out).any() and not np.signbit(out).any()
+    assert np.array_equal(out[3], np.zeros_like(out[3]))
+    _check(out, ref, X.shape[1])
+    comp.clear()

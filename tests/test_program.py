@@ -466,3 +466,97 @@ def test_bind_parameter_validates_before_any_device_call(compiler):
     compiler.unbind_parameter(name)  # nothing bound: a no-op
     with pytest.raises(RuntimeError, match="no parameter 5"):
         compiler.unbind_parameter(name, 5)
+
+
+# ------------------------------------------- DYN-declared functions
+def test_dyn_specialisations_compile_side_by_side(compiler):
+    """A function declared with DYN dimensions is compiled once per call
+    shape, under its name with the shapes appended (reference
+    mlir_edsl/functions/signature.py:98-104, decorator.py:79-107). Both
+    specialisations the front end serialized live in one compiler, each with
+    its own concrete types and the dense form of the body."""
+    for base in ("dyn_dense_relu_f32", "dyn_matmul_f32", "dyn_dense_relu_i32"):
+        cases = [c for c in _cases() if c["fixture"].startswith(base + "__")]
+        assert len(cases) == 2 and all(c.get("declared_dyn") for c in cases)
+        stems = {c["function"].split("__")[0] for c in cases}
+        assert len(stems) == 1, stems  # one DSL function, two variants
+        for c in cases:
+            compiler.compile_function(_bytes(c))
+        ir = compiler.get_module_ir()
+        for c in cases:
+            form = compiler.function_form(c["function"])
+            assert form["form"] == c["expected"]["form"] and form["dtype"] == c["expected"]["dtype"]
+            (M, K), N = c["param_shapes"][0], c["param_shapes"][1][1]
+            assert c["function"].endswith("__" + "__".join("_".join(map(str, s)) for s in c["param_shapes"]))
+            dt = c["expected"]["dtype"]
+            assert f"tensor<{M}x{K}x{dt}>" in ir and f"tensor<{M}x{N}x{dt}>" in ir
+    assert len(compiler.list_functions()) == 6
+
+
+def test_inner_dimension_mismatch_is_rejected_like_the_front_end(compiler):
+    """The front end refuses a DYN matmul called with mismatched inner
+    dimensions before serializing anything (reference
+    tests/linalg/test_linalg_dyn.py:72-80, message recorded by the fixture
+    generator). A FunctionDef that carries such shapes anyway (written here
+    field by field) is refused by the decoder with the same words."""
+    from mlir_edsl_hip import wire
+    with open(os.path.join(GOLDEN, "wire_fixtures.json")) as f:
+        rej = json.load(f)["front_end_rejections"]
+    case = next(r for r in rej if r["case"] == "dyn_matmul_inner_mismatch")
+    assert case["error"] == "TypeError" and not case["serialized"]
+    assert "inner dimensions must match" in case["message"]
+    tA, tB, tC = wire.tensor_type((2, 3), "f32"), wire.tensor_type((4, 2), "f32"), wire.tensor_type((2, 2), "f32")
+    node = wire._linalg(2, wire._len(1, wire._param_node("A", tA)) + wire._len(2, wire._param_node("B", tB)) +
+                        wire._len(3, tC))
+    fdef = (wire._len(1, b"mismatch_0__2_3__4_2") + wire._len(2, wire._len(1, b"A") + wire._len(2, tA)) +
+            wire._len(2, wire._len(1, b"B") + wire._len(2, tB)) + wire._len(3, tC) + wire._len(4, node))
+    with pytest.raises(RuntimeError, match="inner dimensions must match"):
+        compiler.compile_function(fdef)
+    assert compiler.list_functions() == []
+
+
+def test_f32_if_relu_forms_decode_by_their_float_semantics(compiler):
+    """tensor_map If bodies over f32: v > 0 ? v : 0 is the If-ReLU epilogue
+    (NaN and -0 give +0), v <= 0 ? 0 : v is arith.maximumf exactly, and the
+    forms that keep -0 are refused."""
+    got = {}
+    for fx in ("matmul_if_relu_f32", "dense_if_relu_f32", "dense_relu_f32_tensor_map_le"):
+        c = _case(fx)
+        compiler.compile_function(_bytes(c))
+        got[fx] = compiler.function_form(c["function"])["epilogue"]
+    assert got == {"matmul_if_relu_f32": 6, "dense_if_relu_f32": 7, "dense_relu_f32_tensor_map_le": 3}
+    c = _case("reject_f32_if_ge_relu")
+    with pytest.raises(RuntimeError, match="keeps -0"):
+        compiler.compile_function(_bytes(c))
+
+
+def test_bound_array_is_held_until_unbound(compiler, monkeypatch):
+    """The facade keeps the bound object alive while its snapshot is matched
+    by address, and lets go on unbind, rebind and clear. (The device copy is
+    stubbed out: this checks the facade's bookkeeping only.)"""
+    import gc
+    import weakref
+    from mlir_edsl_hip import _mlir_backend as mb
+    L = mb._L()
+    monkeypatch.setattr(L, "edsl_hip_module_bind_parameter", lambda *a: 0)
+    case = _case("dense_relu_f32")
+    compiler.compile_function(_bytes(case))
+    name = case["function"]
+
+    def bound(param):
+        a = np.ones(case["param_shapes"][compiler._param_index(name, param)], np.float32)
+        compiler.bind_parameter(name, param, a)
+        return weakref.ref(a)
+
+    w, b = bound("W"), bound("b")
+    gc.collect()
+    assert w() is not None and b() is not None
+    compiler.unbind_parameter(name, "W")
+    gc.collect()
+    assert w() is None and b() is not None
+    b2 = bound("b")  # rebinding releases the previous object
+    gc.collect()
+    assert b() is None and b2() is not None
+    compiler.clear()
+    gc.collect()
+    assert b2() is None

@@ -18,25 +18,26 @@ from mlir_edsl_hip._mlir_backend import MLIRCompiler
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 L = wire.Layer
 
-# fixture -> the same program written with the encoder
+# fixture -> the same program written with the encoder, given the mangled
+# function name the front end chose (f"{name}_{id}", the id from a
+# process-wide counter; recorded in the fixture index)
 PROGRAMS = {
-    "dense_relu_f32": lambda: wire.dense_layer("dense_relu_0", 16, 64, 32),
-    "matmul_bias_f32": lambda: wire.dense_layer("dense_bias_1", 8, 24, 40, act="none"),
-    "matmul_f32": lambda: wire.dense_layer("mm_2", 32, 48, 16, bias=False, act="none"),
-    "matmul_i32": lambda: wire.dense_layer("mm_op_3", 4, 4, 4, "i32", bias=False, act="none"),
-    "matmul_relu_f32": lambda: wire.dense_layer("mm_relu_4", 64, 64, 64, bias=False),
-    "dense_leaky_f32": lambda: wire.dense_layer("leaky_5", 16, 32, 64, act="leaky", alpha=0.2),
-    "dense_leaky_default_f32": lambda: wire.dense_layer("leaky_default_6", 16, 32, 64, act="leaky"),
-    "dense_relu_f32_1024": lambda: wire.dense_layer("bench_dense_11", 1024, 1024, 1024),
-    "chain_two_layer_net": lambda: wire.dense_program(
-        "two_layer_18", ("X", 2, 4), [L("W1", 8, "b1", "relu"), L("W2", 3, "b2", "relu")]),
-    "chain_three_layer_net": lambda: wire.dense_program(
-        "three_layer_19", ("X", 4, 8), [L("W1", 16, "b1", "relu"), L("W2", 8, "b2", "relu"),
-                                        L("W3", 4, "b3", "relu")]),
-    "chain_relu_no_bias": lambda: wire.dense_program(
-        "chained_20", ("X", 4, 4), [L("W1", 4, None, "relu"), L("W2", 4, None, "relu")]),
-    "chain_relu_then_leaky": lambda: wire.dense_program(
-        "mixed_21", ("X", 64, 128), [L("W1", 256, "b1", "relu"), L("W2", 64, None, "leaky", 0.1)]),
+    "dense_relu_f32": lambda n: wire.dense_layer(n, 16, 64, 32),
+    "matmul_bias_f32": lambda n: wire.dense_layer(n, 8, 24, 40, act="none"),
+    "matmul_f32": lambda n: wire.dense_layer(n, 32, 48, 16, bias=False, act="none"),
+    "matmul_i32": lambda n: wire.dense_layer(n, 4, 4, 4, "i32", bias=False, act="none"),
+    "matmul_relu_f32": lambda n: wire.dense_layer(n, 64, 64, 64, bias=False),
+    "dense_leaky_f32": lambda n: wire.dense_layer(n, 16, 32, 64, act="leaky", alpha=0.2),
+    "dense_leaky_default_f32": lambda n: wire.dense_layer(n, 16, 32, 64, act="leaky"),
+    "dense_relu_f32_1024": lambda n: wire.dense_layer(n, 1024, 1024, 1024),
+    "chain_two_layer_net": lambda n: wire.dense_program(
+        n, ("X", 2, 4), [L("W1", 8, "b1", "relu"), L("W2", 3, "b2", "relu")]),
+    "chain_three_layer_net": lambda n: wire.dense_program(
+        n, ("X", 4, 8), [L("W1", 16, "b1", "relu"), L("W2", 8, "b2", "relu"), L("W3", 4, "b3", "relu")]),
+    "chain_relu_no_bias": lambda n: wire.dense_program(
+        n, ("X", 4, 4), [L("W1", 4, None, "relu"), L("W2", 4, None, "relu")]),
+    "chain_relu_then_leaky": lambda n: wire.dense_program(
+        n, ("X", 64, 128), [L("W1", 256, "b1", "relu"), L("W2", 64, None, "leaky", 0.1)]),
 }
 
 
@@ -50,7 +51,7 @@ def _fixture(name):
 @pytest.mark.parametrize("fixture", sorted(PROGRAMS))
 def test_encoder_writes_the_front_end_bytes(fixture):
     case, data = _fixture(fixture)
-    assert PROGRAMS[fixture]() == data, case["source"]
+    assert PROGRAMS[fixture](case["function"]) == data, case["source"]
 
 
 @pytest.mark.parametrize("M, K, N, bias, act, form", [
