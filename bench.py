@@ -71,7 +71,7 @@ SECONDARY_PLAN = {"c4": (200, 20, 3), "c5": (200, 20, 10), "c2": (100, 20, 1), "
 ROTATE_X = {"c5"}           # workloads whose X is rotated together with W
 RESIDENT_TOO = {"c5"}       # also measured without rotation (inputs cache-resident)
 UNFUSED_TOO = {"c2", "c3"}  # also timed as the reference's unfused three-launch sequence
-LIBRARY_TOO = {"c2", "c3"}  # the vendor library's fp32 GEMM on the same operands, for reference
+LIBRARY_TOO = {"c2", "c3", "c5"}  # the vendor library's GEMM on the same operands, for reference
 
 
 def log(msg: str) -> None:
@@ -219,6 +219,39 @@ def measure_library(p: Prepared, steps: int, warmup: int) -> float:
     ev[0].record()
     for _ in range(steps):
         torch.mm(X, W, out=Y)
+    ev[1].record()
+    torch.cuda.synchronize()
+    return ev[0].elapsed_time(ev[1]) / steps
+
+
+def measure_library_int8(p: Prepared, steps: int, warmup: int) -> float:
+    """Device ms per launch of torch._int_mm (the vendor library's int8 GEMM,
+    i32 accumulation) on int8 copies of the workload's X and W, no bias or
+    activation, timed like kernel_ms_mean. The narrowing to int8 is not
+    included: this is the reference point for the GEMM half of the layer."""
+    import torch
+    X8, W8 = p.Xs[0].to(torch.int8), p.Ws[0].to(torch.int8)
+    out = torch.empty((p.w.M, p.w.N), dtype=torch.int32, device="cuda")
+
+    def run():
+        torch._int_mm(X8, W8, out=out)
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    rows = min(64, p.w.M)  # a row sample against exact float64 sums on the host (|sum| < 2^53)
+    want = (X8[:rows].cpu().double() @ W8.cpu().double()).to(torch.int64)
+    if not torch.equal(out[:rows].cpu().to(torch.int64), want):
+        raise RuntimeError("torch._int_mm is not exact on these operands")
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run()
+    enqueue_s = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(sleep_cycles_per_s() * (enqueue_s * 1.5 + 2e-4)))
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(steps):
+        run()
     ev[1].record()
     torch.cuda.synchronize()
     return ev[0].elapsed_time(ev[1]) / steps
@@ -432,6 +465,123 @@ def cpu_baseline(wname: str, arrays, budget_s: float) -> dict:
             "host_cpu": cpu_model()}
 
 
+# ------------------------------------------------------- trace summaries
+def _short_kernel(name: str) -> str:
+    """`gemm_f32_m16_kernel<2, 0, 3>` from the demangled kernel name."""
+    n = name.replace("void ", "").replace("(anonymous namespace)::", "")
+    depth, end = 0, len(n)
+    for i, ch in enumerate(n):  # the argument list: the first '(' outside template brackets
+        depth += ch == "<"
+        depth -= ch == ">"
+        if ch == "(" and depth == 0:
+            end = i
+            break
+    return n[:end].split("::")[-1]
+
+
+def trace_summary(trace_csv: str, line_json: str, wname: str | None, warmup: int, steps: int) -> int:
+    """Markdown summary of a rocprofv3 kernel trace of one bench run, beside
+    the JSON line that run printed: every kernel's dispatch count and mean,
+    then one workload's steps split into the bench's passes (warmup, timed
+    region, backlogged device-time pass, event pairs; for c5 a second set, the
+    cache-resident inputs) and the roofline its backlogged pass gives, against
+    the line's own `roofline.frac`.
+
+    A step is one dispatch of the workload's first kernel (KERNEL_NAMES) plus
+    the dispatches right after it that belong to the same step (the split-K
+    reduce of the small-M kernel; the int8 GEMM after the narrowing pass). The
+    first kernel's name, template arguments included, is the one whose steps
+    in the backlogged pass come closest to the line's kernel_ms_mean (the
+    unfused sequence's GEMM and other workloads' instances of the same kernel
+    are other template instances or other steps)."""
+    import csv
+    with open(line_json) as f:
+        line = json.loads(f.read().strip().splitlines()[-1])
+    head_name = line["config"]["workload"].split(":")[0]
+    wname = wname or head_name
+    if wname == head_name:
+        rec = line
+    else:
+        rec = next(r for r in line["secondary"] if r["workload"] == wname)
+        steps, warmup = SECONDARY_PLAN[wname][0], SECONDARY_PLAN[wname][1]
+    with open(trace_csv) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Dispatch_Id"]))
+    disp = [(r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3) for r in rows]
+    by_name: dict[str, list[float]] = {}
+    for name, us in disp:
+        by_name.setdefault(name, []).append(us)
+    subs = [k.strip() for k in KERNEL_NAMES[wname].split("+")]
+    block = warmup + 3 * steps
+
+    def steps_of(lead: str) -> list[list[tuple[str, float]]]:
+        out = []
+        for i, (name, us) in enumerate(disp):
+            if name != lead:
+                continue
+            st = [(name, us)]
+            for nm, u in disp[i + 1:]:
+                if nm == lead or not any(k in nm for k in subs[1:]):
+                    break
+                st.append((nm, u))
+            out.append(st)
+        return out
+
+    target_us = rec["kernel_ms_mean"] * 1e3
+    best = None
+    for name in by_name:
+        if subs[0] not in name:
+            continue
+        st = steps_of(name)
+        if len(st) < block:
+            continue
+        back = st[warmup + steps:warmup + 2 * steps]
+        err = abs(statistics.mean(sum(u for _, u in s) for s in back) - target_us)
+        if best is None or err < best[0]:
+            best = (err, name, st)
+    if best is None:
+        print(f"no {subs[0]} kernel has {block} steps in the trace", file=sys.stderr)
+        return 1
+    _, lead, st = best
+    out = ["| kernel | dispatches | mean us | median us |", "|---|---|---|---|"]
+    for n, v in sorted(by_name.items(), key=lambda kv: -sum(kv[1])):
+        short = n if len(n) <= 90 else n[:87] + "..."
+        out.append(f"| `{short}` | {len(v)} | {statistics.mean(v):.1f} | {statistics.median(v):.1f} |")
+    kinds = sorted({nm for s in st[:block] for nm, _ in s}, key=lambda nm: nm != lead)
+    out += ["", f"Workload {wname}: a step is `{lead}`" +
+            "".join(f" then `{k}`" for k in kinds[1:]) + f"; {len(st)} steps in the trace, "
+            f"{block} per pass set ({warmup} warmup + 3 x {steps}).", "",
+            "| pass | steps | step mean us | step median us | " +
+            " | ".join(f"{_short_kernel(k)} mean us" for k in kinds) + " |",
+            "|---|---|---|---|" + "---|" * len(kinds)]
+    labels = ["warmup", "timed region", "backlogged (device time)", "event pairs"]
+    sets = [("", st[:block])]
+    if wname in RESIDENT_TOO and len(st) >= 2 * block:
+        sets.append((" (inputs cache-resident)", st[block:2 * block]))
+    backs = {}
+    for tag, blk in sets:
+        cuts = [blk[:warmup], blk[warmup:warmup + steps], blk[warmup + steps:warmup + 2 * steps],
+                blk[warmup + 2 * steps:]]
+        for label, part in zip(labels, cuts):
+            tot = [sum(u for _, u in s) for s in part]
+            per = [statistics.mean([u for s in part for nm, u in s if nm == k] or [0.0]) for k in kinds]
+            out.append(f"| {label}{tag} | {len(part)} | {statistics.mean(tot):.2f} | {statistics.median(tot):.2f} | " +
+                       " | ".join(f"{v:.2f}" for v in per) + " |")
+        backs[tag] = statistics.mean(sum(u for _, u in s) for s in cuts[2])
+    roof = rec["roofline"]
+    work = roof.get("algorithmic_flops") or roof.get("algorithmic_bytes")
+    scale = 1e12 if roof["unit"] == "TFLOP/s" else 1e9
+    back = backs[""]
+    achieved = work / (back * 1e-6) / scale
+    frac = achieved / roof["peak"]
+    out += ["", f"Backlogged pass, mean step of {steps}: {back:.2f} us -> {achieved:.2f} {roof['unit']}, "
+                f"frac {frac:.4f} of {roof['peak']} {roof['unit']} (kernel durations only). The line: kernel_ms_mean "
+                f"{rec['kernel_ms_mean'] * 1e3:.2f} us (the same pass's event span / {steps}, gaps between "
+                f"dispatches included), achieved {roof['achieved']} {roof['unit']}, frac {roof['frac']}; relative "
+                f"difference {abs(frac - roof['frac']) / roof['frac'] * 100:.2f} %."]
+    print("\n".join(out))
+    return 0
+
+
 # -------------------------------------------------------------------- main
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -452,7 +602,15 @@ def main() -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES (3 times) and exit; "
                          "its FETCH_SIZE / WRITE_SIZE counters calibrate the traffic figures")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_LINE_JSON"),
+                    help="no GPU: summarize a rocprofv3 kernel trace of a bench run (with the same "
+                         "--steps / --warmup) beside the JSON line that run printed; --summary-workload "
+                         "picks the workload (default: the line's headline)")
+    ap.add_argument("--summary-workload", default=None, choices=sorted(UNITS))
     args = ap.parse_args()
+    if args.trace_summary:
+        return trace_summary(args.trace_summary[0], args.trace_summary[1], args.summary_workload, args.warmup,
+                             args.steps)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures the dense path on one GPU only: this build has no multi-GPU "
@@ -528,6 +686,17 @@ def main() -> int:
                 "fused_kernel_vs_library": round(lib_ms / r["kernel_ms_mean"], 3),
                 "what": "torch.mm (hipBLASLt) on the same device operands, no bias or ReLU, timed like "
                         "kernel_ms_mean; a reference point, not part of the product path"}
+        elif n in LIBRARY_TOO:
+            steps = args.steps if n == head_name else SECONDARY_PLAN[n][0]
+            lib_ms = measure_library_int8(p, steps, SECONDARY_PLAN[n][1])
+            r["vendor_library"] = {
+                "kernel_ms_mean": round(lib_ms, 5),
+                "tops": round(p.w.flops / (lib_ms * 1e-3) / 1e12, 2),
+                "layer_vs_library_gemm": round(lib_ms / r["kernel_ms_mean"], 3),
+                "what": "torch._int_mm (the vendor int8 GEMM, i32 accumulation) on int8 copies of the same "
+                        "X and W (one input set, narrowing not included), no bias or ReLU, timed like "
+                        "kernel_ms_mean; compare with this layer's GEMM kernel alone in a kernel trace. "
+                        "A reference point, not part of the product path"}
         log(f"[bench] {n} done: {val:.2f} {UNITS[n]}, kernel {r['kernel_ms_mean'] * 1e3:.1f} us, region "
             f"{r['region_ms_per_step'] * 1e3:.1f} us/step [{r['plan']}]")
         results[n] = r
