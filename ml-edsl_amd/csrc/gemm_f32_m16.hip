@@ -137,7 +137,7 @@ gemm_f32_m16_kernel(GemmF32Args args) {
   static_assert(A_F4 % kThreads == 0 && B_F4 % kThreads == 0, "tile loads must divide evenly");
   static_assert(PF == 2, "prefetch depth");
   __shared__ f32x4 sA[2][A_F4];
-  __shared__ float sB[2][BK * kBN];
+  __shared__ __attribute__((aligned(16))) float sB[2][BK * kBN];  // 16-byte rows: f32x4 stores and reads
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
