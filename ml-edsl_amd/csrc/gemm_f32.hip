@@ -554,8 +554,6 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case kF32M16_128x256Edge: return launch_gemm_f32_m16(2, kGuardEdge, epi, a, stream);
     case kF32M16_128W8: return launch_gemm_f32_m16(3, kGuardNone, epi, a, stream);
     case kF32M16_128W8Edge: return launch_gemm_f32_m16(3, kGuardEdge, epi, a, stream);
-    case kF32M16_64K2: return launch_gemm_f32_m16(4, kGuardNone, epi, a, stream);
-    case kF32M16_64K2Edge: return launch_gemm_f32_m16(4, kGuardEdge, epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -69,28 +69,20 @@ constexpr int PF = 2;    // K steps of global loads in flight
 //  kWide:  128x256 tile, 2x4 waves of 64x64, 32-deep K steps, one workgroup
 //          of eight waves per CU (96 KiB of LDS);
 //  kLarge8: 128x128 tile, 2x4 waves of 64x32, 32-deep K steps, for exactly
-//          one tile per CU (two waves per SIMD);
-//  kSmallK2: the 64x64 tile with eight waves: each 32x32 wave tile is shared
-//          by two waves on one SIMD that take alternate 16-deep groups of
-//          every K step (WK = 2); their partial sums meet in LDS at the end.
-//          For at most one tile per CU: one wave's LDS waits and barrier
-//          then overlap its partner's MFMAs.
-enum : int { kLarge = 0, kSmall = 1, kWide = 2, kLarge8 = 3, kSmallK2 = 4 };
+//          one tile per CU (two waves per SIMD).
+enum : int { kLarge = 0, kSmall = 1, kWide = 2, kLarge8 = 3 };
 template <int L> struct Layout;
 template <> struct Layout<kLarge> {
-  static constexpr int BM = 128, BN = 128, BK = 32, WM = 2, WN = 2, WK = 1;
+  static constexpr int BM = 128, BN = 128, BK = 32, WM = 2, WN = 2;
 };
 template <> struct Layout<kSmall> {
-  static constexpr int BM = 64, BN = 64, BK = 64, WM = 2, WN = 2, WK = 1;
+  static constexpr int BM = 64, BN = 64, BK = 64, WM = 2, WN = 2;
 };
 template <> struct Layout<kWide> {
-  static constexpr int BM = 128, BN = 256, BK = 32, WM = 2, WN = 4, WK = 1;
+  static constexpr int BM = 128, BN = 256, BK = 32, WM = 2, WN = 4;
 };
 template <> struct Layout<kLarge8> {
-  static constexpr int BM = 128, BN = 128, BK = 32, WM = 2, WN = 4, WK = 1;
-};
-template <> struct Layout<kSmallK2> {
-  static constexpr int BM = 64, BN = 64, BK = 64, WM = 2, WN = 2, WK = 2;
+  static constexpr int BM = 128, BN = 128, BK = 32, WM = 2, WN = 4;
 };
 
 template <int N> struct VecT;
@@ -111,10 +103,9 @@ constexpr int share(int n, int slices, int t) { return n / slices + (t < n % sli
 // loads at one address with immediate offsets, B columns past N read column
 // N-1, and the partial step zeroes each element past K.
 template <int L, int GUARD, int EPI>
-__global__ void __launch_bounds__(Layout<L>::WM * Layout<L>::WN * Layout<L>::WK * 64, 2)
+__global__ void __launch_bounds__(Layout<L>::WM * Layout<L>::WN * 64, 2)
 gemm_f32_m16_kernel(GemmF32Args args) {
-  constexpr int WK = Layout<L>::WK;  // waves sharing a wave tile, splitting each K step's groups
-  constexpr int kThreads = Layout<L>::WM * Layout<L>::WN * WK * 64;
+  constexpr int kThreads = Layout<L>::WM * Layout<L>::WN * 64;
   constexpr bool kScalar = GUARD == kGuardScalar;
   constexpr bool kEdge = GUARD == kGuardEdge || kScalar;  // partial tiles and K step
   static_assert(GUARD == kGuardNone || GUARD == kGuardEdge || kScalar, "guard");
@@ -124,7 +115,7 @@ gemm_f32_m16_kernel(GemmF32Args args) {
   constexpr int RB = kBM / Layout<L>::WM / 16;  // 16-row MFMA blocks of a wave tile
   constexpr int CB = kBN / Layout<L>::WN / 16;  // 16-column MFMA blocks of a wave tile
   constexpr int KCH = BK / 4;        // 16-byte chunks of an A row
-  constexpr int G = BK / 16 / WK;    // 16-deep groups of a K step per wave
+  constexpr int G = BK / 16;         // 16-deep groups of a K step
   constexpr int A_F4 = kBM * KCH;
   constexpr int B_F4 = BK * kBN / 4;
   constexpr int A_LD = A_F4 / kThreads;
@@ -133,7 +124,7 @@ gemm_f32_m16_kernel(GemmF32Args args) {
   constexpr int NR = RB + 4;         // fragment reads of one group
   constexpr int NM = 4 * RB * CB;    // MFMAs of one group
   using bvec = typename VecT<CB>::type;
-  static_assert(BK % (16 * WK) == 0 && KCH <= 32 && G % 2 == 0, "BK");
+  static_assert(BK % 16 == 0 && KCH <= 32 && G % 2 == 0, "BK");
   static_assert(A_F4 % kThreads == 0 && B_F4 % kThreads == 0, "tile loads must divide evenly");
   static_assert(PF == 2, "prefetch depth");
   __shared__ f32x4 sA[2][A_F4];
@@ -142,10 +133,7 @@ gemm_f32_m16_kernel(GemmF32Args args) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  // Waves w and w + WM*WN share a wave tile (the hardware gives them the same
-  // SIMD); wave wk of the pair takes the K step's groups wk, wk + WK, ...
-  const int wt = wave % (Layout<L>::WM * Layout<L>::WN);
-  const int wk = wave / (Layout<L>::WM * Layout<L>::WN);
+  const int wt = wave % (Layout<L>::WM * Layout<L>::WN);  // the wave's tile
   const int g = lane >> 4;
   const int r16 = lane & 15;
   const int wm0 = (wt / Layout<L>::WN) * (kBM / Layout<L>::WM);
@@ -238,9 +226,7 @@ gemm_f32_m16_kernel(GemmF32Args args) {
     f32x4 a[RB];  // row block i: A[wm0 + 16i + r16][16j + 4g .. +3]
     bvec b[4];    // step s: B[16j + 4g + s][wn0 + CB*r16 .. +CB-1]
   };
-  // j: the wave's own group index (0 .. G-1), group WK * j + wk of the step.
-  auto read_frag = [&](int buf, int jl, Frag& f) __attribute__((always_inline)) {
-    const int j = WK * jl + wk;
+  auto read_frag = [&](int buf, int j, Frag& f) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
       const int row = wm0 + 16 * i + r16;
@@ -402,30 +388,6 @@ gemm_f32_m16_kernel(GemmF32Args args) {
     }
   }
 
-  if constexpr (WK > 1) {
-    // The waves sharing a wave tile sum their partial accumulators through
-    // LDS (sA is free once every wave is past its last fragment read); wave
-    // wk = 0 adds them and stores.
-    constexpr int kTiles = Layout<L>::WM * Layout<L>::WN;
-    static_assert((WK - 1) * kTiles * RB * CB * 64 <= 2 * A_F4, "reduce buffer");
-    f32x4* red = &sA[0][0];
-    __syncthreads();
-    if (wk > 0) {
-#pragma unroll
-      for (int i = 0; i < RB; ++i)
-#pragma unroll
-        for (int c = 0; c < CB; ++c) red[((((wk - 1) * kTiles + wt) * RB + i) * CB + c) * 64 + lane] = acc[i][c];
-    }
-    __syncthreads();
-    if (wk > 0) return;
-#pragma unroll
-    for (int w = 1; w < WK; ++w)
-#pragma unroll
-      for (int i = 0; i < RB; ++i)
-#pragma unroll
-        for (int c = 0; c < CB; ++c) acc[i][c] += red[((((w - 1) * kTiles + wt) * RB + i) * CB + c) * 64 + lane];
-  }
-
   // Epilogue: lane holds rows wm0 + 16i + 4g + e and columns col0 .. col0+CB-1.
   const float alpha = args.alpha;
 #pragma unroll
@@ -465,7 +427,7 @@ hipError_t launch_layout(int epi, const GemmF32Args& a, hipStream_t stream) {
   }
   if (a.tiles_m != (a.M + BM - 1) / BM || a.tiles_n != (a.N + BN - 1) / BN) return hipErrorInvalidValue;
   const dim3 grid(a.tiles_m * a.tiles_n);
-  const dim3 block(Layout<L>::WM * Layout<L>::WN * Layout<L>::WK * 64);
+  const dim3 block(Layout<L>::WM * Layout<L>::WN * 64);
 #define EDSL_M16_CASE(E)                                                                \
   case E:                                                                               \
     hipLaunchKernelGGL((gemm_f32_m16_kernel<L, GUARD, E>), grid, block, 0, stream, a);  \
@@ -498,8 +460,6 @@ hipError_t launch_gemm_f32_m16(int layout, int guard, int epi, GemmF32Args a, hi
     case kWide * 4 + kGuardEdge: return launch_layout<kWide, kGuardEdge>(epi, a, stream);
     case kLarge8 * 4 + kGuardNone: return launch_layout<kLarge8, kGuardNone>(epi, a, stream);
     case kLarge8 * 4 + kGuardEdge: return launch_layout<kLarge8, kGuardEdge>(epi, a, stream);
-    case kSmallK2 * 4 + kGuardNone: return launch_layout<kSmallK2, kGuardNone>(epi, a, stream);
-    case kSmallK2 * 4 + kGuardEdge: return launch_layout<kSmallK2, kGuardEdge>(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -32,10 +32,12 @@ namespace {
 //      141 against 165 us for 128x128x16), its 64x64x64 twin (1024^3 21.6
 //      against 23.3 us), 128x256x32 with 2x4 waves of 64x64 and one
 //      workgroup per CU (4096^3 938-941 against 959-962 us for 128x128,
-//      8192^3 7411 against 7519 us), 128x128x32 with eight waves for
-//      exactly one tile per CU (2048^3 137 against 139-141 us), and the
-//      64x64x64 tile with eight waves, two per wave tile splitting K, for at
-//      most one tile per CU.
+//      8192^3 7411 against 7519 us), and 128x128x32 with eight waves for
+//      exactly one tile per CU (2048^3 137 against 139-141 us). A 64x64x64
+//      layout with eight waves, two per wave tile splitting K, measured 2 %
+//      slower than the four-wave one at 1024^3 (22.3-22.5 against 21.8-22.1
+//      us) once the latter's fragment reads were placed early, and is not
+//      built.
 const GemmF32Config kConfigs[] = {
     {64, 64, 16, 2, 2, kGuardAll, "f32_64x64x16_w2x2_guard"},
     {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k4_pf4"},
@@ -53,8 +55,6 @@ const GemmF32Config kConfigs[] = {
     {128, 256, 32, 2, 4, kGuardEdge, "f32_128x256x32_mfma16_edge"},
     {128, 128, 32, 2, 4, kGuardNone, "f32_128x128x32_mfma16_w8"},
     {128, 128, 32, 2, 4, kGuardEdge, "f32_128x128x32_mfma16_w8_edge"},
-    {64, 64, 64, 2, 2, kGuardNone, "f32_64x64x64_mfma16_k2"},
-    {64, 64, 64, 2, 2, kGuardEdge, "f32_64x64x64_mfma16_k2_edge"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 static_assert(kNumConfigs == kF32Tiles, "one table entry per F32Tile");
@@ -130,11 +130,7 @@ int plan_f32_tile(const F32TileQuery& q) {
       // their edge-tile twins): the 128x128 tile on 16x16 MFMA blocks, then
       // its 64x64 twin, then 32x32 tiles.
       const int c128 = pick({kF32M16_128, kF32M16_128Edge});
-      int c64 = pick({kF32M16_64, kF32M16_64Edge});
-      // At most one 64x64 tile per CU: the eight-wave twin, two waves per
-      // SIMD splitting each K step (1024^3: 21.9 against 22.2-22.3 us; at four
-      // tiles per CU, 4096x512x4096, 148 against 142 us, so only here).
-      if (tiles_of(c64) <= q.cus) c64 = pick({kF32M16_64K2, kF32M16_64K2Edge});
+      const int c64 = pick({kF32M16_64, kF32M16_64Edge});
       bool skip128 = false;
       if (tiles_of(c128) >= q.cus) {
         // The 128x128 tile against its 64x64 and 128x256 twins, by how the

@@ -43,8 +43,6 @@ enum F32Tile : int {
   kF32M16_128x256Edge,
   kF32M16_128W8,        // 128x128x32 on 16x16 blocks, eight waves (layout 3)
   kF32M16_128W8Edge,
-  kF32M16_64K2,         // 64x64x64 on 16x16 blocks, two waves per wave tile splitting K (layout 4)
-  kF32M16_64K2Edge,
   kF32Tiles
 };
 int gemm_f32_num_configs();

@@ -81,7 +81,7 @@ def test_every_edge_config_on_odd_shapes(torch_cuda):
 
 
 @pytest.mark.parametrize("shape, tile", [
-    ((1000, 1000, 1000), "f32_64x64x64_mfma16_k2_edge"),
+    ((1000, 1000, 1000), "f32_64x64x64_mfma16_edge"),
     ((4000, 256, 4000), "f32_128x256x32_mfma16_edge"),
     # 33 x 32 tiles of 128x128 would give 32 CUs a fifth tile
     ((4097, 256, 4096), "f32_64x64x64_mfma16_edge"),
@@ -98,7 +98,7 @@ def test_auto_plan_takes_edge_tiles(shape, tile, torch_cuda):
 
 def test_aligned_shapes_keep_their_tiles(torch_cuda):
     """Shapes the tiles divide still take the unguarded configurations."""
-    for (M, K, N), tile in (((1024, 1024, 1024), "f32_64x64x64_mfma16_k2"),
+    for (M, K, N), tile in (((1024, 1024, 1024), "f32_64x64x64_mfma16"),
                             ((2048, 2048, 2048), "f32_128x128x32_mfma16_w8"),
                             ((4096, 1024, 4096), "f32_128x256x32_mfma16"),
                             ((3072, 512, 3072), "f32_64x64x64_mfma16"),
@@ -472,9 +472,7 @@ MFMA16_SHAPES = {
     "f32_128x128x32_mfma16_w8": [(128, 32, 128), (256, 64, 256), (384, 96, 128), (128, 1056, 384)],
     "f32_128x256x32_mfma16": [(128, 32, 256), (256, 64, 512), (128, 96, 768), (384, 1056, 256)],
     "f32_64x64x64_mfma16": [(64, 64, 64), (128, 128, 64), (64, 192, 192), (192, 2048, 128),
-                            (1024, 320, 64), (64, 448, 1024)],
-    "f32_64x64x64_mfma16_k2": [(64, 64, 64), (128, 128, 64), (64, 192, 192), (192, 2048, 128),
-                               (1024, 320, 64), (64, 448, 1024), (1024, 1024, 1024)],
+                            (1024, 320, 64), (64, 448, 1024), (1024, 1024, 1024)],
 }
 
 
