@@ -57,7 +57,7 @@ PEAK = {  # MI355X published dense peaks
     "int8_mfma_tops": 5000.0,
     "hbm_gbs": 8000.0,
 }
-KERNEL_NAMES = {"c1": "gemm_f32_kernel", "c2": "gemm_f32_m16_kernel", "c3": "gemm_f32_m16_kernel",
+KERNEL_NAMES = {"c1": "gemm_f32_kernel", "c2": "gemm_f32_m16_kernel", "c3": "gemm_f32_direct_kernel",
                 "c4": "gemv_f32_kernel + gemv_reduce_kernel", "c5": "narrow_i8_kernel + gemm_i8_ksplit_kernel",
                 "c3s8": "gemm_f32_m16_kernel", "c4s8": "gemv_f32_kernel + gemv_reduce_kernel"}
 UNITS = {"c1": "TFLOP/s", "c2": "TFLOP/s", "c3": "TFLOP/s", "c4": "GB/s", "c5": "TOP/s",
@@ -467,7 +467,7 @@ def cpu_baseline(wname: str, arrays, budget_s: float) -> dict:
 
 # ------------------------------------------------------- trace summaries
 def _short_kernel(name: str) -> str:
-    """`gemm_f32_m16_kernel<2, 0, 3>` from the demangled kernel name."""
+    """`gemm_f32_direct_kernel<0, 3>` from the demangled kernel name."""
     n = name.replace("void ", "").replace("(anonymous namespace)::", "")
     depth, end = 0, len(n)
     for i, ch in enumerate(n):  # the argument list: the first '(' outside template brackets

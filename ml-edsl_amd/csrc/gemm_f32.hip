@@ -554,6 +554,8 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case kF32M16_128x256Edge: return launch_gemm_f32_m16(2, kGuardEdge, epi, a, stream);
     case kF32M16_128W8: return launch_gemm_f32_m16(3, kGuardNone, epi, a, stream);
     case kF32M16_128W8Edge: return launch_gemm_f32_m16(3, kGuardEdge, epi, a, stream);
+    case kF32Direct128: return launch_gemm_f32_direct(kGuardNone, epi, a, stream);
+    case kF32Direct128Edge: return launch_gemm_f32_direct(kGuardEdge, epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -25,13 +25,17 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args args, hipStream_t strea
 // The tiles on 16x16 MFMA blocks (gemm_f32_m16.hip), 16-byte aligned operands
 // and row strides: layout 0, a 128x128 tile with 32-deep K steps; 1, a 64x64
 // tile with 64-deep K steps; 2, a 128x256 tile with 32-deep K steps; 3, the
-// 128x128 tile with eight waves; 4, the 64x64 tile with eight waves, two per
-// wave tile splitting K. guard
+// 128x128 tile with eight waves. guard
 // kGuardNone: M and N multiples of the tile, K of the step; kGuardEdge: any
 // M, N >= 4 and K >= 4 that are multiples of 4; kGuardScalar (layout 0 only):
 // any shape, alignment and row strides. tiles_m and tiles_n are M and N over
 // the tile, rounded up.
 hipError_t launch_gemm_f32_m16(int layout, int guard, int epi, GemmF32Args args, hipStream_t stream);
+// The one-wave 128x128 tile without LDS (gemm_f32_direct.hip), 16-byte aligned
+// operands and row strides, N and K multiples of 4, A and B within 32-bit
+// buffer offsets (gemm_f32_direct_offsets_fit). guard kGuardNone: M and N
+// multiples of 128, K of 16; kGuardEdge: any such M, N, K.
+hipError_t launch_gemm_f32_direct(int guard, int epi, GemmF32Args args, hipStream_t stream);
 
 // ------------------------------------------------------------ fp32 small-M
 struct GemvF32Args {

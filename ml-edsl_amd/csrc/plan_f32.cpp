@@ -38,6 +38,11 @@ namespace {
 //      slower than the four-wave one at 1024^3 (22.3-22.5 against 21.8-22.1
 //      us) once the latter's fragment reads were placed early, and is not
 //      built.
+//  kF32Direct128*: 128x128x16 with one wave per tile and no LDS
+//      (gemm_f32_direct.hip): fragments loaded straight into the MFMA operand
+//      registers, four tiles per CU; for layers whose tiles fill whole rounds
+//      of 4 x CUs (4096^3 900-906 us against 926-934 us for 128x256x32,
+//      8192^3 7148 against 7342 us, 4096x256x4096 70.5 against 72.9 us).
 const GemmF32Config kConfigs[] = {
     {64, 64, 16, 2, 2, kGuardAll, "f32_64x64x16_w2x2_guard"},
     {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k4_pf4"},
@@ -55,6 +60,8 @@ const GemmF32Config kConfigs[] = {
     {128, 256, 32, 2, 4, kGuardEdge, "f32_128x256x32_mfma16_edge"},
     {128, 128, 32, 2, 4, kGuardNone, "f32_128x128x32_mfma16_w8"},
     {128, 128, 32, 2, 4, kGuardEdge, "f32_128x128x32_mfma16_w8_edge"},
+    {128, 128, 16, 1, 1, kGuardNone, "f32_128x128x16_direct"},
+    {128, 128, 16, 1, 1, kGuardEdge, "f32_128x128x16_direct_edge"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 static_assert(kNumConfigs == kF32Tiles, "one table entry per F32Tile");
@@ -62,6 +69,11 @@ static_assert(kNumConfigs == kF32Tiles, "one table entry per F32Tile");
 }  // namespace
 
 int gemm_f32_num_configs() { return kNumConfigs; }
+
+bool gemm_f32_direct_offsets_fit(int64_t K, int64_t lda, int64_t ldb) {
+  constexpr int64_t kMax = 0x7fffffff;
+  return K >= 0 && lda >= 0 && ldb >= 0 && 128 * lda * 4 + 64 <= kMax && (K + 16) * ldb * 4 + 1024 <= kMax;
+}
 const GemmF32Config& gemm_f32_config(int cfg) { return kConfigs[cfg]; }
 
 int plan_f32_tile(const F32TileQuery& q) {
@@ -71,8 +83,10 @@ int plan_f32_tile(const F32TileQuery& q) {
   // Partial edge tiles need 16-byte vectors that are all in or all out of
   // range: K and N multiples of 4 (true for every contiguous aligned operand).
   const bool edge_ok = aligned && K >= 4 && N >= 4 && M >= 1 && K % 4 == 0 && N % 4 == 0;
+  const bool direct_ok = gemm_f32_direct_offsets_fit(K, q.lda, q.ldb);
   auto fits = [&](int c) {
     const GemmF32Config& g = gemm_f32_config(c);
+    if ((c == kF32Direct128 || c == kF32Direct128Edge) && !direct_ok) return false;
     if (g.guard == kGuardNone) return aligned && K > 0 && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
     if (g.guard == kGuardEdge) return edge_ok;
     return K > 0;  // kGuardScalar, kGuardAll: any shape, stride and alignment
@@ -156,7 +170,17 @@ int plan_f32_tile(const F32TileQuery& q) {
         const int64_t tw = tiles_of(cwide);
         const double twide =
             tw >= q.cus ? (double)((tw + q.cus - 1) / q.cus) * 2.0 * 0.94 * 0.98 : 1e30;
-        if (twide <= t128 && twide <= t64) {
+        // The one-wave 128x128 tile (gemm_f32_direct.hip) runs one tile per
+        // SIMD, four per CU at a time; a round of them takes ~3.6 of the
+        // units above (4096^3: 914-927 us against 937 us for two rounds of
+        // 128x256; 8192^3: 7167 against 7373-7385 us). It wins where its
+        // tiles fill whole rounds of 4 x cus.
+        const int cdirect = pick({kF32Direct128, kF32Direct128Edge});
+        const double tdirect =
+            cdirect >= 0 ? (double)((tiles_of(cdirect) + 4 * q.cus - 1) / (4 * q.cus)) * 3.6 : 1e30;
+        if (tdirect < twide && tdirect < t128 && tdirect < t64) {
+          cfg = cdirect;
+        } else if (twide <= t128 && twide <= t64) {
           cfg = cwide;
         } else if (t64 < t128) {
           skip128 = true;

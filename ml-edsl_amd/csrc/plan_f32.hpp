@@ -1,7 +1,7 @@
 // The fp32 tile configurations and the planner that picks one for a layer.
-// Host-only (no HIP): the kernels are in gemm_f32.hip and gemm_f32_m16.hip,
-// the planner's callers in runtime.cpp, and tests build this file alone to
-// check plans without a device.
+// Host-only (no HIP): the kernels are in gemm_f32.hip, gemm_f32_m16.hip and
+// gemm_f32_direct.hip, the planner's callers in runtime.cpp, and tests build
+// this file alone to check plans without a device.
 #pragma once
 
 #include <stdint.h>
@@ -43,6 +43,8 @@ enum F32Tile : int {
   kF32M16_128x256Edge,
   kF32M16_128W8,        // 128x128x32 on 16x16 blocks, eight waves (layout 3)
   kF32M16_128W8Edge,
+  kF32Direct128,        // 128x128x16, one wave per tile, no LDS (gemm_f32_direct.hip)
+  kF32Direct128Edge,
   kF32Tiles
 };
 int gemm_f32_num_configs();
@@ -54,6 +56,7 @@ constexpr int kF32SmallM = 64;
 
 struct F32TileQuery {
   int64_t M, N, K;
+  int64_t lda, ldb;  // row strides of A and B, in elements
   // Every operand 16-byte aligned, row strides multiples of 4 elements.
   bool aligned;
   int cus;      // compute units of the device
@@ -61,5 +64,11 @@ struct F32TileQuery {
 };
 // The configuration for a tiled fp32 layer (M, N, K >= 0).
 int plan_f32_tile(const F32TileQuery& q);
+
+// The one-wave tiles read A and B through buffer descriptors with 32-bit
+// byte offsets: 128 rows of A from a tile's first row, and all K rows of B
+// (plus a partial group's overrun) from a tile's first column, must be
+// addressable that way.
+bool gemm_f32_direct_offsets_fit(int64_t K, int64_t lda, int64_t ldb);
 
 }  // namespace edsl

@@ -473,7 +473,7 @@ void launch_f32(DeviceState& ds, const DenseLaunch& L, hipStream_t stream, const
   }
 
   static_assert(kF32SmallM == kGemvMaxM, "the tile planner's small-M rule covers the small-M kernel's rows");
-  const int cfg = plan_f32_tile(F32TileQuery{M, N, K, aligned, ds.cus, g_force_cfg});
+  const int cfg = plan_f32_tile(F32TileQuery{M, N, K, L.ldx, L.ldw, aligned, ds.cus, g_force_cfg});
   const GemmF32Config& g = gemm_f32_config(cfg);
   GemmF32Args a{};
   a.A = static_cast<const float*>(L.x);

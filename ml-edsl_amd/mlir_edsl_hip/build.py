@@ -21,7 +21,7 @@ BUILD_DIR = os.path.join(ROOT, "_build")
 LIB_NAME = "libedsl_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 
-SOURCES = ["gemm_f32.hip", "gemm_f32_m16.hip", "gemv_f32.hip", "gemm_i8.hip", "runtime.cpp", "plan_f32.cpp",
+SOURCES = ["gemm_f32.hip", "gemm_f32_m16.hip", "gemm_f32_direct.hip", "gemv_f32.hip", "gemm_i8.hip", "runtime.cpp", "plan_f32.cpp",
            "program.cpp", "host_stage.cpp", "noalloc.hip", "unfused.hip"]
 ARCH = "gfx950"
 

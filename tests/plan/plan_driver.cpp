@@ -19,7 +19,8 @@ int main() {
     long long M, N, K;
     int aligned, cus;
     if (sscanf(line, "%lld %lld %lld %d %d", &M, &N, &K, &aligned, &cus) != 5) return 2;
-    const int c = edsl::plan_f32_tile(edsl::F32TileQuery{M, N, K, aligned != 0, cus, -1});
+    // Contiguous operands: row strides K and N.
+    const int c = edsl::plan_f32_tile(edsl::F32TileQuery{M, N, K, K, N, aligned != 0, cus, -1});
     printf("%s\n", edsl::gemm_f32_config(c).name);
   }
   return 0;

@@ -82,7 +82,7 @@ def test_every_edge_config_on_odd_shapes(torch_cuda):
 
 @pytest.mark.parametrize("shape, tile", [
     ((1000, 1000, 1000), "f32_64x64x64_mfma16_edge"),
-    ((4000, 256, 4000), "f32_128x256x32_mfma16_edge"),
+    ((4000, 256, 4000), "f32_128x128x16_direct_edge"),
     # 33 x 32 tiles of 128x128 would give 32 CUs a fifth tile
     ((4097, 256, 4096), "f32_64x64x64_mfma16_edge"),
     # K = 1000 leaves a partial last K step on every tile
@@ -100,7 +100,7 @@ def test_aligned_shapes_keep_their_tiles(torch_cuda):
     """Shapes the tiles divide still take the unguarded configurations."""
     for (M, K, N), tile in (((1024, 1024, 1024), "f32_64x64x64_mfma16"),
                             ((2048, 2048, 2048), "f32_128x128x32_mfma16_w8"),
-                            ((4096, 1024, 4096), "f32_128x256x32_mfma16"),
+                            ((4096, 1024, 4096), "f32_128x128x16_direct"),
                             ((3072, 512, 3072), "f32_64x64x64_mfma16"),
                             ((256, 256, 256), "f32_32x32x64_w1x1_k4_pf4")):
         X, W, b = _inputs(M, K, N, 7)
@@ -465,8 +465,12 @@ def test_int8_path_odd_shapes_strided_and_out_of_range(torch_cuda):
 # or 64 (64x64) with loads two steps ahead and each step's last group of MFMAs
 # deferred past its barrier. One, two and three K steps cover the ring's
 # remainder paths and the final deferred group in both parities; the long K
-# and the tall and wide shapes cover many steps and tile orders.
+# and the tall and wide shapes cover many steps and tile orders. The one-wave
+# 128x128 tile (gemm_f32_direct.hip) walks K in 16-deep groups, two register
+# sets: one, two and three groups cover its loop and its odd remainder.
 MFMA16_SHAPES = {
+    "f32_128x128x16_direct": [(128, 16, 128), (256, 32, 128), (128, 48, 384), (384, 2048, 256),
+                              (1024, 160, 128), (128, 208, 1024)],
     "f32_128x128x32_mfma16": [(128, 32, 128), (256, 64, 128), (128, 96, 384), (384, 2048, 256),
                               (1024, 160, 128), (128, 224, 1024)],
     "f32_128x128x32_mfma16_w8": [(128, 32, 128), (256, 64, 256), (384, 96, 128), (128, 1056, 384)],
@@ -512,7 +516,8 @@ def test_mfma16_edge_tiles_on_random_shapes(torch_cuda):
     from mlir_edsl_hip.device import set_f32_config
     torch = torch_cuda
     names = _native.f32_config_names()
-    forced = [names.index("f32_128x128x32_mfma16_edge"), names.index("f32_64x64x64_mfma16_edge")]
+    forced = [names.index("f32_128x128x32_mfma16_edge"), names.index("f32_64x64x64_mfma16_edge"),
+              names.index("f32_128x128x16_direct_edge")]
     rng = np.random.default_rng(77)
     try:
         for case in range(12):
@@ -527,5 +532,42 @@ def test_mfma16_edge_tiles_on_random_shapes(torch_cuda):
                 if cfg >= 0:
                     assert f"cfg={names[cfg]} " in plan, (plan, (M, K, N))
                 assert_f32_parity(got, ref, K)
+    finally:
+        set_f32_config(-1)
+
+
+@pytest.mark.parametrize("tile", ["f32_128x128x16_direct_edge", "f32_128x128x16_direct",
+                                  "f32_128x128x32_mfma16_edge"])
+def test_values_past_the_operands_never_reach_the_output(tile, torch_cuda):
+    """Edge tiles read past K, N and M only in ways whose values are zeroed or
+    never stored: with NaN and Inf in every padding element of A and B (the
+    row pitch past K and N, and the rows after the last), every output
+    element still matches the oracle. The one-wave tile's partial last K
+    group sends A chunks past K out of range and the B rows that pair with
+    them read zero, so an Inf past K cannot become 0 x Inf."""
+    from mlir_edsl_hip.device import dense_launch, set_f32_config
+    torch = torch_cuda
+    names = _native.f32_config_names()
+    shapes = [(384, 2048, 256), (256, 1024, 384)] if not tile.endswith("_edge") else \
+        [(300, 100, 260), (257, 68, 132), (129, 1028, 260), (1, 4, 4)]
+    try:
+        set_f32_config(names.index(tile))
+        for i, (M, K, N) in enumerate(shapes):
+            X, W, b = _inputs(M, K, N, 700 + i)
+            ref = oracle.dense_f32_chains(X, W, b, "relu")
+            views = []
+            for a, fill in ((X, np.nan), (W, np.inf)):
+                rows, cols = a.shape
+                pitch = cols + 8
+                buf = torch.full(((rows + 2) * pitch + 4,), fill, dtype=torch.float32, device="cuda")
+                v = buf[4:4 + rows * pitch].view(rows, pitch)[:, :cols]
+                v.copy_(torch.from_numpy(a))
+                views.append(v)
+            tb = torch.from_numpy(b).cuda()
+            tY = _view(torch, np.full((M, N), np.nan, dtype=np.float32), 8, 4)
+            dense_launch(views[0], views[1], tb, tY, _native.EPI_BIAS_RELU)
+            torch.cuda.synchronize()
+            assert f"cfg={tile} " in _native.last_plan(), _native.last_plan()
+            assert_f32_parity(tY.cpu().numpy(), ref, K)
     finally:
         set_f32_config(-1)
