@@ -57,9 +57,9 @@ PEAK = {  # MI355X published dense peaks
     "int8_mfma_tops": 5000.0,
     "hbm_gbs": 8000.0,
 }
-KERNEL_NAMES = {"c1": "gemm_f32_kernel", "c2": "gemm_f32_m16_kernel", "c3": "gemm_f32_direct_kernel",
+KERNEL_NAMES = {"c1": "gemm_f32_kernel", "c2": "gemm_f32_direct64_kernel", "c3": "gemm_f32_direct_kernel",
                 "c4": "gemv_f32_kernel + gemv_reduce_kernel", "c5": "narrow_i8_kernel + gemm_i8_ksplit_kernel",
-                "c3s8": "gemm_f32_m16_kernel", "c4s8": "gemv_f32_kernel + gemv_reduce_kernel"}
+                "c3s8": "gemm_f32_direct64_kernel", "c4s8": "gemv_f32_kernel + gemv_reduce_kernel"}
 UNITS = {"c1": "TFLOP/s", "c2": "TFLOP/s", "c3": "TFLOP/s", "c4": "GB/s", "c5": "TOP/s",
          "c3s8": "TFLOP/s", "c4s8": "GB/s"}
 # (steps, warmup, input sets rotated) of each workload when it is not the

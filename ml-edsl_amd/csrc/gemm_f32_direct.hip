@@ -233,6 +233,168 @@ gemm_f32_direct_kernel(GemmF32Args args) {
   }
 }
 
+// The 64x64 tile: a workgroup of KS waves, each wave the whole tile (4x4
+// blocks, 64 accumulator registers) over its share of K -- KS contiguous runs
+// of 16-deep groups -- with the same fragment loads as the 128x128 tile (one
+// 4-column quad of B per k slot). The KS partial tiles are then summed
+// through LDS in a fixed order (wave 0 + wave 1 + ...), each wave finishing
+// 16/KS of the 16 rows each lane holds. Groups are 64 MFMAs (~0.85 us), so loads run two groups
+// ahead in three register sets. For layers with too few 128x128 tiles to fill
+// the SIMDs (1024^3: 256 tiles of 64x64, K split four ways).
+constexpr int kSets64 = 3;
+
+template <int KS, int EPI>
+__global__ void __launch_bounds__(64 * KS)
+gemm_f32_direct64_kernel(GemmF32Args args) {
+  static_assert(KS == 1 || KS == 4, "K split");
+  constexpr int RB4 = 4, CB4 = 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4;
+  const int r16 = lane & 15;
+  int tm, tn;
+  tile_coords(blockIdx.x, args.tiles_m, args.tiles_n, tm, tn);
+  const int m0 = __builtin_amdgcn_readfirstlane(tm * 64);
+  const int n0 = __builtin_amdgcn_readfirstlane(tn * 64);
+  const int ngw = args.K / 16 / KS;  // 16-deep groups per wave (K is a multiple of 16 * KS)
+  const int jb = wave * ngw;         // the wave's first group
+  const int lda = (int)args.lda, ldb = (int)args.ldb;
+
+  const i32x4 rsrc_a = buffer_rsrc(args.A + (int64_t)m0 * lda, (int64_t)(args.M - m0) * lda * 4);
+  const i32x4 rsrc_b = buffer_rsrc(args.B + n0, (int64_t)args.K * ldb * 4 - (int64_t)n0 * 4);
+  const int va = (r16 * lda + 4 * g) * 4;
+  const int vb = (4 * g * ldb + 4 * r16) * 4;
+
+  struct Frag {
+    f32x4 a[RB4];  // row block i: A[m0 + 16i + r16][16j + 4g .. +3]
+    f32x4 b[4];    // k slot s: B[16j + 4g + s][n0 + 4*r16 .. +3]
+  };
+  auto load = [&](Frag& f, int j) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < RB4; ++i) f.a[i] = raw_buffer_load_f32x4(rsrc_a, va, 64 * j + i * 64 * lda, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) f.b[s] = raw_buffer_load_f32x4(rsrc_b, vb, (16 * j + s) * ldb * 4, 0);
+  };
+  f32x4 acc[RB4][CB4];
+#pragma unroll
+  for (int i = 0; i < RB4; ++i)
+#pragma unroll
+    for (int c = 0; c < CB4; ++c) acc[i][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto mfmas = [&](const Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < RB4; ++i)
+#pragma unroll
+        for (int c = 0; c < CB4; ++c)
+          acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[i][s], f.b[s][c], acc[i][c], 0, 0, 0);
+  };
+  // 8 loads over 64 MFMAs: one load per 8 MFMAs.
+  auto pin = [&]() __attribute__((always_inline)) {
+    static_for<8>([&](auto) __attribute__((always_inline)) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Group jb + t is computed from set t % 3 while groups jb + t + 1 and
+  // jb + t + 2 are in flight; loads past the wave's last group repeat it.
+  const int jl = jb + ngw - 1;
+  Frag fr[kSets64];
+  load(fr[0], jb);
+  load(fr[1], min(jb + 1, jl));
+  int t = 0;
+  for (; t + kSets64 <= ngw; t += kSets64) {
+    static_for<kSets64>([&](auto sc) __attribute__((always_inline)) {
+      constexpr int S = decltype(sc)::value;
+      load(fr[(S + 2) % kSets64], min(jb + t + S + 2, jl));
+      mfmas(fr[S]);
+      pin();
+    });
+  }
+  static_for<kSets64>([&](auto sc) __attribute__((always_inline)) {
+    constexpr int S = decltype(sc)::value;
+    if (t + S < ngw) {
+      load(fr[(S + 2) % kSets64], min(jb + t + S + 2, jl));
+      mfmas(fr[S]);
+    }
+  });
+
+  // Lane holds rows m0 + 16i + 4g + e and columns n0 + 4*r16 .. +3 of its
+  // partial tile. Sum the KS partials (wave order) for the rows this wave
+  // finishes, then bias, activation and one 16-byte store per row.
+  const float alpha = args.alpha;
+  const int col = n0 + 4 * r16;
+  f32x4 biasv = {};
+  if constexpr (epi_has_bias(EPI)) biasv = *reinterpret_cast<const f32x4*>(args.bias + col);
+  auto store_row = [&](int i, int e, const f32x4& sums) __attribute__((always_inline)) {
+    f32x4 v;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = apply_epilogue_f32<EPI>(sums[c], biasv[c], alpha);
+    const int row = m0 + 16 * i + 4 * g + e;
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(args.C + (int64_t)row * args.ldc + col));
+  };
+  if constexpr (KS == 1) {
+#pragma unroll
+    for (int i = 0; i < RB4; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) store_row(i, e, f32x4{acc[i][0][e], acc[i][1][e], acc[i][2][e], acc[i][3][e]});
+  } else {
+    // [wave][row block][column block][e][lane]: 64 lanes write and read 256
+    // contiguous bytes per access, no bank conflict. The 16 (row block, e)
+    // rows of each lane are shared out, 16/KS per wave.
+    __shared__ float red[KS * RB4 * CB4 * 4 * 64];
+    auto word = [&](int w, int i, int c, int e) { return (((w * RB4 + i) * CB4 + c) * 4 + e) * 64 + lane; };
+#pragma unroll
+    for (int i = 0; i < RB4; ++i)
+#pragma unroll
+      for (int c = 0; c < CB4; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[word(wave, i, c, e)] = acc[i][c][e];
+    __syncthreads();
+    constexpr int kUnits = RB4 * 4 / KS;
+#pragma unroll
+    for (int r = 0; r < kUnits; ++r) {
+      const int u = wave * kUnits + r;
+      const int i = u / 4, e = u % 4;
+      f32x4 sums;
+#pragma unroll
+      for (int c = 0; c < CB4; ++c) {
+        float sum = red[word(0, i, c, e)];
+#pragma unroll
+        for (int w = 1; w < KS; ++w) sum = __fadd_rn(sum, red[word(w, i, c, e)]);
+        sums[c] = sum;
+      }
+      store_row(i, e, sums);
+    }
+  }
+}
+
+template <int KS>
+hipError_t launch_ks64(int epi, const GemmF32Args& a, hipStream_t stream) {
+  const dim3 grid(a.tiles_m * a.tiles_n);
+  const dim3 block(64 * KS);
+#define EDSL_DIRECT64_CASE(E)                                                              \
+  case E:                                                                                  \
+    hipLaunchKernelGGL((gemm_f32_direct64_kernel<KS, E>), grid, block, 0, stream, a);     \
+    break;
+  switch (epi) {
+    EDSL_DIRECT64_CASE(epi_code(false, ACT_NONE))
+    EDSL_DIRECT64_CASE(epi_code(true, ACT_NONE))
+    EDSL_DIRECT64_CASE(epi_code(false, ACT_RELU))
+    EDSL_DIRECT64_CASE(epi_code(true, ACT_RELU))
+    EDSL_DIRECT64_CASE(epi_code(false, ACT_LEAKY))
+    EDSL_DIRECT64_CASE(epi_code(true, ACT_LEAKY))
+    EDSL_DIRECT64_CASE(epi_code(false, ACT_IF_RELU))
+    EDSL_DIRECT64_CASE(epi_code(true, ACT_IF_RELU))
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef EDSL_DIRECT64_CASE
+  return hipGetLastError();
+}
+
 template <int GUARD>
 hipError_t launch_guard(int epi, const GemmF32Args& a, hipStream_t stream) {
   const dim3 grid(a.tiles_m * a.tiles_n);
@@ -259,16 +421,22 @@ hipError_t launch_guard(int epi, const GemmF32Args& a, hipStream_t stream) {
 
 }  // namespace
 
-hipError_t launch_gemm_f32_direct(int guard, int epi, GemmF32Args a, hipStream_t stream) {
-  // Shapes, strides and alignment the kernel assumes (the planner only picks
-  // it for such layers; checked again here because a wrong launch reads out
-  // of bounds).
-  if (a.M < 1 || a.N < 4 || a.K < 4 || a.N % 4 || a.K % 4) return hipErrorInvalidValue;
-  if (a.lda < a.K || a.ldb < a.N || a.ldc < a.N || a.lda % 4 || a.ldb % 4 || a.ldc % 4) return hipErrorInvalidValue;
+namespace {
+// Shapes, strides and alignment every direct tile assumes (the planner only
+// picks one for such layers; checked again here because a wrong launch reads
+// out of bounds).
+bool direct_operands_ok(int epi, const GemmF32Args& a) {
+  if (a.M < 1 || a.N < 4 || a.K < 4 || a.N % 4 || a.K % 4) return false;
+  if (a.lda < a.K || a.ldb < a.N || a.ldc < a.N || a.lda % 4 || a.ldb % 4 || a.ldc % 4) return false;
   const uintptr_t bias_bits = epi_has_bias(epi) ? (uintptr_t)a.bias : 0;
-  if (((uintptr_t)a.A | (uintptr_t)a.B | (uintptr_t)a.C | bias_bits) % 16) return hipErrorInvalidValue;
-  if (epi_has_bias(epi) && a.bias == nullptr) return hipErrorInvalidValue;
-  if (!gemm_f32_direct_offsets_fit(a.K, a.lda, a.ldb)) return hipErrorInvalidValue;
+  if (((uintptr_t)a.A | (uintptr_t)a.B | (uintptr_t)a.C | bias_bits) % 16) return false;
+  if (epi_has_bias(epi) && a.bias == nullptr) return false;
+  return gemm_f32_direct_offsets_fit(a.K, a.lda, a.ldb);
+}
+}  // namespace
+
+hipError_t launch_gemm_f32_direct(int guard, int epi, GemmF32Args a, hipStream_t stream) {
+  if (!direct_operands_ok(epi, a)) return hipErrorInvalidValue;
   if (a.tiles_m != (a.M + kTile - 1) / kTile || a.tiles_n != (a.N + kTile - 1) / kTile) return hipErrorInvalidValue;
   if (guard == kGuardNone) {
     if (a.M % kTile || a.N % kTile || a.K % 16) return hipErrorInvalidValue;
@@ -276,6 +444,17 @@ hipError_t launch_gemm_f32_direct(int guard, int epi, GemmF32Args a, hipStream_t
   }
   if (guard == kGuardEdge) return launch_guard<kGuardEdge>(epi, a, stream);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemm_f32_direct64(int ksplit, int epi, GemmF32Args a, hipStream_t stream) {
+  if (!direct_operands_ok(epi, a)) return hipErrorInvalidValue;
+  if (a.M % 64 || a.N % 64 || a.K % (16 * ksplit)) return hipErrorInvalidValue;
+  if (a.tiles_m != a.M / 64 || a.tiles_n != a.N / 64) return hipErrorInvalidValue;
+  switch (ksplit) {
+    case 1: return launch_ks64<1>(epi, a, stream);
+    case 4: return launch_ks64<4>(epi, a, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace edsl

@@ -43,6 +43,11 @@ namespace {
 //      registers, four tiles per CU; for layers whose tiles fill whole rounds
 //      of 4 x CUs (4096^3 900-906 us against 926-934 us for 128x256x32,
 //      8192^3 7148 against 7342 us, 4096x256x4096 70.5 against 72.9 us).
+//  kF32Direct64*: its 64x64 twin, one wave per tile (bk 16) or four waves of
+//      one workgroup splitting K (bk 64), partials summed through LDS. K
+//      split two or eight ways measured no better than four (1024^3 19.5-19.6
+//      against 18.2-19.6 us, 4096x4096x512 121.3 against 121.7 us) and is
+//      not built.
 const GemmF32Config kConfigs[] = {
     {64, 64, 16, 2, 2, kGuardAll, "f32_64x64x16_w2x2_guard"},
     {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k4_pf4"},
@@ -62,6 +67,8 @@ const GemmF32Config kConfigs[] = {
     {128, 128, 32, 2, 4, kGuardEdge, "f32_128x128x32_mfma16_w8_edge"},
     {128, 128, 16, 1, 1, kGuardNone, "f32_128x128x16_direct"},
     {128, 128, 16, 1, 1, kGuardEdge, "f32_128x128x16_direct_edge"},
+    {64, 64, 16, 1, 1, kGuardNone, "f32_64x64x16_direct"},
+    {64, 64, 64, 1, 1, kGuardNone, "f32_64x64x64_direct_k4"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 static_assert(kNumConfigs == kF32Tiles, "one table entry per F32Tile");
@@ -86,7 +93,8 @@ int plan_f32_tile(const F32TileQuery& q) {
   const bool direct_ok = gemm_f32_direct_offsets_fit(K, q.lda, q.ldb);
   auto fits = [&](int c) {
     const GemmF32Config& g = gemm_f32_config(c);
-    if ((c == kF32Direct128 || c == kF32Direct128Edge) && !direct_ok) return false;
+    if ((c == kF32Direct128 || c == kF32Direct128Edge || c == kF32Direct64 || c == kF32Direct64K4) && !direct_ok)
+      return false;
     if (g.guard == kGuardNone) return aligned && K > 0 && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
     if (g.guard == kGuardEdge) return edge_ok;
     return K > 0;  // kGuardScalar, kGuardAll: any shape, stride and alignment
@@ -190,6 +198,25 @@ int plan_f32_tile(const F32TileQuery& q) {
           // us, 2000^3 137 against 141 us).
           cfg = pick({kF32M16_128W8, kF32M16_128W8Edge});
         }
+      }
+      // The one-wave 64x64 tiles (gemm_f32_direct.hip) take every layer of
+      // whole 64x64 tiles that the one-wave 128x128 tile does not fill, from
+      // one tile per CU on: with K split over four waves of a workgroup, or
+      // unsplit where the tiles fill one or two waves per SIMD exactly. Same
+      // box against the tiles the model above picks: 1024^3 18.2 against 18.9
+      // us, 4096x4096x512 121.7 against 134.3 us, 2048^3 (unsplit) 117.3
+      // against 122.7 us, 3072^3 394 against 428 us, 5120^3 1779 against 1929
+      // us, 6144^3 3071 against 3229 us, 2048x4096x4096 (unsplit) 455 against
+      // 466 us on 128x256; 4096^3 stays on the 128x128 one (902 against 915
+      // us), and so do more than two unsplit waves per SIMD (4096^3 unsplit:
+      // 1120 us). Short K (below 256) is left to the tiles above.
+      if (cfg != kF32Direct128 && cfg != kF32Direct128Edge && K >= 256 && M % 64 == 0 && N % 64 == 0 &&
+          (M / 64) * (N / 64) >= q.cus) {
+        const int64_t t64n = (M / 64) * (N / 64);
+        int cd = -1;
+        if (t64n % (4 * q.cus) == 0 && t64n <= 8 * q.cus) cd = pick({kF32Direct64});
+        if (cd < 0) cd = pick({kF32Direct64K4});
+        if (cd >= 0) cfg = cd;
       }
       if (cfg < 0 && !skip128) consider(c128);
       if (cfg < 0) consider(c64);

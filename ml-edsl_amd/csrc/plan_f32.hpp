@@ -45,6 +45,8 @@ enum F32Tile : int {
   kF32M16_128W8Edge,
   kF32Direct128,        // 128x128x16, one wave per tile, no LDS (gemm_f32_direct.hip)
   kF32Direct128Edge,
+  kF32Direct64,         // 64x64x16, one wave per tile, no LDS
+  kF32Direct64K4,       // 64x64x64, four waves splitting K, partials summed through LDS
   kF32Tiles
 };
 int gemm_f32_num_configs();

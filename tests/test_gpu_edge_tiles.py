@@ -98,10 +98,12 @@ def test_auto_plan_takes_edge_tiles(shape, tile, torch_cuda):
 
 def test_aligned_shapes_keep_their_tiles(torch_cuda):
     """Shapes the tiles divide still take the unguarded configurations."""
-    for (M, K, N), tile in (((1024, 1024, 1024), "f32_64x64x64_mfma16"),
-                            ((2048, 2048, 2048), "f32_128x128x32_mfma16_w8"),
+    for (M, K, N), tile in (((1024, 1024, 1024), "f32_64x64x64_direct_k4"),
+                            ((2048, 2048, 2048), "f32_64x64x16_direct"),
                             ((4096, 1024, 4096), "f32_128x128x16_direct"),
-                            ((3072, 512, 3072), "f32_64x64x64_mfma16"),
+                            ((3072, 512, 3072), "f32_64x64x64_direct_k4"),
+                            ((2048, 128, 2048), "f32_128x128x32_mfma16_w8"),
+                            ((1024, 128, 1024), "f32_64x64x64_mfma16"),
                             ((256, 256, 256), "f32_32x32x64_w1x1_k4_pf4")):
         X, W, b = _inputs(M, K, N, 7)
         got, plan = _run(torch_cuda, X, W, b)
@@ -467,10 +469,16 @@ def test_int8_path_odd_shapes_strided_and_out_of_range(torch_cuda):
 # remainder paths and the final deferred group in both parities; the long K
 # and the tall and wide shapes cover many steps and tile orders. The one-wave
 # 128x128 tile (gemm_f32_direct.hip) walks K in 16-deep groups, two register
-# sets: one, two and three groups cover its loop and its odd remainder.
+# sets: one, two and three groups cover its loop and its odd remainder; its
+# 64x64 twin runs three register sets per wave over the wave's share of K.
 MFMA16_SHAPES = {
     "f32_128x128x16_direct": [(128, 16, 128), (256, 32, 128), (128, 48, 384), (384, 2048, 256),
                               (1024, 160, 128), (128, 208, 1024)],
+    # the 64x64 tile: one to seven groups per wave, K unsplit and split four ways
+    "f32_64x64x16_direct": [(64, 16, 64), (128, 32, 64), (64, 48, 192), (192, 2048, 128), (1024, 160, 64),
+                            (64, 208, 1024)],
+    "f32_64x64x64_direct_k4": [(64, 64, 64), (128, 128, 64), (64, 192, 192), (192, 2048, 128),
+                               (1024, 320, 64), (64, 448, 1024), (1024, 1024, 1024)],
     "f32_128x128x32_mfma16": [(128, 32, 128), (256, 64, 128), (128, 96, 384), (384, 2048, 256),
                               (1024, 160, 128), (128, 224, 1024)],
     "f32_128x128x32_mfma16_w8": [(128, 32, 128), (256, 64, 256), (384, 96, 128), (128, 1056, 384)],

@@ -42,17 +42,17 @@ def table(driver):
 PINNED = [
     # BASELINE layers that take the tiles (C4 takes the small-M kernel)
     ((256, 256, 256), True, "f32_32x32x64_w1x1_k4_pf4"),           # C1
-    ((1024, 1024, 1024), True, "f32_64x64x64_mfma16"),             # C2
+    ((1024, 1024, 1024), True, "f32_64x64x64_direct_k4"),          # C2
     ((4096, 4096, 4096), True, "f32_128x128x16_direct"),           # C3
-    ((2048, 2048, 2048), True, "f32_128x128x32_mfma16_w8"),
-    ((4096, 4096, 512), True, "f32_64x64x64_mfma16"),              # C3 column shard (N = 512)
+    ((2048, 2048, 2048), True, "f32_64x64x16_direct"),
+    ((4096, 4096, 512), True, "f32_64x64x64_direct_k4"),           # C3 column shard (N = 512)
     # tests/test_gpu_edge_tiles.py
     ((1000, 1000, 1000), True, "f32_64x64x64_mfma16_edge"),
     ((4000, 256, 4000), True, "f32_128x128x16_direct_edge"),
     ((4097, 256, 4096), True, "f32_64x64x64_mfma16_edge"),
     ((512, 1000, 512), True, "f32_32x32x64_w1x1_k4_pf4_edge"),
     ((4096, 1024, 4096), True, "f32_128x128x16_direct"),
-    ((3072, 512, 3072), True, "f32_64x64x64_mfma16"),
+    ((3072, 512, 3072), True, "f32_64x64x64_direct_k4"),
     ((2001, 2001, 2001), True, "f32_128x128x32_mfma16_anyshape"),  # K % 4 != 0
     ((1025, 1025, 1025), True, "f32_64x64x64_w2x2_k2_pf2_anyshape"),
     ((2048, 2048, 2048), False, "f32_128x128x32_mfma16_anyshape"),
@@ -65,8 +65,11 @@ PINNED = [
     ((1024, 1025, 1024), True, "f32_64x64x32_w2x2_k2_pf4_anyshape"),
     # K = 0: the element-checked tile writes the epilogue of the bias
     ((100, 0, 100), True, "f32_64x64x16_w2x2_guard"),
-    # nine 128x128 tiles per CU: the two-workgroup 128x128 tile beats its twins
-    ((6144, 6144, 6144), True, "f32_128x128x32_mfma16"),
+    # 2304 one-wave 128x128 tiles would leave the last round three quarters empty
+    ((6144, 6144, 6144), True, "f32_64x64x64_direct_k4"),
+    # short K stays on the LDS-staged tiles: one 128x128 tile per CU, then 64x64
+    ((2048, 128, 2048), True, "f32_128x128x32_mfma16_w8"),
+    ((1024, 128, 1024), True, "f32_64x64x64_mfma16"),
 ]
 
 
@@ -81,7 +84,7 @@ def test_table_is_named_and_every_tile_is_planned(driver):
     layer: the table holds no configuration the planner cannot reach."""
     rows = table(driver)
     names = [r[1] for r in rows]
-    assert len(names) == len(set(names)) == 18
+    assert len(names) == len(set(names)) == 20
     dims = [1, 4, 17, 64, 65, 100, 128, 256, 257, 500, 512, 1000, 1024, 1025, 2000, 2048, 3000, 4096, 4097, 6000,
             6144]
     queries = [(M, N, K, al, CUS) for M in dims for N in dims for K in dims + [0] for al in (0, 1)]
