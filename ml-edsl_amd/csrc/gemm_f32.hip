@@ -556,8 +556,9 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case kF32M16_128W8Edge: return launch_gemm_f32_m16(3, kGuardEdge, epi, a, stream);
     case kF32Direct128: return launch_gemm_f32_direct(kGuardNone, epi, a, stream);
     case kF32Direct128Edge: return launch_gemm_f32_direct(kGuardEdge, epi, a, stream);
-    case kF32Direct64: return launch_gemm_f32_direct64(1, epi, a, stream);
-    case kF32Direct64K4: return launch_gemm_f32_direct64(4, epi, a, stream);
+    case kF32Direct64: return launch_gemm_f32_direct64(1, kGuardNone, epi, a, stream);
+    case kF32Direct64K4: return launch_gemm_f32_direct64(4, kGuardNone, epi, a, stream);
+    case kF32Direct64K4Edge: return launch_gemm_f32_direct64(4, kGuardEdge, epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

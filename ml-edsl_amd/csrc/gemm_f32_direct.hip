@@ -236,17 +236,19 @@ gemm_f32_direct_kernel(GemmF32Args args) {
 // The 64x64 tile: a workgroup of KS waves, each wave the whole tile (4x4
 // blocks, 64 accumulator registers) over its share of K -- KS contiguous runs
 // of 16-deep groups -- with the same fragment loads as the 128x128 tile (one
-// 4-column quad of B per k slot). The KS partial tiles are then summed
+// 4-column quad of B per k slot), and the same edge handling. The KS partial tiles are then summed
 // through LDS in a fixed order (wave 0 + wave 1 + ...), each wave finishing
 // 16/KS of the 16 rows each lane holds. Groups are 64 MFMAs (~0.85 us), so loads run two groups
 // ahead in three register sets. For layers with too few 128x128 tiles to fill
 // the SIMDs (1024^3: 256 tiles of 64x64, K split four ways).
 constexpr int kSets64 = 3;
 
-template <int KS, int EPI>
+template <int KS, int GUARD, int EPI>
 __global__ void __launch_bounds__(64 * KS)
 gemm_f32_direct64_kernel(GemmF32Args args) {
   static_assert(KS == 1 || KS == 4, "K split");
+  static_assert(GUARD == kGuardNone || GUARD == kGuardEdge, "guard");
+  constexpr bool kEdge = GUARD == kGuardEdge;
   constexpr int RB4 = 4, CB4 = 4;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -256,24 +258,50 @@ gemm_f32_direct64_kernel(GemmF32Args args) {
   tile_coords(blockIdx.x, args.tiles_m, args.tiles_n, tm, tn);
   const int m0 = __builtin_amdgcn_readfirstlane(tm * 64);
   const int n0 = __builtin_amdgcn_readfirstlane(tn * 64);
-  const int ngw = args.K / 16 / KS;  // 16-deep groups per wave (K is a multiple of 16 * KS)
-  const int jb = wave * ngw;         // the wave's first group
+  const int K = args.K;
+  // The wave's groups jb .. jb + ngw - 1. Exact tiles: K is a multiple of
+  // 16 * KS. Edge tiles: ceil(K / 16) groups shared as evenly as they go (a
+  // wave may get none when K < 16 * KS), the last one partial.
+  const int ng = (K + 15) / 16;
+  const int jb = kEdge ? wave * ng / KS : wave * (K / 16 / KS);
+  const int ngw = kEdge ? (wave + 1) * ng / KS - jb : K / 16 / KS;
   const int lda = (int)args.lda, ldb = (int)args.ldb;
 
   const i32x4 rsrc_a = buffer_rsrc(args.A + (int64_t)m0 * lda, (int64_t)(args.M - m0) * lda * 4);
-  const i32x4 rsrc_b = buffer_rsrc(args.B + n0, (int64_t)args.K * ldb * 4 - (int64_t)n0 * 4);
+  const i32x4 rsrc_b = buffer_rsrc(args.B + n0, (int64_t)K * ldb * 4 - (int64_t)n0 * 4);
   const int va = (r16 * lda + 4 * g) * 4;
   const int vb = (4 * g * ldb + 4 * r16) * 4;
+  // Edge tiles, as for the 128x128 tile: per-lane row-block offsets (rows
+  // past M out of range), the column quad clamped to N-4.
+  int va_i[RB4];
+  int vb_c = 0;
+  if constexpr (kEdge) {
+#pragma unroll
+    for (int i = 0; i < RB4; ++i) va_i[i] = va + i * 64 * lda;
+    vb_c = (4 * g * ldb + min(n0 + 4 * r16, args.N - 4) - n0) * 4;
+  }
 
   struct Frag {
     f32x4 a[RB4];  // row block i: A[m0 + 16i + r16][16j + 4g .. +3]
     f32x4 b[4];    // k slot s: B[16j + 4g + s][n0 + 4*r16 .. +3]
   };
   auto load = [&](Frag& f, int j) __attribute__((always_inline)) {
+    if constexpr (!kEdge) {
 #pragma unroll
-    for (int i = 0; i < RB4; ++i) f.a[i] = raw_buffer_load_f32x4(rsrc_a, va, 64 * j + i * 64 * lda, 0);
+      for (int i = 0; i < RB4; ++i) f.a[i] = raw_buffer_load_f32x4(rsrc_a, va, 64 * j + i * 64 * lda, 0);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) f.b[s] = raw_buffer_load_f32x4(rsrc_b, vb, (16 * j + s) * ldb * 4, 0);
+      for (int s = 0; s < 4; ++s) f.b[s] = raw_buffer_load_f32x4(rsrc_b, vb, (16 * j + s) * ldb * 4, 0);
+    } else {
+      // A chunks past K are sent out of range; the B rows that pair with them
+      // are at or past K rows of B and read zero.
+      const bool k_in = 16 * j + 4 * g < K;
+#pragma unroll
+      for (int i = 0; i < RB4; ++i)
+        f.a[i] = raw_buffer_load_f32x4(rsrc_a, k_in ? va_i[i] : kOutOfRange, 64 * j, 0);
+      const int vbj = vb_c + 16 * j * ldb * 4;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) f.b[s] = raw_buffer_load_f32x4(rsrc_b, vbj, s * ldb * 4, 0);
+    }
   };
   f32x4 acc[RB4][CB4];
 #pragma unroll
@@ -301,25 +329,27 @@ gemm_f32_direct64_kernel(GemmF32Args args) {
   // Group jb + t is computed from set t % 3 while groups jb + t + 1 and
   // jb + t + 2 are in flight; loads past the wave's last group repeat it.
   const int jl = jb + ngw - 1;
-  Frag fr[kSets64];
-  load(fr[0], jb);
-  load(fr[1], min(jb + 1, jl));
-  int t = 0;
-  for (; t + kSets64 <= ngw; t += kSets64) {
+  if (ngw > 0) {
+    Frag fr[kSets64];
+    load(fr[0], jb);
+    load(fr[1], min(jb + 1, jl));
+    int t = 0;
+    for (; t + kSets64 <= ngw; t += kSets64) {
+      static_for<kSets64>([&](auto sc) __attribute__((always_inline)) {
+        constexpr int S = decltype(sc)::value;
+        load(fr[(S + 2) % kSets64], min(jb + t + S + 2, jl));
+        mfmas(fr[S]);
+        pin();
+      });
+    }
     static_for<kSets64>([&](auto sc) __attribute__((always_inline)) {
       constexpr int S = decltype(sc)::value;
-      load(fr[(S + 2) % kSets64], min(jb + t + S + 2, jl));
-      mfmas(fr[S]);
-      pin();
+      if (t + S < ngw) {
+        load(fr[(S + 2) % kSets64], min(jb + t + S + 2, jl));
+        mfmas(fr[S]);
+      }
     });
   }
-  static_for<kSets64>([&](auto sc) __attribute__((always_inline)) {
-    constexpr int S = decltype(sc)::value;
-    if (t + S < ngw) {
-      load(fr[(S + 2) % kSets64], min(jb + t + S + 2, jl));
-      mfmas(fr[S]);
-    }
-  });
 
   // Lane holds rows m0 + 16i + 4g + e and columns n0 + 4*r16 .. +3 of its
   // partial tile. Sum the KS partials (wave order) for the rows this wave
@@ -327,13 +357,16 @@ gemm_f32_direct64_kernel(GemmF32Args args) {
   const float alpha = args.alpha;
   const int col = n0 + 4 * r16;
   f32x4 biasv = {};
-  if constexpr (epi_has_bias(EPI)) biasv = *reinterpret_cast<const f32x4*>(args.bias + col);
+  if constexpr (epi_has_bias(EPI)) {
+    if (!kEdge || col < args.N) biasv = *reinterpret_cast<const f32x4*>(args.bias + col);
+  }
   auto store_row = [&](int i, int e, const f32x4& sums) __attribute__((always_inline)) {
     f32x4 v;
 #pragma unroll
     for (int c = 0; c < 4; ++c) v[c] = apply_epilogue_f32<EPI>(sums[c], biasv[c], alpha);
     const int row = m0 + 16 * i + 4 * g + e;
-    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(args.C + (int64_t)row * args.ldc + col));
+    if (!kEdge || (row < args.M && col < args.N))
+      __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(args.C + (int64_t)row * args.ldc + col));
   };
   if constexpr (KS == 1) {
 #pragma unroll
@@ -371,13 +404,13 @@ gemm_f32_direct64_kernel(GemmF32Args args) {
   }
 }
 
-template <int KS>
+template <int KS, int GUARD>
 hipError_t launch_ks64(int epi, const GemmF32Args& a, hipStream_t stream) {
   const dim3 grid(a.tiles_m * a.tiles_n);
   const dim3 block(64 * KS);
 #define EDSL_DIRECT64_CASE(E)                                                              \
   case E:                                                                                  \
-    hipLaunchKernelGGL((gemm_f32_direct64_kernel<KS, E>), grid, block, 0, stream, a);     \
+    hipLaunchKernelGGL((gemm_f32_direct64_kernel<KS, GUARD, E>), grid, block, 0, stream, a); \
     break;
   switch (epi) {
     EDSL_DIRECT64_CASE(epi_code(false, ACT_NONE))
@@ -446,15 +479,17 @@ hipError_t launch_gemm_f32_direct(int guard, int epi, GemmF32Args a, hipStream_t
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemm_f32_direct64(int ksplit, int epi, GemmF32Args a, hipStream_t stream) {
+hipError_t launch_gemm_f32_direct64(int ksplit, int guard, int epi, GemmF32Args a, hipStream_t stream) {
   if (!direct_operands_ok(epi, a)) return hipErrorInvalidValue;
-  if (a.M % 64 || a.N % 64 || a.K % (16 * ksplit)) return hipErrorInvalidValue;
-  if (a.tiles_m != a.M / 64 || a.tiles_n != a.N / 64) return hipErrorInvalidValue;
-  switch (ksplit) {
-    case 1: return launch_ks64<1>(epi, a, stream);
-    case 4: return launch_ks64<4>(epi, a, stream);
-    default: return hipErrorInvalidValue;
+  if (a.tiles_m != (a.M + 63) / 64 || a.tiles_n != (a.N + 63) / 64) return hipErrorInvalidValue;
+  if (guard == kGuardNone) {
+    if (a.M % 64 || a.N % 64 || a.K % (16 * ksplit)) return hipErrorInvalidValue;
+    if (ksplit == 1) return launch_ks64<1, kGuardNone>(epi, a, stream);
+    if (ksplit == 4) return launch_ks64<4, kGuardNone>(epi, a, stream);
+  } else if (guard == kGuardEdge && ksplit == 4) {
+    return launch_ks64<4, kGuardEdge>(epi, a, stream);
   }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace edsl

@@ -37,9 +37,10 @@ hipError_t launch_gemm_f32_m16(int layout, int guard, int epi, GemmF32Args args,
 // multiples of 128, K of 16; kGuardEdge: any such M, N, K.
 hipError_t launch_gemm_f32_direct(int guard, int epi, GemmF32Args args, hipStream_t stream);
 // Its 64x64 tile with K split over `ksplit` waves (1 or 4) of one
-// workgroup, partial tiles summed through LDS: M and N multiples of 64, K of
-// 16 * ksplit, the same operand conditions.
-hipError_t launch_gemm_f32_direct64(int ksplit, int epi, GemmF32Args args, hipStream_t stream);
+// workgroup, partial tiles summed through LDS, the same operand conditions.
+// guard kGuardNone: M and N multiples of 64, K of 16 * ksplit; kGuardEdge
+// (ksplit 4): any such M, N, K.
+hipError_t launch_gemm_f32_direct64(int ksplit, int guard, int epi, GemmF32Args args, hipStream_t stream);
 
 // ------------------------------------------------------------ fp32 small-M
 struct GemvF32Args {

@@ -44,7 +44,10 @@ namespace {
 //      of 4 x CUs (4096^3 900-906 us against 926-934 us for 128x256x32,
 //      8192^3 7148 against 7342 us, 4096x256x4096 70.5 against 72.9 us).
 //  kF32Direct64*: its 64x64 twin, one wave per tile (bk 16) or four waves of
-//      one workgroup splitting K (bk 64), partials summed through LDS. K
+//      one workgroup splitting K (bk 64), partials summed through LDS, and
+//      the split tile's edge twin (the unsplit one's tied the eight-wave
+//      128x128 edge tile at 2000^3, 122.3 against 123.1 us, and is not
+//      built). K
 //      split two or eight ways measured no better than four (1024^3 19.5-19.6
 //      against 18.2-19.6 us, 4096x4096x512 121.3 against 121.7 us) and is
 //      not built.
@@ -69,6 +72,7 @@ const GemmF32Config kConfigs[] = {
     {128, 128, 16, 1, 1, kGuardEdge, "f32_128x128x16_direct_edge"},
     {64, 64, 16, 1, 1, kGuardNone, "f32_64x64x16_direct"},
     {64, 64, 64, 1, 1, kGuardNone, "f32_64x64x64_direct_k4"},
+    {64, 64, 64, 1, 1, kGuardEdge, "f32_64x64x64_direct_k4_edge"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 static_assert(kNumConfigs == kF32Tiles, "one table entry per F32Tile");
@@ -93,7 +97,8 @@ int plan_f32_tile(const F32TileQuery& q) {
   const bool direct_ok = gemm_f32_direct_offsets_fit(K, q.lda, q.ldb);
   auto fits = [&](int c) {
     const GemmF32Config& g = gemm_f32_config(c);
-    if ((c == kF32Direct128 || c == kF32Direct128Edge || c == kF32Direct64 || c == kF32Direct64K4) && !direct_ok)
+    if ((c == kF32Direct128 || c == kF32Direct128Edge || c == kF32Direct64 || c == kF32Direct64K4 ||
+         c == kF32Direct64K4Edge) && !direct_ok)
       return false;
     if (g.guard == kGuardNone) return aligned && K > 0 && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
     if (g.guard == kGuardEdge) return edge_ok;
@@ -210,12 +215,22 @@ int plan_f32_tile(const F32TileQuery& q) {
       // 466 us on 128x256; 4096^3 stays on the 128x128 one (902 against 915
       // us), and so do more than two unsplit waves per SIMD (4096^3 unsplit:
       // 1120 us). Short K (below 256) is left to the tiles above.
-      if (cfg != kF32Direct128 && cfg != kF32Direct128Edge && K >= 256 && M % 64 == 0 && N % 64 == 0 &&
-          (M / 64) * (N / 64) >= q.cus) {
-        const int64_t t64n = (M / 64) * (N / 64);
+      // Partial 64x64 tiles take the K-split edge twin from one tile per CU
+      // to four (1000^3 21.8 against 23.6 us, 1000x4000x1000 64.0 against
+      // 68.7 us on the LDS-staged 64x64 edge tile); with more tiles it ties
+      // (3000^3 428 against 440 us, 4097x4096x4096 1056 against 1052 us), and
+      // short K is slower (4097x256x4096 114 against 88 us).
+      if (cfg != kF32Direct128 && cfg != kF32Direct128Edge && K >= 256) {
+        const int64_t t64n = ((M + 63) / 64) * ((N + 63) / 64);
         int cd = -1;
-        if (t64n % (4 * q.cus) == 0 && t64n <= 8 * q.cus) cd = pick({kF32Direct64});
-        if (cd < 0) cd = pick({kF32Direct64K4});
+        if (M % 64 == 0 && N % 64 == 0) {
+          if (t64n >= q.cus) {
+            if (t64n % (4 * q.cus) == 0 && t64n <= 8 * q.cus) cd = pick({kF32Direct64});
+            if (cd < 0) cd = pick({kF32Direct64K4});
+          }
+        } else if (K >= 512 && t64n >= q.cus && t64n <= 4 * q.cus) {
+          cd = pick({kF32Direct64K4Edge});
+        }
         if (cd >= 0) cfg = cd;
       }
       if (cfg < 0 && !skip128) consider(c128);

@@ -47,6 +47,7 @@ enum F32Tile : int {
   kF32Direct128Edge,
   kF32Direct64,         // 64x64x16, one wave per tile, no LDS
   kF32Direct64K4,       // 64x64x64, four waves splitting K, partials summed through LDS
+  kF32Direct64K4Edge,
   kF32Tiles
 };
 int gemm_f32_num_configs();

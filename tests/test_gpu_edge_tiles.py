@@ -81,7 +81,7 @@ def test_every_edge_config_on_odd_shapes(torch_cuda):
 
 
 @pytest.mark.parametrize("shape, tile", [
-    ((1000, 1000, 1000), "f32_64x64x64_mfma16_edge"),
+    ((1000, 1000, 1000), "f32_64x64x64_direct_k4_edge"),
     ((4000, 256, 4000), "f32_128x128x16_direct_edge"),
     # 33 x 32 tiles of 128x128 would give 32 CUs a fifth tile
     ((4097, 256, 4096), "f32_64x64x64_mfma16_edge"),
@@ -525,7 +525,7 @@ def test_mfma16_edge_tiles_on_random_shapes(torch_cuda):
     torch = torch_cuda
     names = _native.f32_config_names()
     forced = [names.index("f32_128x128x32_mfma16_edge"), names.index("f32_64x64x64_mfma16_edge"),
-              names.index("f32_128x128x16_direct_edge")]
+              names.index("f32_128x128x16_direct_edge"), names.index("f32_64x64x64_direct_k4_edge")]
     rng = np.random.default_rng(77)
     try:
         for case in range(12):
@@ -545,19 +545,21 @@ def test_mfma16_edge_tiles_on_random_shapes(torch_cuda):
 
 
 @pytest.mark.parametrize("tile", ["f32_128x128x16_direct_edge", "f32_128x128x16_direct",
-                                  "f32_128x128x32_mfma16_edge"])
+                                  "f32_64x64x64_direct_k4_edge",
+                                  "f32_64x64x64_direct_k4", "f32_128x128x32_mfma16_edge"])
 def test_values_past_the_operands_never_reach_the_output(tile, torch_cuda):
     """Edge tiles read past K, N and M only in ways whose values are zeroed or
     never stored: with NaN and Inf in every padding element of A and B (the
     row pitch past K and N, and the rows after the last), every output
-    element still matches the oracle. The one-wave tile's partial last K
+    element still matches the oracle. The one-wave tiles' partial last K
     group sends A chunks past K out of range and the B rows that pair with
-    them read zero, so an Inf past K cannot become 0 x Inf."""
+    them read zero, so an Inf past K cannot become 0 x Inf; with K split over
+    four waves, K = 4 and 20 leave some waves no group at all."""
     from mlir_edsl_hip.device import dense_launch, set_f32_config
     torch = torch_cuda
     names = _native.f32_config_names()
     shapes = [(384, 2048, 256), (256, 1024, 384)] if not tile.endswith("_edge") else \
-        [(300, 100, 260), (257, 68, 132), (129, 1028, 260), (1, 4, 4)]
+        [(300, 100, 260), (257, 68, 132), (129, 1028, 260), (65, 20, 36), (1, 4, 4)]
     try:
         set_f32_config(names.index(tile))
         for i, (M, K, N) in enumerate(shapes):

@@ -47,7 +47,7 @@ PINNED = [
     ((2048, 2048, 2048), True, "f32_64x64x16_direct"),
     ((4096, 4096, 512), True, "f32_64x64x64_direct_k4"),           # C3 column shard (N = 512)
     # tests/test_gpu_edge_tiles.py
-    ((1000, 1000, 1000), True, "f32_64x64x64_mfma16_edge"),
+    ((1000, 1000, 1000), True, "f32_64x64x64_direct_k4_edge"),
     ((4000, 256, 4000), True, "f32_128x128x16_direct_edge"),
     ((4097, 256, 4096), True, "f32_64x64x64_mfma16_edge"),
     ((512, 1000, 512), True, "f32_32x32x64_w1x1_k4_pf4_edge"),
@@ -84,7 +84,7 @@ def test_table_is_named_and_every_tile_is_planned(driver):
     layer: the table holds no configuration the planner cannot reach."""
     rows = table(driver)
     names = [r[1] for r in rows]
-    assert len(names) == len(set(names)) == 20
+    assert len(names) == len(set(names)) == 21
     dims = [1, 4, 17, 64, 65, 100, 128, 256, 257, 500, 512, 1000, 1024, 1025, 2000, 2048, 3000, 4096, 4097, 6000,
             6144]
     queries = [(M, N, K, al, CUS) for M in dims for N in dims for K in dims + [0] for al in (0, 1)]
