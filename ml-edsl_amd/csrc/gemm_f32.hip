@@ -559,6 +559,7 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case kF32Direct64: return launch_gemm_f32_direct64(1, kGuardNone, epi, a, stream);
     case kF32Direct64K4: return launch_gemm_f32_direct64(4, kGuardNone, epi, a, stream);
     case kF32Direct64K4Edge: return launch_gemm_f32_direct64(4, kGuardEdge, epi, a, stream);
+    case kF32Direct16K4: return launch_gemm_f32_direct16(epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -42,6 +42,16 @@
 #include <utility>
 
 namespace edsl {
+
+// Raw buffer loads (the <4 x i32> descriptor form of the intrinsics, so that
+// a descriptor built from uniform values stays in scalar registers). Offsets
+// at or past the descriptor's byte count read zero. Declared outside the
+// anonymous namespace: these names bind to intrinsics, not to definitions.
+__device__ f32x4 raw_buffer_load_f32x4(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4f32");
+__device__ float raw_buffer_load_f32(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.f32");
+
 namespace {
 
 template <int N>
@@ -55,12 +65,6 @@ template <int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
-
-// Raw buffer load of 16 bytes (the <4 x i32> descriptor form of the
-// intrinsic, so that a descriptor built from uniform values stays in scalar
-// registers). Offsets at or past the descriptor's byte count read zero.
-__device__ f32x4 raw_buffer_load_f32x4(i32x4 rsrc, int voffset, int soffset, int aux)
-    __asm("llvm.amdgcn.raw.buffer.load.v4f32");
 
 // Descriptor of `bytes` bytes from `base` (raw addressing: stride 0, 32-bit
 // data format word of the gfx9 family).
@@ -428,6 +432,91 @@ hipError_t launch_ks64(int epi, const GemmF32Args& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// The 16x16 tile for small layers (256^3: 256 tiles): a workgroup of four
+// waves, each wave one 16x16 MFMA block over a quarter of K, all of its
+// fragments (at most kMaxGroups16 groups of 16) loaded up front, then the
+// four partial blocks summed through LDS in wave order, each wave finishing
+// one of the four rows every lane holds. So the layer's MFMAs spread over
+// 1024 waves, one per SIMD, and a wave waits for its loads once.
+constexpr int kMaxGroups16 = 8;
+
+template <int EPI>
+__global__ void __launch_bounds__(256)
+gemm_f32_direct16_kernel(GemmF32Args args) {
+  constexpr int KS = 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4;
+  const int r16 = lane & 15;
+  int tm, tn;
+  tile_coords(blockIdx.x, args.tiles_m, args.tiles_n, tm, tn);
+  const int m0 = __builtin_amdgcn_readfirstlane(tm * 16);
+  const int n0 = __builtin_amdgcn_readfirstlane(tn * 16);
+  const int ngw = args.K / 16 / KS;  // groups per wave: K is a multiple of 64, at most 64 * kMaxGroups16
+  const int jb = wave * ngw;
+  const int lda = (int)args.lda, ldb = (int)args.ldb;
+  const i32x4 rsrc_a = buffer_rsrc(args.A + (int64_t)m0 * lda, (int64_t)(args.M - m0) * lda * 4);
+  const i32x4 rsrc_b = buffer_rsrc(args.B + n0, (int64_t)args.K * ldb * 4 - (int64_t)n0 * 4);
+  const int va = (r16 * lda + 4 * g) * 4;      // A[m0 + r16][16j + 4g .. +3]
+  const int vb = (4 * g * ldb + r16) * 4;      // B[16j + 4g + s][n0 + r16]
+
+  f32x4 a[kMaxGroups16];
+  float b[kMaxGroups16][4];
+#pragma unroll
+  for (int t = 0; t < kMaxGroups16; ++t) {
+    if (t < ngw) {
+      const int j = jb + t;
+      a[t] = raw_buffer_load_f32x4(rsrc_a, va, 64 * j, 0);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) b[t][s] = raw_buffer_load_f32(rsrc_b, vb, (16 * j + s) * ldb * 4, 0);
+    }
+  }
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int t = 0; t < kMaxGroups16; ++t) {
+    if (t < ngw) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][s], b[t][s], acc, 0, 0, 0);
+    }
+  }
+
+  // Lane holds rows m0 + 4g + e, column n0 + r16. [wave][e][lane] in LDS.
+  __shared__ float red[KS * 4 * 64];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) red[(wave * 4 + e) * 64 + lane] = acc[e];
+  __syncthreads();
+  float sum = red[(0 * 4 + wave) * 64 + lane];
+#pragma unroll
+  for (int w = 1; w < KS; ++w) sum = __fadd_rn(sum, red[(w * 4 + wave) * 64 + lane]);
+  const int row = m0 + 4 * g + wave;
+  const int col = n0 + r16;
+  const float bias = epi_has_bias(EPI) ? args.bias[col] : 0.0f;
+  __builtin_nontemporal_store(apply_epilogue_f32<EPI>(sum, bias, args.alpha), args.C + (int64_t)row * args.ldc + col);
+}
+
+hipError_t launch_direct16(int epi, const GemmF32Args& a, hipStream_t stream) {
+  const dim3 grid(a.tiles_m * a.tiles_n);
+  const dim3 block(256);
+#define EDSL_DIRECT16_CASE(E)                                                          \
+  case E:                                                                              \
+    hipLaunchKernelGGL((gemm_f32_direct16_kernel<E>), grid, block, 0, stream, a);     \
+    break;
+  switch (epi) {
+    EDSL_DIRECT16_CASE(epi_code(false, ACT_NONE))
+    EDSL_DIRECT16_CASE(epi_code(true, ACT_NONE))
+    EDSL_DIRECT16_CASE(epi_code(false, ACT_RELU))
+    EDSL_DIRECT16_CASE(epi_code(true, ACT_RELU))
+    EDSL_DIRECT16_CASE(epi_code(false, ACT_LEAKY))
+    EDSL_DIRECT16_CASE(epi_code(true, ACT_LEAKY))
+    EDSL_DIRECT16_CASE(epi_code(false, ACT_IF_RELU))
+    EDSL_DIRECT16_CASE(epi_code(true, ACT_IF_RELU))
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef EDSL_DIRECT16_CASE
+  return hipGetLastError();
+}
+
 template <int GUARD>
 hipError_t launch_guard(int epi, const GemmF32Args& a, hipStream_t stream) {
   const dim3 grid(a.tiles_m * a.tiles_n);
@@ -490,6 +579,13 @@ hipError_t launch_gemm_f32_direct64(int ksplit, int guard, int epi, GemmF32Args 
     return launch_ks64<4, kGuardEdge>(epi, a, stream);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemm_f32_direct16(int epi, GemmF32Args a, hipStream_t stream) {
+  if (!direct_operands_ok(epi, a)) return hipErrorInvalidValue;
+  if (a.M % 16 || a.N % 16 || a.K % 64 || a.K > 64 * kMaxGroups16) return hipErrorInvalidValue;
+  if (a.tiles_m != a.M / 16 || a.tiles_n != a.N / 16) return hipErrorInvalidValue;
+  return launch_direct16(epi, a, stream);
 }
 
 }  // namespace edsl

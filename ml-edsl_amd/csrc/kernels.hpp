@@ -41,6 +41,9 @@ hipError_t launch_gemm_f32_direct(int guard, int epi, GemmF32Args args, hipStrea
 // guard kGuardNone: M and N multiples of 64, K of 16 * ksplit; kGuardEdge
 // (ksplit 4): any such M, N, K.
 hipError_t launch_gemm_f32_direct64(int ksplit, int guard, int epi, GemmF32Args args, hipStream_t stream);
+// The 16x16 tile for small layers: K split over four waves, every fragment
+// loaded up front; M and N multiples of 16, K a multiple of 64 up to 512.
+hipError_t launch_gemm_f32_direct16(int epi, GemmF32Args args, hipStream_t stream);
 
 // ------------------------------------------------------------ fp32 small-M
 struct GemvF32Args {

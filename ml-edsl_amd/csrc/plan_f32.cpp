@@ -51,6 +51,8 @@ namespace {
 //      split two or eight ways measured no better than four (1024^3 19.5-19.6
 //      against 18.2-19.6 us, 4096x4096x512 121.3 against 121.7 us) and is
 //      not built.
+//  kF32Direct16K4: the one-wave 16x16 tile for small layers, K split over
+//      four waves of a workgroup with every fragment loaded up front.
 const GemmF32Config kConfigs[] = {
     {64, 64, 16, 2, 2, kGuardAll, "f32_64x64x16_w2x2_guard"},
     {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k4_pf4"},
@@ -73,6 +75,7 @@ const GemmF32Config kConfigs[] = {
     {64, 64, 16, 1, 1, kGuardNone, "f32_64x64x16_direct"},
     {64, 64, 64, 1, 1, kGuardNone, "f32_64x64x64_direct_k4"},
     {64, 64, 64, 1, 1, kGuardEdge, "f32_64x64x64_direct_k4_edge"},
+    {16, 16, 64, 1, 1, kGuardNone, "f32_16x16x64_direct_k4"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 static_assert(kNumConfigs == kF32Tiles, "one table entry per F32Tile");
@@ -98,7 +101,9 @@ int plan_f32_tile(const F32TileQuery& q) {
   auto fits = [&](int c) {
     const GemmF32Config& g = gemm_f32_config(c);
     if ((c == kF32Direct128 || c == kF32Direct128Edge || c == kF32Direct64 || c == kF32Direct64K4 ||
-         c == kF32Direct64K4Edge) && !direct_ok)
+         c == kF32Direct64K4Edge || c == kF32Direct16K4) && !direct_ok)
+      return false;
+    if (c == kF32Direct16K4 && K > 512)
       return false;
     if (g.guard == kGuardNone) return aligned && K > 0 && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
     if (g.guard == kGuardEdge) return edge_ok;
@@ -232,6 +237,15 @@ int plan_f32_tile(const F32TileQuery& q) {
           cd = pick({kF32Direct64K4Edge});
         }
         if (cd >= 0) cfg = cd;
+      }
+      // Small layers of at most one 16x16 tile per CU, K up to 512: the 16x16
+      // one-wave tile with K split over four waves and every load up front
+      // (256^3 2.9 against 4.4 us on the 32x32 tile; 256x512x256 3.6 against
+      // 6.0 us). With more tiles it ties or loses (512x256x512 4.8 against
+      // 4.8 us, 512^3 7.5 against 6.6 us).
+      if (cfg < 0 && tiles_of(kF32Direct16K4) <= q.cus) {
+        const int c16 = pick({kF32Direct16K4});
+        if (c16 >= 0) cfg = c16;
       }
       if (cfg < 0 && !skip128) consider(c128);
       if (cfg < 0) consider(c64);

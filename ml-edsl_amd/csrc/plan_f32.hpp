@@ -48,6 +48,7 @@ enum F32Tile : int {
   kF32Direct64,         // 64x64x16, one wave per tile, no LDS
   kF32Direct64K4,       // 64x64x64, four waves splitting K, partials summed through LDS
   kF32Direct64K4Edge,
+  kF32Direct16K4,       // 16x16x64, four waves splitting K, every load up front (small layers)
   kF32Tiles
 };
 int gemm_f32_num_configs();

@@ -104,7 +104,8 @@ def test_aligned_shapes_keep_their_tiles(torch_cuda):
                             ((3072, 512, 3072), "f32_64x64x64_direct_k4"),
                             ((2048, 128, 2048), "f32_128x128x32_mfma16_w8"),
                             ((1024, 128, 1024), "f32_64x64x64_mfma16"),
-                            ((256, 256, 256), "f32_32x32x64_w1x1_k4_pf4")):
+                            ((256, 256, 256), "f32_16x16x64_direct_k4"),
+                            ((512, 512, 512), "f32_32x32x64_w1x1_k4_pf4")):
         X, W, b = _inputs(M, K, N, 7)
         got, plan = _run(torch_cuda, X, W, b)
         assert f"cfg={tile} " in plan, plan
@@ -477,6 +478,8 @@ MFMA16_SHAPES = {
     # the 64x64 tile: one to seven groups per wave, K unsplit and split four ways
     "f32_64x64x16_direct": [(64, 16, 64), (128, 32, 64), (64, 48, 192), (192, 2048, 128), (1024, 160, 64),
                             (64, 208, 1024)],
+    # the 16x16 tile for small layers: one to eight groups per wave, every load up front
+    "f32_16x16x64_direct_k4": [(80, 64, 48), (256, 256, 256), (96, 512, 160), (1024, 128, 32), (128, 448, 16)],
     "f32_64x64x64_direct_k4": [(64, 64, 64), (128, 128, 64), (64, 192, 192), (192, 2048, 128),
                                (1024, 320, 64), (64, 448, 1024), (1024, 1024, 1024)],
     "f32_128x128x32_mfma16": [(128, 32, 128), (256, 64, 128), (128, 96, 384), (384, 2048, 256),
