@@ -211,7 +211,7 @@ int plan_f32_tile(const F32TileQuery& q) {
       }
       // The one-wave 64x64 tiles (gemm_f32_direct.hip) take every layer of
       // whole 64x64 tiles that the one-wave 128x128 tile does not fill, from
-      // one tile per CU on: with K split over four waves of a workgroup, or
+      // about one tile per CU on: with K split over four waves of a workgroup, or
       // unsplit where the tiles fill one or two waves per SIMD exactly. Same
       // box against the tiles the model above picks: 1024^3 18.2 against 18.9
       // us, 4096x4096x512 121.7 against 134.3 us, 2048^3 (unsplit) 117.3
@@ -229,7 +229,10 @@ int plan_f32_tile(const F32TileQuery& q) {
         const int64_t t64n = ((M + 63) / 64) * ((N + 63) / 64);
         int cd = -1;
         if (M % 64 == 0 && N % 64 == 0) {
-          if (t64n >= q.cus) {
+          // From three quarters of a tile per CU (768x256x1024: 192 tiles, 7.9
+          // against 9.0 us on the 32x32 tiles; 768x1024x1024 18.8 against 23.0
+          // us); fewer tiles lose (320x448x1536, 120 tiles: 10.3 against 9.3 us).
+          if (4 * t64n >= 3 * q.cus) {
             if (t64n % (4 * q.cus) == 0 && t64n <= 8 * q.cus) cd = pick({kF32Direct64});
             if (cd < 0) cd = pick({kF32Direct64K4});
           }

@@ -106,6 +106,35 @@ def test_random_large_case(seed, torch_cuda):
                 torch_cuda)
 
 
+# Layers of whole 16-, 64- and 128-row tiles on 16-byte aligned views, fp32:
+# the one-wave tiles of gemm_f32_direct.hip (16x16 and 64x64 with K split over
+# four waves, 64x64 unsplit, 128x128), each seed checked against the oracle and
+# the set of seeds required to reach every one of them.
+_ONE_WAVE_MN = [256, 320, 768, 1024, 1088, 1536, 2048, 2560, 4096]
+_ONE_WAVE_K = [64, 256, 448, 512, 1024, 1536]
+
+
+def test_random_one_wave_tiles(torch_cuda):
+    plans = []
+    for seed in range(5000, 5024):
+        rng = np.random.default_rng(seed)
+        M, N = (int(rng.choice(_ONE_WAVE_MN)) for _ in range(2))
+        K = int(rng.choice(_ONE_WAVE_K))
+        if seed == 5000:
+            M, N, K = 256, 256, 256      # the 16x16 tile
+        elif seed == 5001:
+            M, N, K = 2048, 2048, 512    # 64x64 unsplit
+        elif seed == 5002:
+            M, N, K = 4096, 4096, 256    # 128x128
+        pattern = list(_PATTERNS)[int(rng.integers(len(_PATTERNS)))]
+        pad, off = ((0, 0), (4, 4), (8, 0))[seed % 3]
+        case = (rng, M, K, N, "f32", pattern, True, pad, off, False)
+        _check_case(seed, case, torch_cuda)
+        plans.append(_native.last_plan())
+    for tile in ("f32_16x16x64_direct_k4", "f32_64x64x64_direct_k4", "f32_64x64x16_direct ", "f32_128x128x16_direct "):
+        assert any(tile in p + " " for p in plans), (tile, plans)
+
+
 def _check_case(seed, case, torch):
     rng, M, K, N, dtype, pattern, device, pad, off, wide = case
     bias, act = _PATTERNS[pattern]
