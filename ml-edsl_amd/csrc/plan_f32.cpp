@@ -221,22 +221,25 @@ int plan_f32_tile(const F32TileQuery& q) {
       // us), and so do more than two unsplit waves per SIMD (4096^3 unsplit:
       // 1120 us). Short K (below 256) is left to the tiles above.
       // Partial 64x64 tiles take the K-split edge twin from one tile per CU
-      // to four (1000^3 21.8 against 23.6 us, 1000x4000x1000 64.0 against
-      // 68.7 us on the LDS-staged 64x64 edge tile); with more tiles it ties
-      // (3000^3 428 against 440 us, 4097x4096x4096 1056 against 1052 us), and
-      // short K is slower (4097x256x4096 114 against 88 us).
+      // to two (1000^3 21.8 against 23.6 us, 1000x4000x1000 64.0 against
+      // 68.7 us on the LDS-staged 64x64 edge tile); at four per CU it loses
+      // to the eight-wave 128x128 edge tile (2000^3 133.4 against 121.8 us),
+      // with more it ties (3000^3 428 against 440 us, 4097x4096x4096 1056
+      // against 1052 us), and short K is slower (4097x256x4096 114 against
+      // 88 us).
       if (cfg != kF32Direct128 && cfg != kF32Direct128Edge && K >= 256) {
         const int64_t t64n = ((M + 63) / 64) * ((N + 63) / 64);
         int cd = -1;
         if (M % 64 == 0 && N % 64 == 0) {
-          // From three quarters of a tile per CU (768x256x1024: 192 tiles, 7.9
-          // against 9.0 us on the 32x32 tiles; 768x1024x1024 18.8 against 23.0
-          // us); fewer tiles lose (320x448x1536, 120 tiles: 10.3 against 9.3 us).
-          if (4 * t64n >= 3 * q.cus) {
+          // From 9/16 of a tile per CU (768^3: 144 tiles, 15.1 against 18.3 us
+          // on the 32x32 tiles; 768x256x1024, 192 tiles: 7.9 against 9.0 us;
+          // 768x1024x1024 18.8 against 23.0 us); fewer tiles lose
+          // (320x448x1536, 120 tiles: 10.3 against 9.3 us).
+          if (16 * t64n >= 9 * q.cus) {
             if (t64n % (4 * q.cus) == 0 && t64n <= 8 * q.cus) cd = pick({kF32Direct64});
             if (cd < 0) cd = pick({kF32Direct64K4});
           }
-        } else if (K >= 512 && t64n >= q.cus && t64n <= 4 * q.cus) {
+        } else if (K >= 512 && t64n >= q.cus && t64n <= 2 * q.cus) {
           cd = pick({kF32Direct64K4Edge});
         }
         if (cd >= 0) cfg = cd;
