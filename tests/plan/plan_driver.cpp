@@ -1,4 +1,4 @@
-// Prints the fp32 tile plan for each query line "M N K aligned cus" on
+// Prints the fp32 tile plan for each query line "M N K aligned cus [lda ldb]" on
 // stdin, and the configuration table for the line "table". Built with g++
 // against ml-edsl_amd/csrc/plan_f32.cpp alone (no HIP). Test infrastructure.
 #include <cstdio>
@@ -16,11 +16,16 @@ int main() {
       }
       continue;
     }
-    long long M, N, K;
+    long long M, N, K, lda = -1, ldb = -1;
     int aligned, cus;
-    if (sscanf(line, "%lld %lld %lld %d %d", &M, &N, &K, &aligned, &cus) != 5) return 2;
-    // Contiguous operands: row strides K and N.
-    const int c = edsl::plan_f32_tile(edsl::F32TileQuery{M, N, K, K, N, aligned != 0, cus, -1});
+    const int got = sscanf(line, "%lld %lld %lld %d %d %lld %lld", &M, &N, &K, &aligned, &cus, &lda, &ldb);
+    if (got != 5 && got != 7) return 2;
+    // Row strides K and N (contiguous operands) unless given.
+    if (got == 5) {
+      lda = K;
+      ldb = N;
+    }
+    const int c = edsl::plan_f32_tile(edsl::F32TileQuery{M, N, K, lda, ldb, aligned != 0, cus, -1});
     printf("%s\n", edsl::gemm_f32_config(c).name);
   }
   return 0;

@@ -105,3 +105,25 @@ def test_plans_follow_the_bounds_rules(driver):
             assert al and M % bm == 0 and N % bn == 0 and K % bk == 0, (M, N, K, name)
         elif guard == 1:  # edge tiles
             assert al and K % 4 == 0 and N % 4 == 0 and K >= 4 and N >= 4, (M, N, K, name)
+
+
+def test_one_wave_tiles_need_32_bit_buffer_offsets(driver):
+    """The one-wave tiles address A and B through buffer descriptors with
+    32-bit byte offsets: a row stride that puts K rows of B (or 128 rows of
+    A) past 2^31 bytes must plan an LDS-staged tile instead."""
+    def plan(M, N, K, lda, ldb):
+        out = subprocess.run([driver], input=f"{M} {N} {K} 1 {CUS} {lda} {ldb}\n", capture_output=True,
+                             text=True, check=True).stdout
+        return out.split()[0]
+    assert plan(4096, 4096, 4096, 4096, 4096) == "f32_128x128x16_direct"
+    assert plan(1024, 1024, 1024, 1024, 1024) == "f32_64x64x64_direct_k4"
+    # K rows of B past 2^31 bytes: 4096 rows of 2^17 floats = 2 GiB
+    big_ldb = 1 << 17
+    assert "direct" not in plan(4096, 4096, 4096, 4096, big_ldb)
+    assert "direct" not in plan(1024, 1024, 1024, 1024, 1 << 19)
+    # 128 rows of A past 2^31 bytes
+    assert "direct" not in plan(4096, 4096, 4096, 1 << 22, 4096)
+    # just inside: (K + 16) * ldb * 4 + 1024 <= 2^31 - 1
+    ldb_ok = ((2**31 - 1 - 1024) // ((4096 + 16) * 4)) // 4 * 4
+    assert plan(4096, 4096, 4096, 4096, ldb_ok) == "f32_128x128x16_direct"
+    assert "direct" not in plan(4096, 4096, 4096, 4096, ldb_ok + 4 * 64)
