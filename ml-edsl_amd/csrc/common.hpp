@@ -70,6 +70,30 @@ __device__ __forceinline__ int32_t apply_epilogue_i32(int32_t acc, int32_t b) {
   return y;
 }
 
+// Raw buffer loads: the <4 x i32> descriptor form of the intrinsics, so that a
+// descriptor built from uniform values stays in scalar registers. A load whose
+// per-lane offset lies at or past the descriptor's byte count reads zero.
+// (These names bind to the intrinsics; they have no definitions.)
+__device__ f32x4 raw_buffer_load_f32x4(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4f32");
+__device__ float raw_buffer_load_f32(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.f32");
+__device__ i32x4 raw_buffer_load_i32x4(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+
+// Descriptor of `bytes` bytes from `base` (raw addressing: stride 0, the
+// 32-bit data format word of the gfx9 family), clamped to [0, 2^31 - 1].
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, int64_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const int n = bytes > 0x7fffffff ? 0x7fffffff : bytes < 0 ? 0 : (int)bytes;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
+  r[2] = __builtin_amdgcn_readfirstlane(n);
+  r[3] = 0x00020000;
+  return r;
+}
+
 // Workgroup -> output tile mapping.
 //
 // The hardware hands workgroup w to XCD (w % 8). Each XCD has its own L2, so

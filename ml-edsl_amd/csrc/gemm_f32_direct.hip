@@ -43,15 +43,6 @@
 
 namespace edsl {
 
-// Raw buffer loads (the <4 x i32> descriptor form of the intrinsics, so that
-// a descriptor built from uniform values stays in scalar registers). Offsets
-// at or past the descriptor's byte count read zero. Declared outside the
-// anonymous namespace: these names bind to intrinsics, not to definitions.
-__device__ f32x4 raw_buffer_load_f32x4(i32x4 rsrc, int voffset, int soffset, int aux)
-    __asm("llvm.amdgcn.raw.buffer.load.v4f32");
-__device__ float raw_buffer_load_f32(i32x4 rsrc, int voffset, int soffset, int aux)
-    __asm("llvm.amdgcn.raw.buffer.load.f32");
-
 namespace {
 
 template <int N>
@@ -64,19 +55,6 @@ __device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int
 template <int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-// Descriptor of `bytes` bytes from `base` (raw addressing: stride 0, 32-bit
-// data format word of the gfx9 family).
-__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, int64_t bytes) {
-  const uint64_t p = reinterpret_cast<uint64_t>(base);
-  const int n = bytes > 0x7fffffff ? 0x7fffffff : bytes < 0 ? 0 : (int)bytes;
-  i32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)p);
-  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
-  r[2] = __builtin_amdgcn_readfirstlane(n);
-  r[3] = 0x00020000;
-  return r;
 }
 
 constexpr int kTile = 128;

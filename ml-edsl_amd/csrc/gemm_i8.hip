@@ -355,12 +355,17 @@ gemm_i8_ksplit_kernel(GemmI32Args a) {
   }
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int KT = a.Kp >> 5;  // 32-k steps of the padded K, a multiple of 4
   const int NS = KT >> 2;   // steps per wave, a multiple of D
-  const i32x4* ap = reinterpret_cast<const i32x4*>(a.A8p) + (int64_t)(m0 >> 5) * KT * 64 + lane;
-  const i32x4* bp = reinterpret_cast<const i32x4*>(a.B8p) + (int64_t)(n0 >> 5) * KT * 64 + lane;
-  const int64_t block_stride = (int64_t)KT * 64;  // next 32-row (or 32-column) block
+  // The tile's four 32-row blocks of packed X and four 32-column blocks of
+  // packed W, read through buffer descriptors: the lane's 16 bytes at a
+  // per-lane offset, the block and step at a scalar one (no 64-bit address
+  // arithmetic in the loop).
+  const int block_bytes = KT * 64 * 16;  // one 32-row (or 32-column) block: KT fragments
+  const i32x4 rsrc_a = buffer_rsrc(a.A8p + (int64_t)(m0 >> 5) * block_bytes, 4 * (int64_t)block_bytes);
+  const i32x4 rsrc_b = buffer_rsrc(a.B8p + (int64_t)(n0 >> 5) * block_bytes, 4 * (int64_t)block_bytes);
+  const int vlane = lane * 16;
 
   i32x16 acc[4][4];
 #pragma unroll
@@ -377,11 +382,11 @@ gemm_i8_ksplit_kernel(GemmI32Args a) {
   // accumulators between registers before the tail.)
   i32x4 fa[D][4], fb[D][4];
   auto load = [&](i32x4(&xa)[4], i32x4(&xb)[4], int t) {
-    const int64_t s = (int64_t)(min(t, NS - 1) * 4 + wave) * 64;
+    const int s = (min(t, NS - 1) * 4 + wave) * 64 * 16;  // the step's fragment, in bytes
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xa[i] = ap[i * block_stride + s];
+    for (int i = 0; i < 4; ++i) xa[i] = raw_buffer_load_i32x4(rsrc_a, vlane, i * block_bytes + s, 0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xb[j] = bp[j * block_stride + s];
+    for (int j = 0; j < 4; ++j) xb[j] = raw_buffer_load_i32x4(rsrc_b, vlane, j * block_bytes + s, 0);
   };
 #pragma unroll
   for (int d = 0; d < D; ++d) {
