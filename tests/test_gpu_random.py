@@ -115,8 +115,13 @@ _ONE_WAVE_K = [64, 256, 448, 512, 1024, 1536]
 
 
 def test_random_one_wave_tiles(torch_cuda):
+    """24 seeds; EDSL_ONE_WAVE_SWEEP=N adds N more (progress every 100 with -s)."""
+    import os
+    extra = int(os.environ.get("EDSL_ONE_WAVE_SWEEP", "0"))
     plans = []
-    for seed in range(5000, 5024):
+    for seed in range(5000, 5024 + extra):
+        if seed >= 5024 and (seed - 5024) % 100 == 0:
+            print(f"one-wave sweep: {seed - 5024} of {extra} extra seeds passed", flush=True)
         rng = np.random.default_rng(seed)
         M, N = (int(rng.choice(_ONE_WAVE_MN)) for _ in range(2))
         K = int(rng.choice(_ONE_WAVE_K))
