@@ -1,4 +1,8 @@
-// fp32 dense layer / matmul with one wave per 128x128 output tile and no LDS.
+// fp32 dense layer / matmul with one wave per output tile and no LDS stage:
+// a 128x128 tile (large layers), its 64x64 twin with K optionally split over
+// four waves of a workgroup (mid-size layers) and a 16x16 tile with K split
+// over four waves (small layers). The K-split tiles sum their partial tiles
+// once through LDS; nothing else goes through LDS.
 //
 // C[M,N] = epilogue(A[M,K] x B[K,N] (+ bias[N])) -- the same op as the tiles
 // of gemm_f32.hip and gemm_f32_m16.hip (reference
@@ -31,10 +35,13 @@
 //
 // GUARD kGuardNone: M, N multiples of 128 and K of 16. kGuardEdge: partial
 // tiles (N and K multiples of 4). There the range check of the buffer loads
-// does the bounds work: every offset that can leave an operand is in the
-// per-lane offset (the scalar offset is zero), rows past M read zero, columns
-// past N read values whose outputs are never stored, and A chunks past K are
-// sent out of range so that they read zero (B rows past K read zero too).
+// does the bounds work: every offset that can leave an operand -- a row of A
+// past M, a row of B past K -- is in the per-lane offset, the scalar offset
+// adding only the k position inside a row of A and the k slot (below 4)
+// inside a lane's chunk of B rows. Rows past M read zero, B columns past N
+// are clamped to column N-4 (their outputs are never stored), and A chunks
+// past K are sent out of range so that they read zero, as do the B rows that
+// pair with them.
 #include "common.hpp"
 #include "kernels.hpp"
 
