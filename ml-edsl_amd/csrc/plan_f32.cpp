@@ -211,7 +211,7 @@ int plan_f32_tile(const F32TileQuery& q) {
       }
       // The one-wave 64x64 tiles (gemm_f32_direct.hip) take every layer of
       // whole 64x64 tiles that the one-wave 128x128 tile does not fill, from
-      // about one tile per CU on: with K split over four waves of a workgroup, or
+      // about half a tile per CU on: with K split over four waves of a workgroup, or
       // unsplit where the tiles fill one or two waves per SIMD exactly. Same
       // box against the tiles the model above picks: 1024^3 18.2 against 18.9
       // us, 4096x4096x512 121.7 against 134.3 us, 2048^3 (unsplit) 117.3
