@@ -227,7 +227,7 @@ gemm_f32_direct_kernel(GemmF32Args args) {
 // of 16-deep groups -- with the same fragment loads as the 128x128 tile (one
 // 4-column quad of B per k slot), and the same edge handling. The KS partial tiles are then summed
 // through LDS in a fixed order (wave 0 + wave 1 + ...), each wave finishing
-// 16/KS of the 16 rows each lane holds. Groups are 64 MFMAs (~0.85 us), so loads run two groups
+// 4/KS of the tile's four row blocks. Groups are 64 MFMAs (~0.85 us), so loads run two groups
 // ahead in three register sets. For layers with too few 128x128 tiles to fill
 // the SIMDs (1024^3: 256 tiles of 64x64, K split four ways).
 constexpr int kSets64 = 3;
@@ -363,32 +363,37 @@ gemm_f32_direct64_kernel(GemmF32Args args) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) store_row(i, e, f32x4{acc[i][0][e], acc[i][1][e], acc[i][2][e], acc[i][3][e]});
   } else {
-    // [wave][row block][column block][e][lane]: 64 lanes write and read 256
-    // contiguous bytes per access, no bank conflict. The 16 (row block, e)
-    // rows of each lane are shared out, 16/KS per wave.
-    __shared__ float red[KS * RB4 * CB4 * 4 * 64];
-    auto word = [&](int w, int i, int c, int e) { return (((w * RB4 + i) * CB4 + c) * 4 + e) * 64 + lane; };
+    // [wave][row block][column block][lane] of 16-byte accumulator vectors:
+    // each access moves 64 lanes x 16 contiguous bytes, no bank conflict.
+    // Wave w finishes row blocks w*RB4/KS ..: for each of its blocks and
+    // column blocks it reads the KS partials as vectors and sums them in
+    // wave order.
+    static_assert(RB4 % KS == 0, "row blocks per wave");
+    __shared__ f32x4 red[KS * RB4 * CB4 * 64];
+    auto slot = [&](int w, int i, int c) { return ((w * RB4 + i) * CB4 + c) * 64 + lane; };
 #pragma unroll
     for (int i = 0; i < RB4; ++i)
 #pragma unroll
-      for (int c = 0; c < CB4; ++c)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) red[word(wave, i, c, e)] = acc[i][c][e];
+      for (int c = 0; c < CB4; ++c) red[slot(wave, i, c)] = acc[i][c];
     __syncthreads();
-    constexpr int kUnits = RB4 * 4 / KS;
+    constexpr int kBlocks = RB4 / KS;  // row blocks each wave finishes
 #pragma unroll
-    for (int r = 0; r < kUnits; ++r) {
-      const int u = wave * kUnits + r;
-      const int i = u / 4, e = u % 4;
-      f32x4 sums;
+    for (int r = 0; r < kBlocks; ++r) {
+      const int i = wave * kBlocks + r;
+      f32x4 sums[CB4];  // [column block][e]
 #pragma unroll
       for (int c = 0; c < CB4; ++c) {
-        float sum = red[word(0, i, c, e)];
+        f32x4 sum = red[slot(0, i, c)];
 #pragma unroll
-        for (int w = 1; w < KS; ++w) sum = __fadd_rn(sum, red[word(w, i, c, e)]);
+        for (int w = 1; w < KS; ++w) {
+          const f32x4 p = red[slot(w, i, c)];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sum[e] = __fadd_rn(sum[e], p[e]);
+        }
         sums[c] = sum;
       }
-      store_row(i, e, sums);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) store_row(i, e, f32x4{sums[0][e], sums[1][e], sums[2][e], sums[3][e]});
     }
   }
 }
