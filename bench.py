@@ -506,7 +506,17 @@ def trace_summary(trace_csv: str, line_json: str, wname: str | None, warmup: int
         steps, warmup = SECONDARY_PLAN[wname][0], SECONDARY_PLAN[wname][1]
     with open(trace_csv) as f:
         rows = sorted(csv.DictReader(f), key=lambda r: int(r["Dispatch_Id"]))
-    disp = [(r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3) for r in rows]
+    # A kernel that runs with several grids (the same tile for two workloads)
+    # is told apart by its grid, so that one workload's steps are not mixed
+    # with another's.
+    grids: dict[str, set] = {}
+    for r in rows:
+        grids.setdefault(r["Kernel_Name"], set()).add(r.get("Grid_Size_X", r.get("Grid_Size", "")))
+
+    def key(r):
+        g = r.get("Grid_Size_X", r.get("Grid_Size", ""))
+        return r["Kernel_Name"] + (f" [grid {g}]" if len(grids[r["Kernel_Name"]]) > 1 else "")
+    disp = [(key(r), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3) for r in rows]
     by_name: dict[str, list[float]] = {}
     for name, us in disp:
         by_name.setdefault(name, []).append(us)
