@@ -554,7 +554,10 @@ def trace_summary(trace_csv: str, line_json: str, wname: str | None, warmup: int
     _, lead, st = best
     out = ["| kernel | dispatches | mean us | median us |", "|---|---|---|---|"]
     for n, v in sorted(by_name.items(), key=lambda kv: -sum(kv[1])):
-        short = n if len(n) <= 90 else n[:87] + "..."
+        base, sep, grid = n.partition(" [grid ")
+        short = base if len(base) <= 90 else base[:87] + "..."
+        if sep:
+            short += sep + grid
         out.append(f"| `{short}` | {len(v)} | {statistics.mean(v):.1f} | {statistics.median(v):.1f} |")
     kinds = sorted({nm for s in st[:block] for nm, _ in s}, key=lambda nm: nm != lead)
     out += ["", f"Workload {wname}: a step is `{lead}`" +
