@@ -71,18 +71,13 @@ constexpr int kSets = 2;   // register sets of loads: the current group and the 
 constexpr int kSlices = 16;
 constexpr int kOutOfRange = 0x7fffffff;  // a per-lane offset past every descriptor
 
-template <int GUARD, int EPI>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
-gemm_f32_direct_kernel(GemmF32Args args) {
-  static_assert(GUARD == kGuardNone || GUARD == kGuardEdge, "guard");
-  constexpr bool kEdge = GUARD == kGuardEdge;
+// One 128x128 tile at (m0, n0): kEdge selects the edge loads and the checked
+// stores.
+template <bool kEdge, int EPI>
+__device__ __forceinline__ void direct128_tile(const GemmF32Args& args, int m0, int n0) {
   const int lane = threadIdx.x;
   const int g = lane >> 4;
   const int r16 = lane & 15;
-  int tm, tn;
-  tile_coords(blockIdx.x, args.tiles_m, args.tiles_n, tm, tn);
-  const int m0 = __builtin_amdgcn_readfirstlane(tm * kTile);
-  const int n0 = __builtin_amdgcn_readfirstlane(tn * kTile);
   const int K = args.K;
   const int ng = (K + 15) / 16;  // 16-deep groups (the last one partial on edge tiles)
   const int lda = (int)args.lda, ldb = (int)args.ldb;
@@ -219,6 +214,27 @@ gemm_f32_direct_kernel(GemmF32Args args) {
     // One row block at a time: the scheduler would otherwise gather the
     // values of many blocks and run out of registers.
     __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int GUARD, int EPI>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_f32_direct_kernel(GemmF32Args args) {
+  static_assert(GUARD == kGuardNone || GUARD == kGuardEdge, "guard");
+  int tm, tn;
+  tile_coords(blockIdx.x, args.tiles_m, args.tiles_n, tm, tn);
+  const int m0 = __builtin_amdgcn_readfirstlane(tm * kTile);
+  const int n0 = __builtin_amdgcn_readfirstlane(tn * kTile);
+  if constexpr (GUARD == kGuardNone) {
+    direct128_tile<false, EPI>(args, m0, n0);
+  } else {
+    // Edge layers: the tiles that lie inside M x N with a K of whole groups
+    // take the exact tile's loads and stores; only the others pay for the
+    // per-lane bounds.
+    if (m0 + kTile <= args.M && n0 + kTile <= args.N && args.K % 16 == 0)
+      direct128_tile<false, EPI>(args, m0, n0);
+    else
+      direct128_tile<true, EPI>(args, m0, n0);
   }
 }
 
