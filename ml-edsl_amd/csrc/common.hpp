@@ -76,6 +76,8 @@ __device__ __forceinline__ int32_t apply_epilogue_i32(int32_t acc, int32_t b) {
 // (These names bind to the intrinsics; they have no definitions.)
 __device__ f32x4 raw_buffer_load_f32x4(i32x4 rsrc, int voffset, int soffset, int aux)
     __asm("llvm.amdgcn.raw.buffer.load.v4f32");
+__device__ f32x2 raw_buffer_load_f32x2(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v2f32");
 __device__ float raw_buffer_load_f32(i32x4 rsrc, int voffset, int soffset, int aux)
     __asm("llvm.amdgcn.raw.buffer.load.f32");
 __device__ i32x4 raw_buffer_load_i32x4(i32x4 rsrc, int voffset, int soffset, int aux)

@@ -1,8 +1,10 @@
 // fp32 dense layer / matmul with one wave per output tile and no LDS stage:
 // a 128x128 tile (large layers), its 64x64 twin with K optionally split over
-// four waves of a workgroup (mid-size layers) and a 16x16 tile with K split
-// over four waves (small layers). The K-split tiles sum their partial tiles
-// once through LDS; nothing else goes through LDS.
+// four waves of a workgroup (mid-size layers), R x C tiles of 32x32 to 96x96
+// with K split over four waves (mid-size layers whose 64x64 tiles do not fill
+// whole rounds of the CUs) and a 16x16 tile with K split over four waves
+// (small layers). The K-split tiles sum their partial tiles once through LDS;
+// nothing else goes through LDS.
 //
 // C[M,N] = epilogue(A[M,K] x B[K,N] (+ bias[N])) -- the same op as the tiles
 // of gemm_f32.hip and gemm_f32_m16.hip (reference
@@ -523,6 +525,241 @@ hipError_t launch_direct16(int epi, const GemmF32Args& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// The R x C tile (16R x 16C outputs, K split over the four waves of a
+// workgroup) for layers whose 64x64 tiles do not fill whole rounds of the
+// CUs: 768^3 is 256 tiles of 48x48 (R = C = 3) and 1536^3 256 tiles of 96x96
+// (R = C = 6), one workgroup per CU and one wave per SIMD, so every SIMD runs
+// the same number of MFMAs in one round. Each wave computes the whole tile
+// over a quarter of K with the 64x64 tile's A fragments and its loop (loads
+// two 16-deep groups ahead in three register sets). B columns come in pieces
+// of 64, 32 or 16 columns, read with 16-, 8- or 4-byte loads per lane and k
+// slot: in a piece of width w (column blocks first .. first + w - 1) lane r16
+// holds columns n0 + 16 first + w r16 + c, c < w, the c-th of them in column
+// block first + c, so the lane's outputs of a row are w adjacent columns.
+// The four partial tiles are summed through LDS in wave order; wave w
+// finishes row 4g + w of every row block (R x C x 4 KiB of LDS: 144 KiB for
+// 6 x 6).
+template <int C>
+struct ColPieces {
+  static constexpr int n4 = C / 4, n2 = (C % 4) / 2, n1 = C % 2;
+  static constexpr int count = n4 + n2 + n1;
+  static constexpr int width(int p) { return p < n4 ? 4 : (p < n4 + n2 ? 2 : 1); }
+  static constexpr int first(int p) {
+    return p < n4 ? 4 * p : (p < n4 + n2 ? 4 * n4 + 2 * (p - n4) : 4 * n4 + 2 * n2);
+  }
+};
+
+template <int W>
+__device__ __forceinline__ void load_piece(float* dst, i32x4 rsrc, int voffset, int soffset) {
+  if constexpr (W == 4) {
+    const f32x4 v = raw_buffer_load_f32x4(rsrc, voffset, soffset, 0);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) dst[c] = v[c];
+  } else if constexpr (W == 2) {
+    const f32x2 v = raw_buffer_load_f32x2(rsrc, voffset, soffset, 0);
+    dst[0] = v[0];
+    dst[1] = v[1];
+  } else {
+    dst[0] = raw_buffer_load_f32(rsrc, voffset, soffset, 0);
+  }
+}
+
+template <int W>
+struct VecOf;
+template <>
+struct VecOf<4> { using T = f32x4; };
+template <>
+struct VecOf<2> { using T = f32x2; };
+template <>
+struct VecOf<1> { using T = float; };
+
+template <int R, int C, int EPI>
+__global__ void __launch_bounds__(256)
+gemm_f32_direct_rc_kernel(GemmF32Args args) {
+  using P = ColPieces<C>;
+  constexpr int KS = 4;
+  constexpr int kLoads = R + 4 * P::count;  // per group: one per row block, one per piece and k slot
+  constexpr int kMfmas = 4 * R * C;         // per group
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4;
+  const int r16 = lane & 15;
+  int tm, tn;
+  tile_coords(blockIdx.x, args.tiles_m, args.tiles_n, tm, tn);
+  const int m0 = __builtin_amdgcn_readfirstlane(tm * 16 * R);
+  const int n0 = __builtin_amdgcn_readfirstlane(tn * 16 * C);
+  const int ngw = args.K / 16 / KS;  // groups per wave: K is a multiple of 64
+  const int jb = wave * ngw;
+  const int lda = (int)args.lda, ldb = (int)args.ldb;
+  const i32x4 rsrc_a = buffer_rsrc(args.A + (int64_t)m0 * lda, (int64_t)(args.M - m0) * lda * 4);
+  const i32x4 rsrc_b = buffer_rsrc(args.B + n0, (int64_t)args.K * ldb * 4 - (int64_t)n0 * 4);
+  const int va = (r16 * lda + 4 * g) * 4;  // A[m0 + 16i + r16][16j + 4g .. +3]
+  int vb[P::count];                        // B[16j + 4g + s][piece columns of the lane]
+  static_for<P::count>([&](auto pc) __attribute__((always_inline)) {
+    constexpr int p = decltype(pc)::value;
+    vb[p] = (4 * g * ldb + 16 * P::first(p) + P::width(p) * r16) * 4;
+  });
+
+  struct Frag {
+    f32x4 a[R];      // row block i: A[m0 + 16i + r16][16j + 4g .. +3]
+    float b[4][C];   // k slot s, column block c
+  };
+  auto load = [&](Frag& f, int j) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) f.a[i] = raw_buffer_load_f32x4(rsrc_a, va, 64 * j + i * 64 * lda, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      static_for<P::count>([&](auto pc) __attribute__((always_inline)) {
+        constexpr int p = decltype(pc)::value;
+        load_piece<P::width(p)>(&f.b[s][P::first(p)], rsrc_b, vb[p], (16 * j + s) * ldb * 4);
+      });
+  };
+  // The bias values of the lane's columns, loaded before the first group.
+  float biasv[C];
+  static_for<P::count>([&](auto pc) __attribute__((always_inline)) {
+    constexpr int p = decltype(pc)::value;
+    constexpr int W = P::width(p);
+#pragma unroll
+    for (int c = 0; c < W; ++c) biasv[P::first(p) + c] = 0.0f;
+    if constexpr (epi_has_bias(EPI)) {
+      const typename VecOf<W>::T v =
+          *reinterpret_cast<const typename VecOf<W>::T*>(args.bias + n0 + 16 * P::first(p) + W * r16);
+      if constexpr (W == 1) {
+        biasv[P::first(p)] = v;
+      } else {
+#pragma unroll
+        for (int c = 0; c < W; ++c) biasv[P::first(p) + c] = v[c];
+      }
+    }
+  });
+  f32x4 acc[R][C];
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[i][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto mfmas = [&](const Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+          acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[i][s], f.b[s][c], acc[i][c], 0, 0, 0);
+  };
+  // The group's loads spread evenly over its MFMAs.
+  auto pin = [&]() __attribute__((always_inline)) {
+    static_for<kLoads>([&](auto qc) __attribute__((always_inline)) {
+      constexpr int q = decltype(qc)::value;
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, (q + 1) * kMfmas / kLoads - q * kMfmas / kLoads, 0);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Group jb + t is computed from set t % 3 while groups jb + t + 1 and
+  // jb + t + 2 are in flight; loads past the wave's last group repeat it.
+  const int jl = jb + ngw - 1;
+  {
+    Frag fr[kSets64];
+    load(fr[0], jb);
+    load(fr[1], min(jb + 1, jl));
+    int t = 0;
+    for (; t + kSets64 <= ngw; t += kSets64) {
+      static_for<kSets64>([&](auto sc) __attribute__((always_inline)) {
+        constexpr int S = decltype(sc)::value;
+        load(fr[(S + 2) % kSets64], min(jb + t + S + 2, jl));
+        mfmas(fr[S]);
+        pin();
+      });
+    }
+    static_for<kSets64>([&](auto sc) __attribute__((always_inline)) {
+      constexpr int S = decltype(sc)::value;
+      if (t + S < ngw) {
+        load(fr[(S + 2) % kSets64], min(jb + t + S + 2, jl));
+        mfmas(fr[S]);
+      }
+    });
+  }
+
+  // LDS [wave][row block][e][column block][lane]: per (wave, i, e) the lane's
+  // w adjacent columns of each piece as one vector, 64 lanes contiguous.
+  __shared__ float red[KS * R * 4 * C * 64];
+  auto base = [&](int w, int i, int e) { return ((w * R + i) * 4 + e) * C * 64; };
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      static_for<P::count>([&](auto pc) __attribute__((always_inline)) {
+        constexpr int p = decltype(pc)::value;
+        constexpr int W = P::width(p);
+        constexpr int c0 = P::first(p);
+        float* dst = red + base(wave, i, e) + c0 * 64 + lane * W;
+        if constexpr (W == 4) {
+          *reinterpret_cast<f32x4*>(dst) = f32x4{acc[i][c0][e], acc[i][c0 + 1][e], acc[i][c0 + 2][e], acc[i][c0 + 3][e]};
+        } else if constexpr (W == 2) {
+          *reinterpret_cast<f32x2*>(dst) = f32x2{acc[i][c0][e], acc[i][c0 + 1][e]};
+        } else {
+          *dst = acc[i][c0][e];
+        }
+      });
+  __syncthreads();
+  const float alpha = args.alpha;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int row = m0 + 16 * i + 4 * g + wave;
+    static_for<P::count>([&](auto pc) __attribute__((always_inline)) {
+      constexpr int p = decltype(pc)::value;
+      constexpr int W = P::width(p);
+      constexpr int c0 = P::first(p);
+      using V = typename VecOf<W>::T;
+      V sum = *reinterpret_cast<const V*>(red + base(0, i, wave) + c0 * 64 + lane * W);
+#pragma unroll
+      for (int w = 1; w < KS; ++w) {
+        const V part = *reinterpret_cast<const V*>(red + base(w, i, wave) + c0 * 64 + lane * W);
+        if constexpr (W == 1) {
+          sum = __fadd_rn(sum, part);
+        } else {
+#pragma unroll
+          for (int c = 0; c < W; ++c) sum[c] = __fadd_rn(sum[c], part[c]);
+        }
+      }
+      V out;
+      if constexpr (W == 1) {
+        out = apply_epilogue_f32<EPI>(sum, biasv[c0], alpha);
+      } else {
+#pragma unroll
+        for (int c = 0; c < W; ++c) out[c] = apply_epilogue_f32<EPI>(sum[c], biasv[c0 + c], alpha);
+      }
+      __builtin_nontemporal_store(
+          out, reinterpret_cast<V*>(args.C + (int64_t)row * args.ldc + n0 + 16 * c0 + W * r16));
+    });
+  }
+}
+
+template <int R, int C>
+hipError_t launch_rc(int epi, const GemmF32Args& a, hipStream_t stream) {
+  const dim3 grid(a.tiles_m * a.tiles_n);
+  const dim3 block(256);
+#define EDSL_DIRECT_RC_CASE(E)                                                             \
+  case E:                                                                                  \
+    hipLaunchKernelGGL((gemm_f32_direct_rc_kernel<R, C, E>), grid, block, 0, stream, a);  \
+    break;
+  switch (epi) {
+    EDSL_DIRECT_RC_CASE(epi_code(false, ACT_NONE))
+    EDSL_DIRECT_RC_CASE(epi_code(true, ACT_NONE))
+    EDSL_DIRECT_RC_CASE(epi_code(false, ACT_RELU))
+    EDSL_DIRECT_RC_CASE(epi_code(true, ACT_RELU))
+    EDSL_DIRECT_RC_CASE(epi_code(false, ACT_LEAKY))
+    EDSL_DIRECT_RC_CASE(epi_code(true, ACT_LEAKY))
+    EDSL_DIRECT_RC_CASE(epi_code(false, ACT_IF_RELU))
+    EDSL_DIRECT_RC_CASE(epi_code(true, ACT_IF_RELU))
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef EDSL_DIRECT_RC_CASE
+  return hipGetLastError();
+}
+
 template <int GUARD>
 hipError_t launch_guard(int epi, const GemmF32Args& a, hipStream_t stream) {
   const dim3 grid(a.tiles_m * a.tiles_n);
@@ -592,6 +829,19 @@ hipError_t launch_gemm_f32_direct16(int epi, GemmF32Args a, hipStream_t stream) 
   if (a.M % 16 || a.N % 16 || a.K % 64 || a.K > 64 * kMaxGroups16) return hipErrorInvalidValue;
   if (a.tiles_m != a.M / 16 || a.tiles_n != a.N / 16) return hipErrorInvalidValue;
   return launch_direct16(epi, a, stream);
+}
+
+hipError_t launch_gemm_f32_direct_rc(int r, int c, int epi, GemmF32Args a, hipStream_t stream) {
+  if (!direct_operands_ok(epi, a)) return hipErrorInvalidValue;
+  if (r < 1 || c < 1 || a.M % (16 * r) || a.N % (16 * c) || a.K % 64) return hipErrorInvalidValue;
+  if (a.tiles_m != a.M / (16 * r) || a.tiles_n != a.N / (16 * c)) return hipErrorInvalidValue;
+  if (r == 2 && c == 2) return launch_rc<2, 2>(epi, a, stream);
+  if (r == 3 && c == 3) return launch_rc<3, 3>(epi, a, stream);
+  if (r == 5 && c == 5) return launch_rc<5, 5>(epi, a, stream);
+  if (r == 6 && c == 6) return launch_rc<6, 6>(epi, a, stream);
+  if (r == 3 && c == 6) return launch_rc<3, 6>(epi, a, stream);
+  if (r == 6 && c == 3) return launch_rc<6, 3>(epi, a, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace edsl

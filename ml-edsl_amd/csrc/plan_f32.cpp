@@ -53,6 +53,10 @@ namespace {
 //      not built.
 //  kF32Direct16K4: the one-wave 16x16 tile for small layers, K split over
 //      four waves of a workgroup with every fragment loaded up front.
+//  kF32DirectRC*: one-wave tiles of R x C 16x16 blocks (32x32, 48x48, 80x80,
+//      96x96, 48x96, 96x48), K split over four waves of a workgroup, for
+//      layers whose 64x64 tiles leave a round of workgroups partly empty
+//      (768^3: 144 tiles of 64x64 or 256 of 48x48, 15.3 against 10.5 us).
 const GemmF32Config kConfigs[] = {
     {64, 64, 16, 2, 2, kGuardAll, "f32_64x64x16_w2x2_guard"},
     {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k4_pf4"},
@@ -76,6 +80,12 @@ const GemmF32Config kConfigs[] = {
     {64, 64, 64, 1, 1, kGuardNone, "f32_64x64x64_direct_k4"},
     {64, 64, 64, 1, 1, kGuardEdge, "f32_64x64x64_direct_k4_edge"},
     {16, 16, 64, 1, 1, kGuardNone, "f32_16x16x64_direct_k4"},
+    {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_direct_k4"},
+    {48, 48, 64, 1, 1, kGuardNone, "f32_48x48x64_direct_k4"},
+    {80, 80, 64, 1, 1, kGuardNone, "f32_80x80x64_direct_k4"},
+    {96, 96, 64, 1, 1, kGuardNone, "f32_96x96x64_direct_k4"},
+    {48, 96, 64, 1, 1, kGuardNone, "f32_48x96x64_direct_k4"},
+    {96, 48, 64, 1, 1, kGuardNone, "f32_96x48x64_direct_k4"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 static_assert(kNumConfigs == kF32Tiles, "one table entry per F32Tile");
@@ -100,9 +110,7 @@ int plan_f32_tile(const F32TileQuery& q) {
   const bool direct_ok = gemm_f32_direct_offsets_fit(K, q.lda, q.ldb);
   auto fits = [&](int c) {
     const GemmF32Config& g = gemm_f32_config(c);
-    if ((c == kF32Direct128 || c == kF32Direct128Edge || c == kF32Direct64 || c == kF32Direct64K4 ||
-         c == kF32Direct64K4Edge || c == kF32Direct16K4) && !direct_ok)
-      return false;
+    if (c >= kF32Direct128 && !direct_ok) return false;  // the one-wave tiles
     if (c == kF32Direct16K4 && K > 512)
       return false;
     if (g.guard == kGuardNone) return aligned && K > 0 && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
@@ -243,6 +251,42 @@ int plan_f32_tile(const F32TileQuery& q) {
           cd = pick({kF32Direct64K4Edge});
         }
         if (cd >= 0) cfg = cd;
+      }
+      // The R x C one-wave tiles (K split over four waves, one workgroup per
+      // CU) where their tiles fill the CUs more evenly than 64x64 ones. Cost:
+      // the MFMAs of each SIMD, R x C blocks over a quarter of K per round of
+      // workgroups; the 64x64 K-split tile is R = C = 4, the unsplit one 16
+      // blocks over all of K per round of four tiles per CU. In one round
+      // (768^3: 256 tiles of 48x48, 10.5 against 15.3 us; 1536x3072x1536 on
+      // 96x96 114.9 against 141.6 us; 720x768x720 10.5 against 19.0 us on the
+      // 32x32 edge tile); over several rounds only tiles that read no more
+      // per output than 64x64 ones, 1/bm + 1/bn <= 1/32 (2560x1024x2560 on
+      // 80x80 113.3 against 124.8 us, 2304^3 on 48x96 204.4 against 211.7
+      // us, where 48x48 tiles take 234.2 us).
+      if (cfg != kF32Direct128 && cfg != kF32Direct128Edge && K >= 256 && K % 64 == 0 && M % 16 == 0 &&
+          N % 16 == 0 && aligned && direct_ok) {
+        const int64_t t64n = ((M + 63) / 64) * ((N + 63) / 64);
+        const int64_t cus = q.cus;
+        int64_t inc = -1;  // the incumbent's cost where comparable
+        if (cfg == kF32Direct64K4) inc = 16 * ((t64n + cus - 1) / cus);
+        if (cfg == kF32Direct64) inc = 64 * ((t64n + 4 * cus - 1) / (4 * cus));
+        int best_rc = -1;
+        int64_t best_cost = 0, best_rounds = 0;
+        for (int c : {kF32DirectRC2x2, kF32DirectRC3x3, kF32DirectRC5x5, kF32DirectRC6x6, kF32DirectRC3x6,
+                      kF32DirectRC6x3}) {
+          if (!fits(c)) continue;
+          const GemmF32Config& g = gemm_f32_config(c);
+          const int64_t rounds = (tiles_of(c) + cus - 1) / cus;
+          if (rounds > 1 && 32 * (g.bm + g.bn) > g.bm * g.bn) continue;
+          const int64_t cost = (int64_t)(g.bm / 16) * (g.bn / 16) * rounds;
+          if (best_rc < 0 || cost < best_cost || (cost == best_cost && rounds < best_rounds)) {
+            best_rc = c;
+            best_cost = cost;
+            best_rounds = rounds;
+          }
+        }
+        if (best_rc >= 0 && (inc < 0 ? best_rounds == 1 && 2 * tiles_of(best_rc) >= cus : best_cost < inc))
+          cfg = best_rc;
       }
       // Small layers of at most one 16x16 tile per CU, K up to 512: the 16x16
       // one-wave tile with K split over four waves and every load up front

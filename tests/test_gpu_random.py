@@ -106,11 +106,12 @@ def test_random_large_case(seed, torch_cuda):
                 torch_cuda)
 
 
-# Layers of whole 16-, 64- and 128-row tiles on 16-byte aligned views, fp32:
-# the one-wave tiles of gemm_f32_direct.hip (16x16 and 64x64 with K split over
-# four waves, 64x64 unsplit, 128x128), each seed checked against the oracle and
-# the set of seeds required to reach every one of them.
-_ONE_WAVE_MN = [256, 320, 768, 1024, 1088, 1536, 2048, 2560, 4096]
+# Layers of whole 16-, 48-, 64-, 80- and 128-row tiles on 16-byte aligned
+# views, fp32: the one-wave tiles of gemm_f32_direct.hip (16x16, 64x64 and
+# R x C with K split over four waves, 64x64 unsplit, 128x128), each seed
+# checked against the oracle and the set of seeds required to reach every one
+# of them.
+_ONE_WAVE_MN = [256, 320, 720, 768, 1024, 1088, 1440, 1536, 2048, 2560, 4096]
 _ONE_WAVE_K = [64, 256, 448, 512, 1024, 1536]
 
 
@@ -131,12 +132,19 @@ def test_random_one_wave_tiles(torch_cuda):
             M, N, K = 2048, 2048, 512    # 64x64 unsplit
         elif seed == 5002:
             M, N, K = 4096, 4096, 256    # 128x128
+        elif seed == 5003:
+            M, N, K = 768, 768, 768      # 48x48, K split four ways
+        elif seed == 5004:
+            M, N, K = 1200, 1200, 1024   # 80x80
+        elif seed == 5005:
+            M, N, K = 1536, 1536, 512    # 96x96
         pattern = list(_PATTERNS)[int(rng.integers(len(_PATTERNS)))]
         pad, off = ((0, 0), (4, 4), (8, 0))[seed % 3]
         case = (rng, M, K, N, "f32", pattern, True, pad, off, False)
         _check_case(seed, case, torch_cuda)
         plans.append(_native.last_plan())
-    for tile in ("f32_16x16x64_direct_k4", "f32_64x64x64_direct_k4", "f32_64x64x16_direct ", "f32_128x128x16_direct "):
+    for tile in ("f32_16x16x64_direct_k4", "f32_64x64x64_direct_k4", "f32_64x64x16_direct ", "f32_128x128x16_direct ",
+                 "f32_48x48x64_direct_k4", "f32_80x80x64_direct_k4", "f32_96x96x64_direct_k4"):
         assert any(tile in p + " " for p in plans), (tile, plans)
 
 
