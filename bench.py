@@ -57,7 +57,7 @@ PEAK = {  # MI355X published dense peaks
     "int8_mfma_tops": 5000.0,
     "hbm_gbs": 8000.0,
 }
-KERNEL_NAMES = {"c1": "gemm_f32_direct16_kernel", "c2": "gemm_f32_direct64_kernel", "c3": "gemm_f32_direct_kernel",
+KERNEL_NAMES = {"c1": "gemm_f32_direct16_kernel", "c2": "gemm_f32_direct_rc_kernel", "c3": "gemm_f32_direct_kernel",
                 "c4": "gemv_f32_kernel + gemv_reduce_kernel", "c5": "narrow_i8_kernel + gemm_i8_ksplit_kernel",
                 "c3s8": "gemm_f32_direct64_kernel", "c4s8": "gemv_f32_kernel + gemv_reduce_kernel"}
 UNITS = {"c1": "TFLOP/s", "c2": "TFLOP/s", "c3": "TFLOP/s", "c4": "GB/s", "c5": "TOP/s",

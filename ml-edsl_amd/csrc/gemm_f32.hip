@@ -566,6 +566,7 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case kF32DirectRC6x6: return launch_gemm_f32_direct_rc(6, 6, epi, a, stream);
     case kF32DirectRC3x6: return launch_gemm_f32_direct_rc(3, 6, epi, a, stream);
     case kF32DirectRC6x3: return launch_gemm_f32_direct_rc(6, 3, epi, a, stream);
+    case kF32DirectRC4x4: return launch_gemm_f32_direct_rc(4, 4, epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

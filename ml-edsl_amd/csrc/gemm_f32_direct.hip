@@ -841,6 +841,7 @@ hipError_t launch_gemm_f32_direct_rc(int r, int c, int epi, GemmF32Args a, hipSt
   if (r == 6 && c == 6) return launch_rc<6, 6>(epi, a, stream);
   if (r == 3 && c == 6) return launch_rc<3, 6>(epi, a, stream);
   if (r == 6 && c == 3) return launch_rc<6, 3>(epi, a, stream);
+  if (r == 4 && c == 4) return launch_rc<4, 4>(epi, a, stream);
   return hipErrorInvalidValue;
 }
 

@@ -56,7 +56,8 @@ namespace {
 //  kF32DirectRC*: one-wave tiles of R x C 16x16 blocks (32x32, 48x48, 80x80,
 //      96x96, 48x96, 96x48), K split over four waves of a workgroup, for
 //      layers whose 64x64 tiles leave a round of workgroups partly empty
-//      (768^3: 144 tiles of 64x64 or 256 of 48x48, 15.3 against 10.5 us).
+//      (768^3: 144 tiles of 64x64 or 256 of 48x48, 15.3 against 10.5 us),
+//      and the 4x4 instance (64x64) for one round of 64x64 K-split tiles.
 const GemmF32Config kConfigs[] = {
     {64, 64, 16, 2, 2, kGuardAll, "f32_64x64x16_w2x2_guard"},
     {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k4_pf4"},
@@ -80,12 +81,13 @@ const GemmF32Config kConfigs[] = {
     {64, 64, 64, 1, 1, kGuardNone, "f32_64x64x64_direct_k4"},
     {64, 64, 64, 1, 1, kGuardEdge, "f32_64x64x64_direct_k4_edge"},
     {16, 16, 64, 1, 1, kGuardNone, "f32_16x16x64_direct_k4"},
-    {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_direct_k4"},
-    {48, 48, 64, 1, 1, kGuardNone, "f32_48x48x64_direct_k4"},
-    {80, 80, 64, 1, 1, kGuardNone, "f32_80x80x64_direct_k4"},
-    {96, 96, 64, 1, 1, kGuardNone, "f32_96x96x64_direct_k4"},
-    {48, 96, 64, 1, 1, kGuardNone, "f32_48x96x64_direct_k4"},
-    {96, 48, 64, 1, 1, kGuardNone, "f32_96x48x64_direct_k4"},
+    {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_direct_rc"},
+    {48, 48, 64, 1, 1, kGuardNone, "f32_48x48x64_direct_rc"},
+    {80, 80, 64, 1, 1, kGuardNone, "f32_80x80x64_direct_rc"},
+    {96, 96, 64, 1, 1, kGuardNone, "f32_96x96x64_direct_rc"},
+    {48, 96, 64, 1, 1, kGuardNone, "f32_48x96x64_direct_rc"},
+    {96, 48, 64, 1, 1, kGuardNone, "f32_96x48x64_direct_rc"},
+    {64, 64, 64, 1, 1, kGuardNone, "f32_64x64x64_direct_rc"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 static_assert(kNumConfigs == kF32Tiles, "one table entry per F32Tile");
@@ -287,6 +289,12 @@ int plan_f32_tile(const F32TileQuery& q) {
         }
         if (best_rc >= 0 && (inc < 0 ? best_rounds == 1 && 2 * tiles_of(best_rc) >= cus : best_cost < inc))
           cfg = best_rc;
+        else if (cfg == kF32Direct64K4 && t64n <= cus && fits(kF32DirectRC4x4))
+          // One round of K-split 64x64 tiles: the R x C kernel's 4 x 4 instance
+          // (1024^3 20.1-20.3 against 20.6-20.8 us, alternating on one box;
+          // over several rounds neither is ahead: 3072^3 425-447 against
+          // 415-445 us).
+          cfg = kF32DirectRC4x4;
       }
       // Small layers of at most one 16x16 tile per CU, K up to 512: the 16x16
       // one-wave tile with K split over four waves and every load up front

@@ -55,6 +55,7 @@ enum F32Tile : int {
   kF32DirectRC6x6,
   kF32DirectRC3x6,
   kF32DirectRC6x3,
+  kF32DirectRC4x4,      // 64x64x64 on the R x C kernel: one round of K-split 64x64 tiles
   kF32Tiles
 };
 int gemm_f32_num_configs();

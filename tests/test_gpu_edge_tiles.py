@@ -98,16 +98,16 @@ def test_auto_plan_takes_edge_tiles(shape, tile, torch_cuda):
 
 def test_aligned_shapes_keep_their_tiles(torch_cuda):
     """Shapes the tiles divide still take the unguarded configurations."""
-    for (M, K, N), tile in (((1024, 1024, 1024), "f32_64x64x64_direct_k4"),
+    for (M, K, N), tile in (((1024, 1024, 1024), "f32_64x64x64_direct_rc"),
                             ((2048, 2048, 2048), "f32_64x64x16_direct"),
                             ((4096, 1024, 4096), "f32_128x128x16_direct"),
                             ((3072, 512, 3072), "f32_64x64x64_direct_k4"),
                             ((2048, 128, 2048), "f32_128x128x32_mfma16_w8"),
                             ((1024, 128, 1024), "f32_64x64x64_mfma16"),
                             ((256, 256, 256), "f32_16x16x64_direct_k4"),
-                            ((512, 512, 512), "f32_32x32x64_direct_k4"),
-                            ((768, 768, 768), "f32_48x48x64_direct_k4"),
-                            ((1536, 512, 1536), "f32_96x96x64_direct_k4")):
+                            ((512, 512, 512), "f32_32x32x64_direct_rc"),
+                            ((768, 768, 768), "f32_48x48x64_direct_rc"),
+                            ((1536, 512, 1536), "f32_96x96x64_direct_rc")):
         X, W, b = _inputs(M, K, N, 7)
         got, plan = _run(torch_cuda, X, W, b)
         assert f"cfg={tile} " in plan, plan
@@ -486,12 +486,14 @@ MFMA16_SHAPES = {
                                (1024, 320, 64), (64, 448, 1024), (1024, 1024, 1024)],
     # the R x C tiles with K split four ways: one to 32 groups per wave, B in
     # pieces of 64, 32 and 16 columns (3 = 2 + 1, 5 = 4 + 1, 6 = 4 + 2)
-    "f32_32x32x64_direct_k4": [(96, 64, 32), (128, 128, 96), (512, 512, 512), (96, 1024, 64), (160, 2048, 256)],
-    "f32_48x48x64_direct_k4": [(96, 64, 48), (144, 128, 144), (768, 768, 768), (144, 2048, 48), (96, 320, 480)],
-    "f32_80x80x64_direct_k4": [(80, 64, 80), (160, 192, 240), (400, 1024, 160), (1280, 256, 1280)],
-    "f32_96x96x64_direct_k4": [(96, 64, 96), (192, 128, 288), (96, 2048, 192), (1536, 384, 1536)],
-    "f32_48x96x64_direct_k4": [(96, 64, 96), (144, 256, 192), (768, 512, 3072)],
-    "f32_96x48x64_direct_k4": [(96, 64, 48), (192, 256, 96), (3072, 512, 768)],
+    "f32_32x32x64_direct_rc": [(96, 64, 32), (128, 128, 96), (512, 512, 512), (96, 1024, 64), (160, 2048, 256)],
+    "f32_48x48x64_direct_rc": [(96, 64, 48), (144, 128, 144), (768, 768, 768), (144, 2048, 48), (96, 320, 480)],
+    "f32_80x80x64_direct_rc": [(80, 64, 80), (160, 192, 240), (400, 1024, 160), (1280, 256, 1280)],
+    "f32_96x96x64_direct_rc": [(96, 64, 96), (192, 128, 288), (96, 2048, 192), (1536, 384, 1536)],
+    "f32_48x96x64_direct_rc": [(96, 64, 96), (144, 256, 192), (768, 512, 3072)],
+    "f32_96x48x64_direct_rc": [(96, 64, 48), (192, 256, 96), (3072, 512, 768)],
+    "f32_64x64x64_direct_rc": [(64, 64, 64), (128, 128, 64), (64, 192, 192), (192, 2048, 128),
+                               (1024, 320, 64), (1024, 1024, 1024)],
     "f32_128x128x32_mfma16": [(128, 32, 128), (256, 64, 128), (128, 96, 384), (384, 2048, 256),
                               (1024, 160, 128), (128, 224, 1024)],
     "f32_128x128x32_mfma16_w8": [(128, 32, 128), (256, 64, 256), (384, 96, 128), (128, 1056, 384)],
@@ -560,8 +562,8 @@ def test_mfma16_edge_tiles_on_random_shapes(torch_cuda):
 @pytest.mark.parametrize("tile", ["f32_128x128x16_direct_edge", "f32_128x128x16_direct",
                                   "f32_64x64x64_direct_k4_edge",
                                   "f32_64x64x64_direct_k4", "f32_128x128x32_mfma16_edge",
-                                  "f32_48x48x64_direct_k4", "f32_96x96x64_direct_k4",
-                                  "f32_80x80x64_direct_k4", "f32_48x96x64_direct_k4"])
+                                  "f32_48x48x64_direct_rc", "f32_96x96x64_direct_rc",
+                                  "f32_80x80x64_direct_rc", "f32_48x96x64_direct_rc"])
 def test_values_past_the_operands_never_reach_the_output(tile, torch_cuda):
     """Edge tiles read past K, N and M only in ways whose values are zeroed or
     never stored: with NaN and Inf in every padding element of A and B (the

@@ -100,7 +100,7 @@ def test_small_m_weights_beyond_2_31(torch_cuda):
 # (K + 16) * ldb * 4 + 1024 fit in 2^31 - 1 (gemm_f32_direct_offsets_fit).
 ONE_WAVE_TILES = ["f32_128x128x16_direct", "f32_128x128x16_direct_edge", "f32_64x64x16_direct",
                   "f32_64x64x64_direct_k4", "f32_64x64x64_direct_k4_edge", "f32_16x16x64_direct_k4",
-                  "f32_32x32x64_direct_k4"]
+                  "f32_32x32x64_direct_rc"]
 LDA_LIMIT = (2**31 - 1 - 64) // 512 // 4 * 4          # 4,194,300 elements
 LDB_LIMIT_K256 = (2**31 - 1 - 1024) // (272 * 4) // 4 * 4  # 1,973,788 elements at K = 256
 

@@ -144,7 +144,7 @@ def test_random_one_wave_tiles(torch_cuda):
         _check_case(seed, case, torch_cuda)
         plans.append(_native.last_plan())
     for tile in ("f32_16x16x64_direct_k4", "f32_64x64x64_direct_k4", "f32_64x64x16_direct ", "f32_128x128x16_direct ",
-                 "f32_48x48x64_direct_k4", "f32_80x80x64_direct_k4", "f32_96x96x64_direct_k4"):
+                 "f32_48x48x64_direct_rc", "f32_80x80x64_direct_rc", "f32_96x96x64_direct_rc"):
         assert any(tile in p + " " for p in plans), (tile, plans)
 
 

@@ -42,7 +42,7 @@ def table(driver):
 PINNED = [
     # BASELINE layers that take the tiles (C4 takes the small-M kernel)
     ((256, 256, 256), True, "f32_16x16x64_direct_k4"),             # C1
-    ((1024, 1024, 1024), True, "f32_64x64x64_direct_k4"),          # C2
+    ((1024, 1024, 1024), True, "f32_64x64x64_direct_rc"),          # C2
     ((4096, 4096, 4096), True, "f32_128x128x16_direct"),           # C3
     ((2048, 2048, 2048), True, "f32_64x64x16_direct"),
     ((4096, 4096, 512), True, "f32_64x64x64_direct_k4"),           # C3 column shard (N = 512)
@@ -71,16 +71,16 @@ PINNED = [
     ((2048, 128, 2048), True, "f32_128x128x32_mfma16_w8"),
     ((1024, 128, 1024), True, "f32_64x64x64_mfma16"),
     # R x C one-wave tiles, K split four ways: one round of workgroups ...
-    ((512, 512, 512), True, "f32_32x32x64_direct_k4"),
-    ((768, 768, 768), True, "f32_48x48x64_direct_k4"),
-    ((720, 768, 720), True, "f32_48x48x64_direct_k4"),
-    ((1200, 1024, 1200), True, "f32_80x80x64_direct_k4"),
-    ((1536, 512, 1536), True, "f32_96x96x64_direct_k4"),
-    ((1536, 1024, 720), True, "f32_96x48x64_direct_k4"),
-    ((720, 1024, 1536), True, "f32_48x96x64_direct_k4"),
+    ((512, 512, 512), True, "f32_32x32x64_direct_rc"),
+    ((768, 768, 768), True, "f32_48x48x64_direct_rc"),
+    ((720, 768, 720), True, "f32_48x48x64_direct_rc"),
+    ((1200, 1024, 1200), True, "f32_80x80x64_direct_rc"),
+    ((1536, 512, 1536), True, "f32_96x96x64_direct_rc"),
+    ((1536, 1024, 720), True, "f32_96x48x64_direct_rc"),
+    ((720, 1024, 1536), True, "f32_48x96x64_direct_rc"),
     # ... or several, with tiles that read no more per output than 64x64
-    ((2304, 2304, 2304), True, "f32_48x96x64_direct_k4"),
-    ((2560, 1024, 2560), True, "f32_80x80x64_direct_k4"),
+    ((2304, 2304, 2304), True, "f32_48x96x64_direct_rc"),
+    ((2560, 1024, 2560), True, "f32_80x80x64_direct_rc"),
     # too few tiles for half the CUs, and even cost against 64x64
     ((256, 1024, 256), True, "f32_32x32x64_w1x1_k4_pf4"),
     ((3072, 3072, 3072), True, "f32_64x64x64_direct_k4"),
@@ -98,7 +98,7 @@ def test_table_is_named_and_every_tile_is_planned(driver):
     layer: the table holds no configuration the planner cannot reach."""
     rows = table(driver)
     names = [r[1] for r in rows]
-    assert len(names) == len(set(names)) == 28
+    assert len(names) == len(set(names)) == 29
     dims = [1, 4, 17, 64, 65, 100, 128, 256, 257, 500, 512, 720, 768, 1000, 1024, 1025, 1536, 2000, 2048, 2304,
             3000, 4096, 4097, 6000, 6144]
     queries = [(M, N, K, al, CUS) for M in dims for N in dims for K in dims + [0] for al in (0, 1)]
@@ -130,7 +130,7 @@ def test_one_wave_tiles_need_32_bit_buffer_offsets(driver):
                              text=True, check=True).stdout
         return out.split()[0]
     assert plan(4096, 4096, 4096, 4096, 4096) == "f32_128x128x16_direct"
-    assert plan(1024, 1024, 1024, 1024, 1024) == "f32_64x64x64_direct_k4"
+    assert plan(1024, 1024, 1024, 1024, 1024) == "f32_64x64x64_direct_rc"
     # K rows of B past 2^31 bytes: 4096 rows of 2^17 floats = 2 GiB
     big_ldb = 1 << 17
     assert "direct" not in plan(4096, 4096, 4096, 4096, big_ldb)
