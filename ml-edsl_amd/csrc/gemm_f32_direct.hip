@@ -525,9 +525,9 @@ hipError_t launch_direct16(int epi, const GemmF32Args& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// The R x C tile (16R x 16C outputs, K split over the four waves of a
-// workgroup) for layers whose 64x64 tiles do not fill whole rounds of the
-// CUs: 768^3 is 256 tiles of 48x48 (R = C = 3) and 1536^3 256 tiles of 96x96
+// The R x C tile (16R x 16C outputs, K -- a multiple of 16, at least 64 --
+// split over the four waves of a workgroup) for layers whose 64x64 tiles do
+// not fill whole rounds of the CUs: 768^3 is 256 tiles of 48x48 (R = C = 3) and 1536^3 256 tiles of 96x96
 // (R = C = 6), one workgroup per CU and one wave per SIMD, so every SIMD runs
 // the same number of MFMAs in one round. Each wave computes the whole tile
 // over a quarter of K with the 64x64 tile's A fragments and its loop (loads
@@ -588,8 +588,11 @@ gemm_f32_direct_rc_kernel(GemmF32Args args) {
   tile_coords(blockIdx.x, args.tiles_m, args.tiles_n, tm, tn);
   const int m0 = __builtin_amdgcn_readfirstlane(tm * 16 * R);
   const int n0 = __builtin_amdgcn_readfirstlane(tn * 16 * C);
-  const int ngw = args.K / 16 / KS;  // groups per wave: K is a multiple of 64
-  const int jb = wave * ngw;
+  // The wave's groups jb .. jb + ngw - 1: K / 16 groups (K a multiple of 16,
+  // at least 64) shared as evenly as they go, at least one per wave.
+  const int ng = args.K / 16;
+  const int jb = wave * ng / KS;
+  const int ngw = (wave + 1) * ng / KS - jb;
   const int lda = (int)args.lda, ldb = (int)args.ldb;
   const i32x4 rsrc_a = buffer_rsrc(args.A + (int64_t)m0 * lda, (int64_t)(args.M - m0) * lda * 4);
   const i32x4 rsrc_b = buffer_rsrc(args.B + n0, (int64_t)args.K * ldb * 4 - (int64_t)n0 * 4);
@@ -833,7 +836,7 @@ hipError_t launch_gemm_f32_direct16(int epi, GemmF32Args a, hipStream_t stream) 
 
 hipError_t launch_gemm_f32_direct_rc(int r, int c, int epi, GemmF32Args a, hipStream_t stream) {
   if (!direct_operands_ok(epi, a)) return hipErrorInvalidValue;
-  if (r < 1 || c < 1 || a.M % (16 * r) || a.N % (16 * c) || a.K % 64) return hipErrorInvalidValue;
+  if (r < 1 || c < 1 || a.M % (16 * r) || a.N % (16 * c) || a.K % 16 || a.K < 64) return hipErrorInvalidValue;
   if (a.tiles_m != a.M / (16 * r) || a.tiles_n != a.N / (16 * c)) return hipErrorInvalidValue;
   if (r == 2 && c == 2) return launch_rc<2, 2>(epi, a, stream);
   if (r == 3 && c == 3) return launch_rc<3, 3>(epi, a, stream);

@@ -115,6 +115,8 @@ int plan_f32_tile(const F32TileQuery& q) {
     if (c >= kF32Direct128 && !direct_ok) return false;  // the one-wave tiles
     if (c == kF32Direct16K4 && K > 512)
       return false;
+    if (c >= kF32DirectRC2x2)  // the R x C tiles split K / 16 groups over four waves
+      return aligned && M % g.bm == 0 && N % g.bn == 0 && K % 16 == 0 && K >= 64;
     if (g.guard == kGuardNone) return aligned && K > 0 && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
     if (g.guard == kGuardEdge) return edge_ok;
     return K > 0;  // kGuardScalar, kGuardAll: any shape, stride and alignment
@@ -265,7 +267,7 @@ int plan_f32_tile(const F32TileQuery& q) {
       // per output than 64x64 ones, 1/bm + 1/bn <= 1/32 (2560x1024x2560 on
       // 80x80 113.3 against 124.8 us, 2304^3 on 48x96 204.4 against 211.7
       // us, where 48x48 tiles take 234.2 us).
-      if (cfg != kF32Direct128 && cfg != kF32Direct128Edge && K >= 256 && K % 64 == 0 && M % 16 == 0 &&
+      if (cfg != kF32Direct128 && cfg != kF32Direct128Edge && K >= 256 && K % 16 == 0 && M % 16 == 0 &&
           N % 16 == 0 && aligned && direct_ok) {
         const int64_t t64n = ((M + 63) / 64) * ((N + 63) / 64);
         const int64_t cus = q.cus;
@@ -274,8 +276,8 @@ int plan_f32_tile(const F32TileQuery& q) {
         if (cfg == kF32Direct64) inc = 64 * ((t64n + 4 * cus - 1) / (4 * cus));
         int best_rc = -1;
         int64_t best_cost = 0, best_rounds = 0;
-        for (int c : {kF32DirectRC2x2, kF32DirectRC3x3, kF32DirectRC5x5, kF32DirectRC6x6, kF32DirectRC3x6,
-                      kF32DirectRC6x3}) {
+        for (int c : {kF32DirectRC2x2, kF32DirectRC3x3, kF32DirectRC4x4, kF32DirectRC5x5, kF32DirectRC6x6,
+                      kF32DirectRC3x6, kF32DirectRC6x3}) {
           if (!fits(c)) continue;
           const GemmF32Config& g = gemm_f32_config(c);
           const int64_t rounds = (tiles_of(c) + cus - 1) / cus;

@@ -49,7 +49,7 @@ enum F32Tile : int {
   kF32Direct64K4,       // 64x64x64, four waves splitting K, partials summed through LDS
   kF32Direct64K4Edge,
   kF32Direct16K4,       // 16x16x64, four waves splitting K, every load up front (small layers)
-  kF32DirectRC2x2,      // 16R x 16C x 64, four waves splitting K (R x C MFMA blocks per wave)
+  kF32DirectRC2x2,      // 16R x 16C, four waves splitting K (K % 16 == 0, K >= 64; R x C blocks per wave)
   kF32DirectRC3x3,
   kF32DirectRC5x5,
   kF32DirectRC6x6,

@@ -484,12 +484,15 @@ MFMA16_SHAPES = {
     "f32_16x16x64_direct_k4": [(80, 64, 48), (256, 256, 256), (96, 512, 160), (1024, 128, 32), (128, 448, 16)],
     "f32_64x64x64_direct_k4": [(64, 64, 64), (128, 128, 64), (64, 192, 192), (192, 2048, 128),
                                (1024, 320, 64), (64, 448, 1024), (1024, 1024, 1024)],
-    # the R x C tiles with K split four ways: one to 32 groups per wave, B in
-    # pieces of 64, 32 and 16 columns (3 = 2 + 1, 5 = 4 + 1, 6 = 4 + 2)
-    "f32_32x32x64_direct_rc": [(96, 64, 32), (128, 128, 96), (512, 512, 512), (96, 1024, 64), (160, 2048, 256)],
-    "f32_48x48x64_direct_rc": [(96, 64, 48), (144, 128, 144), (768, 768, 768), (144, 2048, 48), (96, 320, 480)],
+    # the R x C tiles with K split four ways: one to 32 groups per wave (K / 16
+    # groups shared as evenly as they go), B in pieces of 64, 32 and 16
+    # columns (3 = 2 + 1, 5 = 4 + 1, 6 = 4 + 2)
+    "f32_32x32x64_direct_rc": [(96, 64, 32), (128, 128, 96), (512, 512, 512), (96, 1024, 64), (160, 2048, 256),
+                               (96, 80, 64), (128, 208, 96)],
+    "f32_48x48x64_direct_rc": [(96, 64, 48), (144, 128, 144), (768, 768, 768), (144, 2048, 48), (96, 320, 480),
+                               (144, 112, 96), (768, 784, 768)],
     "f32_80x80x64_direct_rc": [(80, 64, 80), (160, 192, 240), (400, 1024, 160), (1280, 256, 1280)],
-    "f32_96x96x64_direct_rc": [(96, 64, 96), (192, 128, 288), (96, 2048, 192), (1536, 384, 1536)],
+    "f32_96x96x64_direct_rc": [(96, 64, 96), (192, 128, 288), (96, 2048, 192), (1536, 384, 1536), (192, 1040, 96)],
     "f32_48x96x64_direct_rc": [(96, 64, 96), (144, 256, 192), (768, 512, 3072)],
     "f32_96x48x64_direct_rc": [(96, 64, 48), (192, 256, 96), (3072, 512, 768)],
     "f32_64x64x64_direct_rc": [(64, 64, 64), (128, 128, 64), (64, 192, 192), (192, 2048, 128),

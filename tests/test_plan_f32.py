@@ -74,6 +74,7 @@ PINNED = [
     ((512, 512, 512), True, "f32_32x32x64_direct_rc"),
     ((768, 768, 768), True, "f32_48x48x64_direct_rc"),
     ((720, 768, 720), True, "f32_48x48x64_direct_rc"),
+    ((768, 784, 768), True, "f32_48x48x64_direct_rc"),      # K a multiple of 16, not of 64
     ((1200, 1024, 1200), True, "f32_80x80x64_direct_rc"),
     ((1536, 512, 1536), True, "f32_96x96x64_direct_rc"),
     ((1536, 1024, 720), True, "f32_96x48x64_direct_rc"),
