@@ -560,13 +560,18 @@ hipError_t launch_gemm_f32(int cfg, int epi, GemmF32Args a, hipStream_t stream) 
     case kF32Direct64K4: return launch_gemm_f32_direct64(4, kGuardNone, epi, a, stream);
     case kF32Direct64K4Edge: return launch_gemm_f32_direct64(4, kGuardEdge, epi, a, stream);
     case kF32Direct16K4: return launch_gemm_f32_direct16(epi, a, stream);
-    case kF32DirectRC2x2: return launch_gemm_f32_direct_rc(2, 2, epi, a, stream);
-    case kF32DirectRC3x3: return launch_gemm_f32_direct_rc(3, 3, epi, a, stream);
-    case kF32DirectRC5x5: return launch_gemm_f32_direct_rc(5, 5, epi, a, stream);
-    case kF32DirectRC6x6: return launch_gemm_f32_direct_rc(6, 6, epi, a, stream);
-    case kF32DirectRC3x6: return launch_gemm_f32_direct_rc(3, 6, epi, a, stream);
-    case kF32DirectRC6x3: return launch_gemm_f32_direct_rc(6, 3, epi, a, stream);
-    case kF32DirectRC4x4: return launch_gemm_f32_direct_rc(4, 4, epi, a, stream);
+    case kF32DirectRC2x2: return launch_gemm_f32_direct_rc(2, 2, kGuardNone, epi, a, stream);
+    case kF32DirectRC3x3: return launch_gemm_f32_direct_rc(3, 3, kGuardNone, epi, a, stream);
+    case kF32DirectRC5x5: return launch_gemm_f32_direct_rc(5, 5, kGuardNone, epi, a, stream);
+    case kF32DirectRC6x6: return launch_gemm_f32_direct_rc(6, 6, kGuardNone, epi, a, stream);
+    case kF32DirectRC3x6: return launch_gemm_f32_direct_rc(3, 6, kGuardNone, epi, a, stream);
+    case kF32DirectRC6x3: return launch_gemm_f32_direct_rc(6, 3, kGuardNone, epi, a, stream);
+    case kF32DirectRC4x4: return launch_gemm_f32_direct_rc(4, 4, kGuardNone, epi, a, stream);
+    case kF32DirectRC2x2Edge: return launch_gemm_f32_direct_rc(2, 2, kGuardEdge, epi, a, stream);
+    case kF32DirectRC3x3Edge: return launch_gemm_f32_direct_rc(3, 3, kGuardEdge, epi, a, stream);
+    case kF32DirectRC4x4Edge: return launch_gemm_f32_direct_rc(4, 4, kGuardEdge, epi, a, stream);
+    case kF32DirectRC5x5Edge: return launch_gemm_f32_direct_rc(5, 5, kGuardEdge, epi, a, stream);
+    case kF32DirectRC6x6Edge: return launch_gemm_f32_direct_rc(6, 6, kGuardEdge, epi, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

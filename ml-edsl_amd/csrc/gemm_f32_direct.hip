@@ -573,7 +573,7 @@ struct VecOf<2> { using T = f32x2; };
 template <>
 struct VecOf<1> { using T = float; };
 
-template <int R, int C, int EPI>
+template <int R, int C, bool kEdge, int EPI>
 __global__ void __launch_bounds__(256)
 gemm_f32_direct_rc_kernel(GemmF32Args args) {
   using P = ColPieces<C>;
@@ -589,33 +589,61 @@ gemm_f32_direct_rc_kernel(GemmF32Args args) {
   const int m0 = __builtin_amdgcn_readfirstlane(tm * 16 * R);
   const int n0 = __builtin_amdgcn_readfirstlane(tn * 16 * C);
   // The wave's groups jb .. jb + ngw - 1: K / 16 groups (K a multiple of 16,
-  // at least 64) shared as evenly as they go, at least one per wave.
-  const int ng = args.K / 16;
+  // at least 64) shared as evenly as they go, at least one per wave; edge
+  // tiles: ceil(K / 16) groups, the last one partial, and a wave whose share
+  // of a short K is empty skips the loop.
+  const int K = args.K;
+  const int ng = kEdge ? (K + 15) / 16 : K / 16;
   const int jb = wave * ng / KS;
   const int ngw = (wave + 1) * ng / KS - jb;
   const int lda = (int)args.lda, ldb = (int)args.ldb;
   const i32x4 rsrc_a = buffer_rsrc(args.A + (int64_t)m0 * lda, (int64_t)(args.M - m0) * lda * 4);
-  const i32x4 rsrc_b = buffer_rsrc(args.B + n0, (int64_t)args.K * ldb * 4 - (int64_t)n0 * 4);
+  const i32x4 rsrc_b = buffer_rsrc(args.B + n0, (int64_t)K * ldb * 4 - (int64_t)n0 * 4);
   const int va = (r16 * lda + 4 * g) * 4;  // A[m0 + 16i + r16][16j + 4g .. +3]
   int vb[P::count];                        // B[16j + 4g + s][piece columns of the lane]
+  // Edge tiles, as for the 128x128 tile: per-lane row-block offsets (rows
+  // past M out of range, and so are A chunks past K), each piece's columns
+  // clamped to N - w (their outputs are never stored); the k row of B is in
+  // the per-lane offset, so B rows past K read zero.
+  int va_i[kEdge ? R : 1];
   static_for<P::count>([&](auto pc) __attribute__((always_inline)) {
     constexpr int p = decltype(pc)::value;
-    vb[p] = (4 * g * ldb + 16 * P::first(p) + P::width(p) * r16) * 4;
+    constexpr int W = P::width(p);
+    const int col = kEdge ? min(n0 + 16 * P::first(p) + W * r16, args.N - W) : n0 + 16 * P::first(p) + W * r16;
+    vb[p] = (4 * g * ldb + col - n0) * 4;
   });
+  if constexpr (kEdge) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) va_i[i] = va + i * 64 * lda;
+  }
 
   struct Frag {
     f32x4 a[R];      // row block i: A[m0 + 16i + r16][16j + 4g .. +3]
     float b[4][C];   // k slot s, column block c
   };
   auto load = [&](Frag& f, int j) __attribute__((always_inline)) {
+    if constexpr (!kEdge) {
 #pragma unroll
-    for (int i = 0; i < R; ++i) f.a[i] = raw_buffer_load_f32x4(rsrc_a, va, 64 * j + i * 64 * lda, 0);
+      for (int i = 0; i < R; ++i) f.a[i] = raw_buffer_load_f32x4(rsrc_a, va, 64 * j + i * 64 * lda, 0);
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      static_for<P::count>([&](auto pc) __attribute__((always_inline)) {
-        constexpr int p = decltype(pc)::value;
-        load_piece<P::width(p)>(&f.b[s][P::first(p)], rsrc_b, vb[p], (16 * j + s) * ldb * 4);
-      });
+      for (int s = 0; s < 4; ++s)
+        static_for<P::count>([&](auto pc) __attribute__((always_inline)) {
+          constexpr int p = decltype(pc)::value;
+          load_piece<P::width(p)>(&f.b[s][P::first(p)], rsrc_b, vb[p], (16 * j + s) * ldb * 4);
+        });
+    } else {
+      const bool k_in = 16 * j + 4 * g < K;
+#pragma unroll
+      for (int i = 0; i < R; ++i)
+        f.a[i] = raw_buffer_load_f32x4(rsrc_a, k_in ? va_i[i] : kOutOfRange, 64 * j, 0);
+      const int rowj = 16 * j * ldb * 4;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        static_for<P::count>([&](auto pc) __attribute__((always_inline)) {
+          constexpr int p = decltype(pc)::value;
+          load_piece<P::width(p)>(&f.b[s][P::first(p)], rsrc_b, vb[p] + rowj, s * ldb * 4);
+        });
+    }
   };
   // The bias values of the lane's columns, loaded before the first group.
   float biasv[C];
@@ -624,9 +652,9 @@ gemm_f32_direct_rc_kernel(GemmF32Args args) {
     constexpr int W = P::width(p);
 #pragma unroll
     for (int c = 0; c < W; ++c) biasv[P::first(p) + c] = 0.0f;
-    if constexpr (epi_has_bias(EPI)) {
-      const typename VecOf<W>::T v =
-          *reinterpret_cast<const typename VecOf<W>::T*>(args.bias + n0 + 16 * P::first(p) + W * r16);
+    const int col = n0 + 16 * P::first(p) + W * r16;
+    if (epi_has_bias(EPI) && (!kEdge || col < args.N)) {
+      const typename VecOf<W>::T v = *reinterpret_cast<const typename VecOf<W>::T*>(args.bias + col);
       if constexpr (W == 1) {
         biasv[P::first(p)] = v;
       } else {
@@ -662,7 +690,7 @@ gemm_f32_direct_rc_kernel(GemmF32Args args) {
   // Group jb + t is computed from set t % 3 while groups jb + t + 1 and
   // jb + t + 2 are in flight; loads past the wave's last group repeat it.
   const int jl = jb + ngw - 1;
-  {
+  if (!kEdge || ngw > 0) {
     Frag fr[kSets64];
     load(fr[0], jb);
     load(fr[1], min(jb + 1, jl));
@@ -733,19 +761,20 @@ gemm_f32_direct_rc_kernel(GemmF32Args args) {
 #pragma unroll
         for (int c = 0; c < W; ++c) out[c] = apply_epilogue_f32<EPI>(sum[c], biasv[c0 + c], alpha);
       }
-      __builtin_nontemporal_store(
-          out, reinterpret_cast<V*>(args.C + (int64_t)row * args.ldc + n0 + 16 * c0 + W * r16));
+      const int col = n0 + 16 * c0 + W * r16;
+      if (!kEdge || (row < args.M && col < args.N))
+        __builtin_nontemporal_store(out, reinterpret_cast<V*>(args.C + (int64_t)row * args.ldc + col));
     });
   }
 }
 
-template <int R, int C>
+template <int R, int C, bool kEdge = false>
 hipError_t launch_rc(int epi, const GemmF32Args& a, hipStream_t stream) {
   const dim3 grid(a.tiles_m * a.tiles_n);
   const dim3 block(256);
-#define EDSL_DIRECT_RC_CASE(E)                                                             \
-  case E:                                                                                  \
-    hipLaunchKernelGGL((gemm_f32_direct_rc_kernel<R, C, E>), grid, block, 0, stream, a);  \
+#define EDSL_DIRECT_RC_CASE(E)                                                                    \
+  case E:                                                                                         \
+    hipLaunchKernelGGL((gemm_f32_direct_rc_kernel<R, C, kEdge, E>), grid, block, 0, stream, a);  \
     break;
   switch (epi) {
     EDSL_DIRECT_RC_CASE(epi_code(false, ACT_NONE))
@@ -834,10 +863,19 @@ hipError_t launch_gemm_f32_direct16(int epi, GemmF32Args a, hipStream_t stream) 
   return launch_direct16(epi, a, stream);
 }
 
-hipError_t launch_gemm_f32_direct_rc(int r, int c, int epi, GemmF32Args a, hipStream_t stream) {
+hipError_t launch_gemm_f32_direct_rc(int r, int c, int guard, int epi, GemmF32Args a, hipStream_t stream) {
   if (!direct_operands_ok(epi, a)) return hipErrorInvalidValue;
-  if (r < 1 || c < 1 || a.M % (16 * r) || a.N % (16 * c) || a.K % 16 || a.K < 64) return hipErrorInvalidValue;
-  if (a.tiles_m != a.M / (16 * r) || a.tiles_n != a.N / (16 * c)) return hipErrorInvalidValue;
+  if (r < 1 || c < 1) return hipErrorInvalidValue;
+  if (a.tiles_m != (a.M + 16 * r - 1) / (16 * r) || a.tiles_n != (a.N + 16 * c - 1) / (16 * c)) return hipErrorInvalidValue;
+  if (guard == kGuardEdge) {  // any M; N and K multiples of 4 (direct_operands_ok)
+    if (r == 2 && c == 2) return launch_rc<2, 2, true>(epi, a, stream);
+    if (r == 3 && c == 3) return launch_rc<3, 3, true>(epi, a, stream);
+    if (r == 4 && c == 4) return launch_rc<4, 4, true>(epi, a, stream);
+    if (r == 5 && c == 5) return launch_rc<5, 5, true>(epi, a, stream);
+    if (r == 6 && c == 6) return launch_rc<6, 6, true>(epi, a, stream);
+    return hipErrorInvalidValue;
+  }
+  if (guard != kGuardNone || a.M % (16 * r) || a.N % (16 * c) || a.K % 16 || a.K < 64) return hipErrorInvalidValue;
   if (r == 2 && c == 2) return launch_rc<2, 2>(epi, a, stream);
   if (r == 3 && c == 3) return launch_rc<3, 3>(epi, a, stream);
   if (r == 5 && c == 5) return launch_rc<5, 5>(epi, a, stream);

@@ -44,10 +44,11 @@ hipError_t launch_gemm_f32_direct64(int ksplit, int guard, int epi, GemmF32Args 
 // The 16x16 tile for small layers: K split over four waves, every fragment
 // loaded up front; M and N multiples of 16, K a multiple of 64 up to 512.
 hipError_t launch_gemm_f32_direct16(int epi, GemmF32Args args, hipStream_t stream);
-// The (16r x 16c) tile, r x c MFMA blocks per wave, K split over four waves
-// (r x c one of 2x2, 3x3, 4x4, 5x5, 6x6, 3x6, 6x3); M a multiple of 16r, N of
-// 16c, K of 16 and at least 64.
-hipError_t launch_gemm_f32_direct_rc(int r, int c, int epi, GemmF32Args args, hipStream_t stream);
+// The (16r x 16c) tile, r x c MFMA blocks per wave, K split over four waves,
+// the same operand conditions. guard kGuardNone (r x c one of 2x2, 3x3, 4x4,
+// 5x5, 6x6, 3x6, 6x3): M a multiple of 16r, N of 16c, K of 16 and at least
+// 64; kGuardEdge (2x2 to 6x6): any such M, N, K.
+hipError_t launch_gemm_f32_direct_rc(int r, int c, int guard, int epi, GemmF32Args args, hipStream_t stream);
 
 // ------------------------------------------------------------ fp32 small-M
 struct GemvF32Args {

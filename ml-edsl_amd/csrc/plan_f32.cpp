@@ -88,6 +88,11 @@ const GemmF32Config kConfigs[] = {
     {48, 96, 64, 1, 1, kGuardNone, "f32_48x96x64_direct_rc"},
     {96, 48, 64, 1, 1, kGuardNone, "f32_96x48x64_direct_rc"},
     {64, 64, 64, 1, 1, kGuardNone, "f32_64x64x64_direct_rc"},
+    {32, 32, 64, 1, 1, kGuardEdge, "f32_32x32x64_direct_rc_edge"},
+    {48, 48, 64, 1, 1, kGuardEdge, "f32_48x48x64_direct_rc_edge"},
+    {64, 64, 64, 1, 1, kGuardEdge, "f32_64x64x64_direct_rc_edge"},
+    {80, 80, 64, 1, 1, kGuardEdge, "f32_80x80x64_direct_rc_edge"},
+    {96, 96, 64, 1, 1, kGuardEdge, "f32_96x96x64_direct_rc_edge"},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 static_assert(kNumConfigs == kF32Tiles, "one table entry per F32Tile");
@@ -115,8 +120,10 @@ int plan_f32_tile(const F32TileQuery& q) {
     if (c >= kF32Direct128 && !direct_ok) return false;  // the one-wave tiles
     if (c == kF32Direct16K4 && K > 512)
       return false;
-    if (c >= kF32DirectRC2x2)  // the R x C tiles split K / 16 groups over four waves
+    if (c >= kF32DirectRC2x2) {  // the R x C tiles split K / 16 groups over four waves
+      if (g.guard == kGuardEdge) return edge_ok;
       return aligned && M % g.bm == 0 && N % g.bn == 0 && K % 16 == 0 && K >= 64;
+    }
     if (g.guard == kGuardNone) return aligned && K > 0 && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
     if (g.guard == kGuardEdge) return edge_ok;
     return K > 0;  // kGuardScalar, kGuardAll: any shape, stride and alignment
@@ -267,18 +274,23 @@ int plan_f32_tile(const F32TileQuery& q) {
       // per output than 64x64 ones, 1/bm + 1/bn <= 1/32 (2560x1024x2560 on
       // 80x80 113.3 against 124.8 us, 2304^3 on 48x96 204.4 against 211.7
       // us, where 48x48 tiles take 234.2 us).
-      if (cfg != kF32Direct128 && cfg != kF32Direct128Edge && K >= 256 && K % 16 == 0 && M % 16 == 0 &&
-          N % 16 == 0 && aligned && direct_ok) {
+      if (cfg != kF32Direct128 && cfg != kF32Direct128Edge && K >= 256 && edge_ok && direct_ok) {
         const int64_t t64n = ((M + 63) / 64) * ((N + 63) / 64);
         const int64_t cus = q.cus;
         int64_t inc = -1;  // the incumbent's cost where comparable
-        if (cfg == kF32Direct64K4) inc = 16 * ((t64n + cus - 1) / cus);
+        if (cfg == kF32Direct64K4 || cfg == kF32Direct64K4Edge) inc = 16 * ((t64n + cus - 1) / cus);
         if (cfg == kF32Direct64) inc = 64 * ((t64n + 4 * cus - 1) / (4 * cus));
         int best_rc = -1;
         int64_t best_cost = 0, best_rounds = 0;
-        for (int c : {kF32DirectRC2x2, kF32DirectRC3x3, kF32DirectRC4x4, kF32DirectRC5x5, kF32DirectRC6x6,
-                      kF32DirectRC3x6, kF32DirectRC6x3}) {
-          if (!fits(c)) continue;
+        for (int c0 : {kF32DirectRC2x2, kF32DirectRC3x3, kF32DirectRC4x4, kF32DirectRC5x5, kF32DirectRC6x6,
+                       kF32DirectRC3x6, kF32DirectRC6x3}) {
+          const int edge_twin = c0 == kF32DirectRC2x2 ? kF32DirectRC2x2Edge
+                                : c0 == kF32DirectRC3x3 ? kF32DirectRC3x3Edge
+                                : c0 == kF32DirectRC4x4 ? kF32DirectRC4x4Edge
+                                : c0 == kF32DirectRC5x5 ? kF32DirectRC5x5Edge
+                                : c0 == kF32DirectRC6x6 ? kF32DirectRC6x6Edge : -1;
+          const int c = fits(c0) ? c0 : edge_twin >= 0 && fits(edge_twin) ? edge_twin : -1;
+          if (c < 0) continue;
           const GemmF32Config& g = gemm_f32_config(c);
           const int64_t rounds = (tiles_of(c) + cus - 1) / cus;
           if (rounds > 1 && 32 * (g.bm + g.bn) > g.bm * g.bn) continue;
@@ -295,7 +307,8 @@ int plan_f32_tile(const F32TileQuery& q) {
           // One round of K-split 64x64 tiles: the R x C kernel's 4 x 4 instance
           // (1024^3 20.1-20.3 against 20.6-20.8 us, alternating on one box;
           // over several rounds neither is ahead: 3072^3 425-447 against
-          // 415-445 us).
+          // 415-445 us). Its edge twin measured no better than the 64x64
+          // K-split edge twin at 1000^3 (21.5-22.6 against 22.0 us).
           cfg = kF32DirectRC4x4;
       }
       // Small layers of at most one 16x16 tile per CU, K up to 512: the 16x16

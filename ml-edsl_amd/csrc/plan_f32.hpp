@@ -56,6 +56,11 @@ enum F32Tile : int {
   kF32DirectRC3x6,
   kF32DirectRC6x3,
   kF32DirectRC4x4,      // 64x64x64 on the R x C kernel: one round of K-split 64x64 tiles
+  kF32DirectRC2x2Edge,  // edge twins of the square R x C tiles
+  kF32DirectRC3x3Edge,
+  kF32DirectRC4x4Edge,
+  kF32DirectRC5x5Edge,
+  kF32DirectRC6x6Edge,
   kF32Tiles
 };
 int gemm_f32_num_configs();

@@ -86,7 +86,7 @@ def test_every_edge_config_on_odd_shapes(torch_cuda):
     # 33 x 32 tiles of 128x128 would give 32 CUs a fifth tile
     ((4097, 256, 4096), "f32_64x64x64_mfma16_edge"),
     # K = 1000 leaves a partial last K step on every tile
-    ((512, 1000, 512), "f32_32x32x64_w1x1_k4_pf4_edge"),
+    ((512, 1000, 512), "f32_32x32x64_direct_rc_edge"),
 ], ids=["1000^3", "4000x256x4000", "4097x256x4096", "512x1000x512"])
 def test_auto_plan_takes_edge_tiles(shape, tile, torch_cuda):
     M, K, N = shape
@@ -543,7 +543,8 @@ def test_mfma16_edge_tiles_on_random_shapes(torch_cuda):
     torch = torch_cuda
     names = _native.f32_config_names()
     forced = [names.index("f32_128x128x32_mfma16_edge"), names.index("f32_64x64x64_mfma16_edge"),
-              names.index("f32_128x128x16_direct_edge"), names.index("f32_64x64x64_direct_k4_edge")]
+              names.index("f32_128x128x16_direct_edge"), names.index("f32_64x64x64_direct_k4_edge"),
+              names.index("f32_48x48x64_direct_rc_edge"), names.index("f32_96x96x64_direct_rc_edge")]
     rng = np.random.default_rng(77)
     try:
         for case in range(12):
@@ -566,7 +567,8 @@ def test_mfma16_edge_tiles_on_random_shapes(torch_cuda):
                                   "f32_64x64x64_direct_k4_edge",
                                   "f32_64x64x64_direct_k4", "f32_128x128x32_mfma16_edge",
                                   "f32_48x48x64_direct_rc", "f32_96x96x64_direct_rc",
-                                  "f32_80x80x64_direct_rc", "f32_48x96x64_direct_rc"])
+                                  "f32_80x80x64_direct_rc", "f32_48x96x64_direct_rc",
+                                  "f32_48x48x64_direct_rc_edge", "f32_96x96x64_direct_rc_edge"])
 def test_values_past_the_operands_never_reach_the_output(tile, torch_cuda):
     """Edge tiles read past K, N and M only in ways whose values are zeroed or
     never stored: with NaN and Inf in every padding element of A and B (the

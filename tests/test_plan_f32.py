@@ -50,7 +50,7 @@ PINNED = [
     ((1000, 1000, 1000), True, "f32_64x64x64_direct_k4_edge"),
     ((4000, 256, 4000), True, "f32_128x128x16_direct_edge"),
     ((4097, 256, 4096), True, "f32_64x64x64_mfma16_edge"),
-    ((512, 1000, 512), True, "f32_32x32x64_w1x1_k4_pf4_edge"),
+    ((512, 1000, 512), True, "f32_32x32x64_direct_rc_edge"),
     ((4096, 1024, 4096), True, "f32_128x128x16_direct"),
     ((3072, 512, 3072), True, "f32_64x64x64_direct_k4"),
     ((2001, 2001, 2001), True, "f32_128x128x32_mfma16_anyshape"),  # K % 4 != 0
@@ -75,6 +75,13 @@ PINNED = [
     ((768, 768, 768), True, "f32_48x48x64_direct_rc"),
     ((720, 768, 720), True, "f32_48x48x64_direct_rc"),
     ((768, 784, 768), True, "f32_48x48x64_direct_rc"),      # K a multiple of 16, not of 64
+    # ... and their edge twins
+    ((1500, 1500, 1500), True, "f32_96x96x64_direct_rc_edge"),
+    ((760, 760, 760), True, "f32_48x48x64_direct_rc_edge"),
+    ((500, 500, 500), True, "f32_32x32x64_direct_rc_edge"),
+    ((1200, 1204, 1200), True, "f32_80x80x64_direct_rc_edge"),  # K a multiple of 4 only
+    # two rounds of partial 64x64 tiles against one of 80x80
+    ((1500, 1000, 1000), True, "f32_80x80x64_direct_rc_edge"),
     ((1200, 1024, 1200), True, "f32_80x80x64_direct_rc"),
     ((1536, 512, 1536), True, "f32_96x96x64_direct_rc"),
     ((1536, 1024, 720), True, "f32_96x48x64_direct_rc"),
@@ -99,7 +106,7 @@ def test_table_is_named_and_every_tile_is_planned(driver):
     layer: the table holds no configuration the planner cannot reach."""
     rows = table(driver)
     names = [r[1] for r in rows]
-    assert len(names) == len(set(names)) == 29
+    assert len(names) == len(set(names)) == 34
     dims = [1, 4, 17, 64, 65, 100, 128, 256, 257, 500, 512, 720, 768, 1000, 1024, 1025, 1536, 2000, 2048, 2304,
             3000, 4096, 4097, 6000, 6144]
     queries = [(M, N, K, al, CUS) for M in dims for N in dims for K in dims + [0] for al in (0, 1)]
