@@ -257,6 +257,59 @@ def measure_library_int8(p: Prepared, steps: int, warmup: int) -> float:
     return ev[0].elapsed_time(ev[1]) / steps
 
 
+def measure_shapes(spec: str, steps: int, warmup: int) -> int:
+    """--shapes "M,K,N;M,K,N...": the fused fp32 layer relu(X @ W + b) at each
+    shape through the device entry (automatic plan), and the vendor's
+    torch.mm (no bias or activation) on the same operands, both timed like
+    kernel_ms_mean (launches queued behind a spin kernel). One JSON line per
+    shape. A sample of rows is checked against a float64 torch product first."""
+    import torch
+    from mlir_edsl_hip import _native
+    from mlir_edsl_hip.device import dense_launch
+    shapes = [tuple(int(v) for v in t.split(",")) for t in spec.split(";") if t.strip()]
+    g = torch.Generator(device="cuda").manual_seed(1234)
+
+    def backlogged(fn) -> float:
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        enqueue_s = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int(sleep_cycles_per_s() * (enqueue_s * 1.5 + 2e-4)))
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        for _ in range(steps):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[1]) / steps
+
+    for M, K, N in shapes:
+        X = torch.randn(M, K, device="cuda", generator=g)
+        W = torch.randn(K, N, device="cuda", generator=g) / K ** 0.5
+        b = torch.randn(N, device="cuda", generator=g)
+        Y = torch.empty(M, N, device="cuda")
+        dense_launch(X, W, b, Y, _native.EPI_BIAS_RELU)
+        torch.cuda.synchronize()
+        rows = torch.arange(0, M, max(1, M // 64), device="cuda")
+        ref = torch.relu(X[rows].double() @ W.double() + b.double())
+        err = ((Y[rows].double() - ref).norm() / ref.norm().clamp_min(1e-300)).item()
+        if not err <= 1e-5:
+            raise RuntimeError(f"{M}x{K}x{N}: relative error {err:.2e} against float64")
+        plan = _native.last_plan()
+        ms = backlogged(lambda: dense_launch(X, W, b, Y, _native.EPI_BIAS_RELU))
+        vendor_ms = backlogged(lambda: torch.mm(X, W, out=Y))
+        flops = 2.0 * M * N * K
+        print(json.dumps({"shape": {"M": M, "K": K, "N": N}, "plan": plan, "kernel_ms_mean": round(ms, 5),
+                          "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "vendor_ms": round(vendor_ms, 5),
+                          "vendor_vs_fused": round(vendor_ms / ms, 3), "rel_err_f64": float(f"{err:.2e}")}),
+              flush=True)
+    return 0
+
+
 def step_value(wname: str, step_s: float) -> float:
     """Whole-step throughput in the workload's unit."""
     from mlir_edsl_hip.inputs import WORKLOADS
@@ -620,6 +673,9 @@ def main() -> int:
                          "--steps / --warmup) beside the JSON line that run printed; --summary-workload "
                          "picks the workload (default: the line's headline)")
     ap.add_argument("--summary-workload", default=None, choices=sorted(UNITS))
+    ap.add_argument("--shapes", default=None, metavar="M,K,N;...",
+                    help="only time the fused fp32 layer and the vendor's torch.mm at these shapes, "
+                         "one JSON line each (--steps / --warmup apply)")
     args = ap.parse_args()
     if args.trace_summary:
         return trace_summary(args.trace_summary[0], args.trace_summary[1], args.summary_workload, args.warmup,
@@ -637,6 +693,8 @@ def main() -> int:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
     torch.cuda.set_device(0)
+    if args.shapes:
+        return measure_shapes(args.shapes, args.steps, args.warmup)
     if args.copy_calibration:
         n = args.copy_calibration // 4
         src = torch.ones(n, dtype=torch.float32, device="cuda")
