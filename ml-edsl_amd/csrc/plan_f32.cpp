@@ -270,18 +270,28 @@ int plan_f32_tile(const F32TileQuery& q) {
       // blocks over all of K per round of four tiles per CU. In one round
       // (768^3: 256 tiles of 48x48, 10.5 against 15.3 us; 1536x3072x1536 on
       // 96x96 114.9 against 141.6 us; 720x768x720 10.5 against 19.0 us on the
-      // 32x32 edge tile); over several rounds only tiles that read no more
-      // per output than 64x64 ones, 1/bm + 1/bn <= 1/32 (2560x1024x2560 on
-      // 80x80 113.3 against 124.8 us, 2304^3 on 48x96 204.4 against 211.7
-      // us, where 48x48 tiles take 234.2 us).
+      // 32x32 edge tile); over several rounds tiles of 64 and more that read
+      // no more per output than 64x64 ones (2560x1024x2560 on 80x80 113.3
+      // against 124.8 us; 48x48 tiles over nine rounds took 234.2 us at
+      // 2304^3 against 211.7 us for 64x64).
       if (cfg != kF32Direct128 && cfg != kF32Direct128Edge && K >= 256 && edge_ok && direct_ok) {
         const int64_t t64n = ((M + 63) / 64) * ((N + 63) / 64);
         const int64_t cus = q.cus;
         int64_t inc = -1;  // the incumbent's cost where comparable
         if (cfg == kF32Direct64K4 || cfg == kF32Direct64K4Edge) inc = 16 * ((t64n + cus - 1) / cus);
         if (cfg == kF32Direct64) inc = 64 * ((t64n + 4 * cus - 1) / (4 * cus));
-        int best_rc = -1;
-        int64_t best_cost = 0, best_rounds = 0;
+        // Candidates by cost; a tile that reads more per output than a 64x64
+        // one, or is narrower than 64, over several rounds only where it costs
+        // at most 2/3 of every other candidate (128x4096x4096: 512 tiles of
+        // 32x32 in two rounds, 51.0 us, against one half-full round of 64x64,
+        // 62.9-63.2 us).
+        struct Cand {
+          int c;
+          int64_t cost, rounds;
+          bool light;  // one round, or no more reads per output than 64x64
+        };
+        Cand cands[7];
+        int n_cands = 0;
         for (int c0 : {kF32DirectRC2x2, kF32DirectRC3x3, kF32DirectRC4x4, kF32DirectRC5x5, kF32DirectRC6x6,
                        kF32DirectRC3x6, kF32DirectRC6x3}) {
           const int edge_twin = c0 == kF32DirectRC2x2 ? kF32DirectRC2x2Edge
@@ -289,19 +299,41 @@ int plan_f32_tile(const F32TileQuery& q) {
                                 : c0 == kF32DirectRC4x4 ? kF32DirectRC4x4Edge
                                 : c0 == kF32DirectRC5x5 ? kF32DirectRC5x5Edge
                                 : c0 == kF32DirectRC6x6 ? kF32DirectRC6x6Edge : -1;
-          const int c = fits(c0) ? c0 : edge_twin >= 0 && fits(edge_twin) ? edge_twin : -1;
+          // Edge twins from K = 384 (at 256 the LDS-staged edge tiles were
+          // 1-9 % faster: 96x256x4096 6.0 against 6.6 us; 500^3 5.8 against
+          // 8.6 us).
+          const int c = fits(c0) ? c0 : edge_twin >= 0 && K >= 384 && fits(edge_twin) ? edge_twin : -1;
           if (c < 0) continue;
           const GemmF32Config& g = gemm_f32_config(c);
           const int64_t rounds = (tiles_of(c) + cus - 1) / cus;
-          if (rounds > 1 && 32 * (g.bm + g.bn) > g.bm * g.bn) continue;
           const int64_t cost = (int64_t)(g.bm / 16) * (g.bn / 16) * rounds;
-          if (best_rc < 0 || cost < best_cost || (cost == best_cost && rounds < best_rounds)) {
-            best_rc = c;
-            best_cost = cost;
-            best_rounds = rounds;
+          // Over several rounds only square-ish tiles of 64 and more (48x96
+          // over three rounds: 1536x1024x2304 79.6 against 72.2 us for 64x64).
+          const bool light = rounds == 1 || (g.bm >= 64 && g.bn >= 64 && 32 * (g.bm + g.bn) <= g.bm * g.bn);
+          cands[n_cands++] = {c, cost, rounds, light};
+        }
+        int64_t light_min = -1;
+        for (int i = 0; i < n_cands; ++i)
+          if (cands[i].light && (light_min < 0 || cands[i].cost < light_min)) light_min = cands[i].cost;
+        int best_rc = -1;
+        int64_t best_cost = 0, best_rounds = 0;
+        for (int i = 0; i < n_cands; ++i) {
+          const Cand& k = cands[i];
+          if (!k.light && !(light_min < 0 || 3 * k.cost <= 2 * light_min)) continue;
+          if (best_rc < 0 || k.cost < best_cost || (k.cost == best_cost && k.rounds < best_rounds)) {
+            best_rc = k.c;
+            best_cost = k.cost;
+            best_rounds = k.rounds;
           }
         }
-        if (best_rc >= 0 && (inc < 0 ? best_rounds == 1 && 2 * tiles_of(best_rc) >= cus : best_cost < inc))
+        // With no comparable incumbent: one round at least half full, or
+        // several rounds at 2/3 of the cost of such a round at most.
+        bool take = best_rc >= 0 && (inc >= 0 ? best_cost < inc : best_rounds == 1 && 2 * tiles_of(best_rc) >= cus);
+        if (best_rc >= 0 && inc < 0 && best_rounds > 1)
+          for (int i = 0; i < n_cands; ++i)
+            if (cands[i].rounds == 1 && 2 * tiles_of(cands[i].c) >= cus && 3 * best_cost <= 2 * cands[i].cost)
+              take = true;
+        if (take)
           cfg = best_rc;
         else if (cfg == kF32Direct64K4 && t64n <= cus && fits(kF32DirectRC4x4))
           // One round of K-split 64x64 tiles: the R x C kernel's 4 x 4 instance

@@ -86,11 +86,15 @@ PINNED = [
     ((1536, 512, 1536), True, "f32_96x96x64_direct_rc"),
     ((1536, 1024, 720), True, "f32_96x48x64_direct_rc"),
     ((720, 1024, 1536), True, "f32_48x96x64_direct_rc"),
-    # ... or several, with tiles that read no more per output than 64x64
-    ((2304, 2304, 2304), True, "f32_48x96x64_direct_rc"),
+    # ... or several, with tiles of 64 and more that read no more per output than 64x64
+    ((2304, 2304, 2304), True, "f32_64x64x64_direct_k4"),    # 48x96 over 4.5 rounds: not taken
     ((2560, 1024, 2560), True, "f32_80x80x64_direct_rc"),
     # too few tiles for half the CUs, and even cost against 64x64
     ((256, 1024, 256), True, "f32_32x32x64_w1x1_k4_pf4"),
+    # two rounds of 32x32 at half the cost of a half-full round of 64x64
+    ((128, 4096, 4096), True, "f32_32x32x64_direct_rc"),
+    # edge twins need K >= 384
+    ((96, 256, 4096), True, "f32_32x32x64_w1x1_k4_pf4"),
     ((3072, 3072, 3072), True, "f32_64x64x64_direct_k4"),
 ]
 
