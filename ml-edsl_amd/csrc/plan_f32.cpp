@@ -58,7 +58,7 @@ namespace {
 //      layers whose 64x64 tiles leave a round of workgroups partly empty
 //      (768^3: 144 tiles of 64x64 or 256 of 48x48, 15.3 against 10.5 us),
 //      the 4x4 instance (64x64) for one round of 64x64 K-split tiles, and
-//      edge twins of the square ones (1500^3 on 96x96: 84.6 against 62.7 us).
+//      edge twins of the square ones (1500^3 on 96x96: 62.7 against 84.6 us).
 const GemmF32Config kConfigs[] = {
     {64, 64, 16, 2, 2, kGuardAll, "f32_64x64x16_w2x2_guard"},
     {32, 32, 64, 1, 1, kGuardNone, "f32_32x32x64_w1x1_k4_pf4"},
