@@ -525,11 +525,13 @@ hipError_t launch_direct16(int epi, const GemmF32Args& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// The R x C tile (16R x 16C outputs, K -- a multiple of 16, at least 64 --
-// split over the four waves of a workgroup) for layers whose 64x64 tiles do
-// not fill whole rounds of the CUs: 768^3 is 256 tiles of 48x48 (R = C = 3) and 1536^3 256 tiles of 96x96
+// The R x C tile (16R x 16C outputs, K split over the four waves of a
+// workgroup) for layers whose 64x64 tiles do not fill whole rounds of the
+// CUs: 768^3 is 256 tiles of 48x48 (R = C = 3) and 1536^3 256 tiles of 96x96
 // (R = C = 6), one workgroup per CU and one wave per SIMD, so every SIMD runs
-// the same number of MFMAs in one round. Each wave computes the whole tile
+// the same number of MFMAs in one round. Exact tiles take K a multiple of 16
+// (at least 64); the edge twins (kEdge) take partial tiles and any K that is
+// a multiple of 4, with the 128x128 edge twin's range-checked loads. Each wave computes the whole tile
 // over a quarter of K with the 64x64 tile's A fragments and its loop (loads
 // two 16-deep groups ahead in three register sets). B columns come in pieces
 // of 64, 32 or 16 columns, read with 16-, 8- or 4-byte loads per lane and k
