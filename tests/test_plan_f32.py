@@ -95,6 +95,12 @@ PINNED = [
     ((128, 4096, 4096), True, "f32_32x32x64_direct_rc"),
     # edge twins need K >= 384
     ((96, 256, 4096), True, "f32_32x32x64_w1x1_k4_pf4"),
+    ((96, 4096, 4096), True, "f32_48x48x64_direct_rc_edge"),
+    ((500, 512, 2304), True, "f32_80x80x64_direct_rc_edge"),
+    # 48x96 over three rounds lost to 64x64 (79.6 against 72.2 us)
+    ((1536, 1024, 2304), True, "f32_64x64x64_direct_k4"),
+    # a round three quarters full of 64x64 beats three rounds of 32x32
+    ((192, 4096, 4096), True, "f32_64x64x64_direct_rc"),
     ((3072, 3072, 3072), True, "f32_64x64x64_direct_k4"),
 ]
 
